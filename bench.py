@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Benchmark of the GGUF quantized matrix-vector hot path on one MI355X.
+
+Default workload: Q4_K matvec 4096 -> 14336 at batch 1 with fp16 activations,
+the configuration the headline metric is quoted on. A step is one matvec
+launch over one batch of synthetic input; the weights rotate over enough
+distinct device copies (>= 2x the 256 MB Infinity Cache) that every step reads
+its weights from HBM.
+
+Two timed passes over the same K steps:
+  * whole job: the K launches captured in one HIP graph, timed with events
+    around the graph launch -> ms_per_step and `value` (GB/s of algorithmic
+    bytes, inputs resident in HBM);
+  * kernel: each launch's dispatch records its own start/stop events
+    (rqmv_matvec_timed) -> the average kernel duration behind
+    roofline.achieved, comparable with a rocprofv3 kernel trace.
+The CPU baseline times the oracle's restatement of recipe's CPU path (fp32,
+exact per-weight decode, sequential fma per block, all rows split over
+threads) on a bounded sample of the same workload.
+
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "recipe-dev_amd")]
+
+import numpy as np  # noqa: E402
+
+METRIC = "Q4_K matvec effective HBM GB/s (% of peak) at batch 1; decode tok/s"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 * 2 ** 20
+
+WORKLOADS = {
+    "q4_k_up": ("q4_k", 14336, 4096, "f16", "Q4_K matvec 4096->14336 batch 1 (FFN up/gate)"),
+    "q4_k_down": ("q4_k", 4096, 14336, "f16", "Q4_K matvec 14336->4096 batch 1 (FFN down)"),
+    "q4_0_up": ("q4_0", 14336, 4096, "f16", "Q4_0 matvec 4096->14336 batch 1"),
+    "q4_0_down": ("q4_0", 4096, 14336, "f16", "Q4_0 matvec 14336->4096 batch 1"),
+    "q8_0_4096": ("q8_0", 4096, 4096, "f32", "Q8_0 matvec 4096x4096, fp32 activations"),
+    "q6_k_25600": ("q6_k", 25600, 5120, "f16", "Q6_K matvec 5120->25600, M activation rows"),
+    "q8_0_5120": ("q8_0", 5120, 5120, "f16", "Q8_0 matvec 5120->5120, M activation rows"),
+}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def traffic_from_profiles(workload, m):
+    """HBM bytes per launch measured by rocprofv3 counters, if recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        return json.load(open(path)).get(f"{workload}_m{m}")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(fmt, rows, cols, x32, seconds, weights_bytes, alg_bytes):
+    import oracle
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    # the same matvec, repeated over the full weight for ~`seconds`
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matvec_recipe_f32(fmt, weights_bytes, rows, cols, x32, threads=cores)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / runs
+    return {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{runs} full {fmt} {cols}->{rows} matvecs (M={x32.shape[0]}) in {el:.1f} s, "
+                      f"{per * 1e3:.2f} ms each, fp32 recipe-order restatement, {cores} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="q4_k_up", choices=sorted(WORKLOADS))
+    ap.add_argument("--m", type=int, default=1, help="activation rows")
+    ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 2x MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs the matvec on a "
+              f"single MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import rqmv
+    from rqmv import synth
+
+    fmt, rows, cols, xdt, desc = WORKLOADS[args.workload]
+    m = args.m
+    log(f"bench: {args.workload} ({desc}) M={m} steps={args.steps} warmup={args.warmup}")
+    rqmv.init(0)
+    w = synth.weights(fmt, rows, cols)
+    if xdt == "f16":
+        xh = synth.activations_f16(m * cols).reshape(m, cols)
+        x32 = synth.fp16_to_f32(xh)
+        dtype_code, xbytes = rqmv.DTYPE_F16, 2
+    else:
+        xh = synth.activations_f32(m * cols).reshape(m, cols)
+        x32 = xh
+        dtype_code, xbytes = rqmv.DTYPE_F32, 4
+    weight_bytes = w.nbytes
+    alg_bytes = weight_bytes + m * cols * xbytes + m * rows * 4
+    flops = 2.0 * m * rows * cols
+    copies = args.copies or max(2, -(-2 * MALL_BYTES // weight_bytes) + 1)
+    log(f"bench: {copies} weight copies of {weight_bytes / 1e6:.1f} MB")
+    Ws = [rqmv.Weight(fmt, rows, cols, w) for _ in range(copies)]
+    xb = rqmv.DeviceBuffer.from_array(xh)
+    yb = rqmv.DeviceBuffer(4 * m * rows)
+    stream = rqmv.Stream()
+
+    rel = None
+    if not args.no_check:
+        import oracle
+
+        Ws[0].matvec(xb, dtype_code, m, cols, yb, rows, stream)
+        stream.synchronize()
+        y = yb.download(np.float32).reshape(m, rows)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=8)
+        rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+        log(f"bench: parity rel-L2 {rel:.3e}")
+        if not rel <= 1e-3:
+            log("bench: parity check failed")
+            sys.exit(1)
+
+    def enqueue_steps(count, start=0):
+        for i in range(count):
+            Ws[(start + i) % copies].matvec(xb, dtype_code, m, cols, yb, rows, stream)
+
+    # whole job: K launches in one graph
+    graph = rqmv.Graph(stream, lambda: enqueue_steps(args.steps))
+    for _ in range(max(1, args.warmup // max(1, args.steps) + 1)):
+        graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = rqmv.Event(), rqmv.Event()
+    e0.record(stream)
+    graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    total_ms = e0.elapsed_ms(e1)
+    ms_per_step = total_ms / args.steps
+    log(f"bench: graph {args.steps} steps {total_ms:.3f} ms -> {ms_per_step * 1e3:.2f} us/step")
+
+    # kernel durations: each dispatch records its own start/stop events
+    enqueue_steps(args.warmup)
+    stream.synchronize()
+    starts = [rqmv.Event() for _ in range(args.steps)]
+    stops = [rqmv.Event() for _ in range(args.steps)]
+    for i in range(args.steps):
+        Ws[i % copies].matvec_timed(xb, dtype_code, m, cols, yb, rows, stream, starts[i], stops[i])
+    stream.synchronize()
+    ker = np.array([starts[i].elapsed_ms(stops[i]) for i in range(args.steps)])
+    ker_ms = float(ker.mean())
+    log(f"bench: kernel mean {ker_ms * 1e3:.2f} us, median {np.median(ker) * 1e3:.2f} us, "
+        f"p10 {np.percentile(ker, 10) * 1e3:.2f} p90 {np.percentile(ker, 90) * 1e3:.2f}")
+
+    achieved = alg_bytes / (ker_ms * 1e-3) / 1e9
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if xdt == "f16" else "f32",
+        "data": "synthetic",
+        "config": {"workload": desc, "format": fmt.upper(), "rows": rows, "cols": cols, "m": m,
+                   "activations": xdt, "accumulate": "f32", "weight_copies": copies,
+                   "bytes_per_step": alg_bytes, "flops_per_step": flops, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.workload, m)},
+        "kernel_us": round(ker_ms * 1e3, 3),
+        "gflops": round(flops / (ker_ms * 1e-3) / 1e9, 1),
+        "parity_rel_l2": rel,
+    }
+    if not args.no_cpu:
+        log("bench: cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(fmt, rows, cols, x32, args.cpu_seconds, w, alg_bytes)
+    print(json.dumps(out), flush=True)
+    graph.close()
+
+
+if __name__ == "__main__":
+    main()

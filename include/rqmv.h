@@ -1,0 +1,154 @@
+/*
+ * rqmv: MI355X (gfx950) GGUF quantized matrix-vector library, C ABI.
+ *
+ * The drop-in boundary for recipe's packed-sum hot path. recipe binds GGUF
+ * tensors to projections by name and lowers each to a Contraction (or
+ * ExpertIn/ExpertOut/TopK) node whose packed StoredWeight its device code reads
+ * (recipe.rs:4532-4832); this library takes over those nodes' storage and
+ * arithmetic for batch 1 and small M. A Rust FFI binding of these entry points
+ * is shown in INTEGRATION.md.
+ *
+ * Conventions
+ *   - Every entry point returns 0 on success and a negative RQMV_E* code on
+ *     failure; rqmv_last_error() then names the failure (thread-local). No entry
+ *     point aborts the process.
+ *   - Weights are owned by the library (device memory, freed by
+ *     rqmv_weight_destroy). Activations and outputs are caller-owned device
+ *     buffers.
+ *   - Work is ordered on the caller's HIP stream (`stream` is a hipStream_t;
+ *     NULL = the default stream) and never synchronises the host, except
+ *     rqmv_weight_create/unpack, which copy host bytes.
+ *   - A weight handle is immutable after creation and may be shared by
+ *     threads; launches on one stream are ordered by that stream.
+ *   - Activations x are M rows of K values, row m at x + m*ldx elements
+ *     (recipe stores positions contiguously per channel, x[k*length + p],
+ *     amd-nv-cpu.ll:1161-1165; pass the transpose). Outputs y are fp32, row m
+ *     of N values at y + m*ldy.
+ */
+#ifndef RQMV_H
+#define RQMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids, as recipe's GGUF loader maps them (recipe.rs:9925-9961). */
+typedef enum {
+    RQMV_F16 = 1,
+    RQMV_Q4_0 = 2,
+    RQMV_Q8_0 = 8,
+    RQMV_Q4_K = 12,
+    RQMV_Q6_K = 14
+} rqmv_format;
+
+/* Element type of activations. */
+typedef enum { RQMV_DTYPE_F32 = 0, RQMV_DTYPE_F16 = 1 } rqmv_dtype;
+
+/* Routing score function (recipe's Scoring: softmax = 0, sigmoid = 1). */
+typedef enum { RQMV_SCORE_SOFTMAX = 0, RQMV_SCORE_SIGMOID = 1 } rqmv_scoring;
+
+enum {
+    RQMV_OK = 0,
+    RQMV_EINVAL = -1,   /* bad argument, shape or format */
+    RQMV_EDEVICE = -2,  /* HIP runtime error */
+    RQMV_ENOMEM = -3,   /* device allocation failed */
+    RQMV_ESTATE = -4    /* library not initialised for this device */
+};
+
+typedef struct rqmv_weight rqmv_weight;
+
+/* Selects and initialises a device; call once per thread that uses it.
+ * Replaces the device/queue set-up of recipe's HSA runtime
+ * (recipe.rs:28007-28612, Gpu::open). */
+int rqmv_init(int device);
+
+/* The last failure on the calling thread, or "" (recipe.rs:13416-13433). */
+const char* rqmv_last_error(void);
+
+/* Uploads rows x cols weights given as GGUF block bytes (row-major: row r is
+ * cols/block consecutive blocks, recipe.rs:9875-9889), repacked into the
+ * kernels' layout. Replaces StoredWeight + Buffer::fill_weights with
+ * row_interleave (recipe.rs:15859-16069, 26980-27010, 3162-3212). */
+int rqmv_weight_create(int format, int64_t rows, int64_t cols, const void* gguf_bytes, size_t nbytes,
+                       rqmv_weight** out);
+
+/* An expert bank: `experts` consecutive rows x cols matrices, as GGUF stores
+ * ffn_{gate,up,down}_exps shaped [cols, rows, experts] (recipe.rs:9861-9868,
+ * 18286-18292). */
+int rqmv_expert_bank_create(int format, int64_t experts, int64_t rows, int64_t cols, const void* gguf_bytes,
+                            size_t nbytes, rqmv_weight** out);
+
+int rqmv_weight_destroy(rqmv_weight* weight);
+
+/* Shape, format and device footprint of a weight (experts = 1 for a plain one). */
+int rqmv_weight_info(const rqmv_weight* weight, int* format, int64_t* rows, int64_t* cols, int64_t* experts,
+                     size_t* device_bytes);
+
+/* Copies the weight back to host memory as GGUF block bytes (the inverse of
+ * the repack; nbytes must equal the GGUF size). Synchronises the device. */
+int rqmv_weight_unpack(const rqmv_weight* weight, void* gguf_bytes, size_t nbytes);
+
+/* Writes every weight as fp32, rows x cols (x experts) in GGUF order, each
+ * equal to recipe's reference dequantization rounded to fp32
+ * (HostQuantOps, recipe.rs:3687-3833, 3973-4057). */
+int rqmv_weight_dequantize(const rqmv_weight* weight, float* out_dev, void* stream);
+
+/* y = W x for M activation rows (Gguf::contract, recipe.rs:17130; a packed
+ * Contraction node, recipe.rs:4532-4604 / amd-nv-cpu.ll:2674-3126). */
+int rqmv_matvec(const rqmv_weight* weight, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev,
+                int64_t ldy, void* stream);
+
+/* rqmv_matvec with two HIP events (hipEvent_t, either may be NULL) that the
+ * kernel dispatch itself records at its start and at its completion, for
+ * measuring kernel time without host launch overhead. No counterpart in the
+ * reference; for benchmarks and profilers. */
+int rqmv_matvec_timed(const rqmv_weight* weight, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev,
+                      int64_t ldy, void* stream, void* start_event, void* stop_event);
+
+/* y = W_e x with expert `expert` of a bank (Gguf::expert, recipe.rs:17135). */
+int rqmv_expert_matvec(const rqmv_weight* bank, int64_t expert, const void* x_dev, int x_dtype, int m, int64_t ldx,
+                       float* y_dev, int64_t ldy, void* stream);
+
+/* The gguf_moe block (recipe.rs:14722, lowered at 23415-23459): router,
+ * top-k routing, routed SiLU-GLU experts and an optional gated shared expert. */
+typedef struct {
+    const rqmv_weight* router;      /* F16, experts x d_model (ffn_gate_inp) */
+    const rqmv_weight* gate_exps;   /* bank: experts x hidden x d_model (ffn_gate_exps) */
+    const rqmv_weight* up_exps;     /* bank: experts x hidden x d_model (ffn_up_exps) */
+    const rqmv_weight* down_exps;   /* bank: experts x d_model x hidden (ffn_down_exps) */
+    const rqmv_weight* shared_gate_inp; /* F16, 1 x d_model (ffn_gate_inp_shexp) or NULL */
+    const rqmv_weight* gate_shexp;  /* hidden_shared x d_model, or NULL for no shared expert */
+    const rqmv_weight* up_shexp;
+    const rqmv_weight* down_shexp;  /* d_model x hidden_shared */
+    int top_k;
+    int scoring;        /* rqmv_scoring */
+    int renormalize;    /* divide the kept weights by their total */
+    float scale;        /* routed weight scale (1 = none) */
+} rqmv_moe_params;
+
+/* Device workspace bytes rqmv_moe needs for one position. */
+int rqmv_moe_workspace_size(const rqmv_moe_params* params, size_t* bytes);
+
+/* One position: x (d_model, f16 or f32) -> y (d_model, fp32). The routing
+ * weights (experts floats, zero off the top-k) are written to route_dev when
+ * it is not NULL. `workspace` is a device buffer of rqmv_moe_workspace_size
+ * bytes that the call may overwrite. */
+int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,
+             void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only loader functions (no device needed): the repacked layout's size
+ * and the repack / unpack themselves, for inspection and testing. */
+int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* code_bytes, size_t* meta0_bytes,
+                      size_t* meta1_bytes);
+int rqmv_repack_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, void* code, void* meta0,
+                     void* meta1);
+int rqmv_unpack_host(int format, int64_t rows, int64_t cols, const void* code, const void* meta0, const void* meta1,
+                     void* gguf_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

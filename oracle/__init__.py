@@ -1,0 +1,146 @@
+"""ctypes binding of the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU restatement of
+recipe's CPU path. The product (librqmv and the rqmv package) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_double, c_float, c_int, c_int64, c_uint16, c_uint32, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+FORMATS = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_k": Q4_K, "q6_k": Q6_K}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle not built: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.orc_fp16_from_f32.argtypes = [c_float]
+        L.orc_fp16_from_f32.restype = c_uint16
+        L.orc_f32_from_fp16.argtypes = [c_uint16]
+        L.orc_f32_from_fp16.restype = c_float
+        L.orc_fp16_from_f32_n.argtypes = [c_void_p, c_void_p, ctypes.c_size_t]
+        L.orc_dequant_value.argtypes = [c_int, c_void_p, c_int]
+        L.orc_dequant_value.restype = c_double
+        L.orc_dequant_rows.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p]
+        L.orc_matvec_f64.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int64, c_void_p, c_int64]
+        L.orc_matvec_recipe_f32.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int64, c_void_p,
+                                            c_int64, c_int]
+        L.orc_topk.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_void_p]
+        L.orc_moe_f64.argtypes = [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_double, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_void_p]
+        L.orc_q4k_q81_reference.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
+        L.orc_q4k_xorshift_rows.argtypes = [c_uint32, c_int64, c_uint16, c_void_p]
+        _lib = L
+    return _lib
+
+
+def _fmt(fmt):
+    return FORMATS[fmt] if isinstance(fmt, str) else int(fmt)
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data if a is not None else None
+
+
+def fp16_from_f32(values) -> np.ndarray:
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    out = np.empty(v.size, np.uint16)
+    lib().orc_fp16_from_f32_n(v.ctypes.data, out.ctypes.data, v.size)
+    return out
+
+
+def f32_from_fp16(bits) -> np.ndarray:
+    b = np.asarray(bits, dtype=np.uint16).reshape(-1)
+    return np.array([lib().orc_f32_from_fp16(int(v)) for v in b], dtype=np.float32)
+
+
+def dequant_rows(fmt, gguf: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    out = np.empty(rows * cols, np.float32)
+    rc = lib().orc_dequant_rows(_fmt(fmt), g.ctypes.data, rows, cols, out.ctypes.data)
+    assert rc == 0, rc
+    return out.reshape(rows, cols)
+
+
+def dequant_value(fmt, block: np.ndarray, index: int) -> float:
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    return lib().orc_dequant_value(_fmt(fmt), b.ctypes.data, index)
+
+
+def matvec_f64(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """x (M, K) float64 -> y (M, N) float64."""
+    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float64)
+    m = x2.shape[0]
+    y = np.empty((m, rows), np.float64)
+    rc = lib().orc_matvec_f64(_fmt(fmt), g.ctypes.data, rows, cols, x2.ctypes.data, m, cols, y.ctypes.data, rows)
+    assert rc == 0, rc
+    return y
+
+
+def matvec_recipe_f32(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """recipe's fp32 float packed path: x (M, K) float32 -> y (M, N) float32."""
+    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    m = x2.shape[0]
+    y = np.empty((m, rows), np.float32)
+    rc = lib().orc_matvec_recipe_f32(_fmt(fmt), g.ctypes.data, rows, cols, x2.ctypes.data, m, cols, y.ctypes.data,
+                                     rows, threads)
+    assert rc == 0, rc
+    return y
+
+
+def topk(scores: np.ndarray, top: int, scoring: int = 0, renormalize: bool = True) -> np.ndarray:
+    s = np.ascontiguousarray(scores, dtype=np.float64)
+    w = np.empty_like(s)
+    rc = lib().orc_topk(s.ctypes.data, s.size, top, scoring, 1 if renormalize else 0, w.ctypes.data)
+    assert rc == 0, rc
+    return w
+
+
+def moe_f64(fmt, d_model, experts, top, hidden, router_bits, gate, up, down, x, scoring=0, renormalize=True,
+            scale=1.0, hidden_shared=0, shared_gate_bits=None, gate_sh=None, up_sh=None, down_sh=None):
+    """Returns (y float64 (d_model,), routing weights float64 (experts,))."""
+    r = np.ascontiguousarray(router_bits, dtype=np.uint16)
+    xs = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty(d_model, np.float64)
+    rw = np.empty(experts, np.float64)
+    conv = lambda a, t: None if a is None else np.ascontiguousarray(a, dtype=t)  # noqa: E731
+    sg, gs, us, ds = conv(shared_gate_bits, np.uint16), conv(gate_sh, np.uint8), conv(up_sh, np.uint8), conv(down_sh, np.uint8)
+    g, u, d = conv(gate, np.uint8), conv(up, np.uint8), conv(down, np.uint8)
+    rc = lib().orc_moe_f64(_fmt(fmt), d_model, experts, top, hidden, scoring, 1 if renormalize else 0, scale,
+                           r.ctypes.data, g.ctypes.data, u.ctypes.data, d.ctypes.data, hidden_shared, _ptr(sg),
+                           _ptr(gs), _ptr(us), _ptr(ds), xs.ctypes.data, y.ctypes.data, rw.ctypes.data)
+    assert rc == 0, rc
+    return y, rw
+
+
+def q4k_q81_reference(w: np.ndarray, rows: int, cols: int, x: np.ndarray):
+    """evidence bench.rs algebra: returns (y float32 (rows,), x as used float64 (cols,))."""
+    g = np.ascontiguousarray(w, dtype=np.uint8)
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, np.float32)
+    xu = np.empty(cols, np.float64)
+    rc = lib().orc_q4k_q81_reference(g.ctypes.data, rows, cols, xs.ctypes.data, y.ctypes.data, xu.ctypes.data)
+    assert rc == 0, rc
+    return y, xu
+
+
+def q4k_xorshift_rows(seed: int, rows: int, scale_bits: int) -> np.ndarray:
+    out = np.empty(rows * 16 * 144, np.uint8)
+    lib().orc_q4k_xorshift_rows(seed, rows, scale_bits, out.ctypes.data)
+    return out

@@ -1,0 +1,478 @@
+/*
+ * CPU oracle for the GGUF quantized matrix-vector path: TEST INFRASTRUCTURE.
+ * Used only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
+ * as the checker or as the timed restatement of recipe's CPU path. Never part
+ * of the product path. The declarations in oracle.h list what pins each function.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* recipe.rs:15098-15113 `fp16`: round half to even on normal values; values
+ * that become subnormal are first truncated to the subnormal grid scaled by
+ * 2^13 and then rounded; finite values at or beyond 2^16 map to inf when their
+ * mantissa is zero and to a NaN (0x7c01) otherwise, exactly as written there. */
+uint16_t orc_fp16_from_f32(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, 4);
+    uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    int32_t exponent = (int32_t)((bits >> 23) & 0xffu) - 112;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent <= 0) {
+        if (exponent < -10) return sign;
+        uint32_t v = (mantissa | 0x800000u) >> (1 - exponent);
+        return (uint16_t)(sign | ((v + 0xfffu + ((v >> 13) & 1u)) >> 13));
+    }
+    if (exponent >= 31) return (uint16_t)(sign | 0x7c00u | (mantissa != 0 ? 1u : 0u));
+    uint32_t rounded = mantissa + 0xfffu + ((mantissa >> 13) & 1u);
+    if (rounded & 0x800000u) {
+        int32_t e = exponent + 1 < 31 ? exponent + 1 : 31;
+        return (uint16_t)(sign | ((uint32_t)e << 10));
+    }
+    return (uint16_t)(sign | ((uint32_t)exponent << 10) | (rounded >> 13));
+}
+
+/* recipe.rs:15114-15126 `unfp16`. */
+float orc_f32_from_fp16(uint16_t value) {
+    uint32_t sign = ((uint32_t)value & 0x8000u) << 16;
+    uint32_t exponent = (value >> 10) & 31u;
+    uint32_t mantissa = value & 1023u;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign;
+        } else {
+            uint32_t shift = (uint32_t)__builtin_clz(mantissa) - 21u;
+            bits = sign | ((113u - shift) << 23) | ((mantissa << (shift + 13u)) & 0x7fffffu);
+        }
+    } else if (exponent == 31) {
+        bits = sign | 0x7f800000u | (mantissa << 13);
+    } else {
+        bits = sign | ((exponent + 112u) << 23) | (mantissa << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+void orc_fp16_from_f32_n(const float* in, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_fp16_from_f32(in[i]);
+}
+
+/* recipe.rs:15811-15826 (the quantizations! table rows for these formats). */
+int orc_block_values(int format) {
+    switch (format) {
+        case ORC_F32: case ORC_F16: return 1;
+        case ORC_Q4_0: case ORC_Q8_0: return 32;
+        case ORC_Q4_K: case ORC_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+int orc_block_bytes(int format) {
+    switch (format) {
+        case ORC_F32: return 4;
+        case ORC_F16: return 2;
+        case ORC_Q4_0: return 18;
+        case ORC_Q8_0: return 34;
+        case ORC_Q4_K: return 144;
+        case ORC_Q6_K: return 210;
+        default: return 0;
+    }
+}
+
+/* HostQuantOps::half (recipe.rs:4006-4008 via `half`, recipe.rs:15130). */
+static double half_at(const uint8_t* b, int offset) {
+    return (double)orc_f32_from_fp16((uint16_t)(b[offset] | (b[offset + 1] << 8)));
+}
+
+/* dequant_scalar, Q8_0 (recipe.rs:3782-3833, man 8, variant 0, header 2):
+ * the code is the sign-extended byte 2 + i, times the fp16 scale at 0. */
+static double dequant_q8_0(const uint8_t* b, int i) {
+    int64_t code = (int8_t)b[2 + i];
+    return (double)code * half_at(b, 0);
+}
+
+/* dequant_scalar, Q4_0 (man 4, sign 1, variant 0): nibble (i / 16) of byte
+ * 2 + i % 16, less 1 << (man - sign) = 8, times the scale at 0. */
+static double dequant_q4_0(const uint8_t* b, int i) {
+    uint64_t byte = b[2 + (i % 16)];
+    uint64_t code = (byte >> (4 * (i / 16))) & 15u;
+    int64_t signed_code = (int64_t)(code - 8u);
+    return (double)signed_code * half_at(b, 0);
+}
+
+/* dequant_q45k with man = 4 (recipe.rs:3687-3741): nibble (sub % 2) of byte
+ * 16 + 32 * (sub / 2) + i % 32; 6-bit scale and minimum of sub-block `sub`
+ * by the k_scale packing (recipe.rs:15204-15210); w = d*sc*q - dmin*m. */
+static double dequant_q4_k(const uint8_t* b, int i) {
+    uint64_t sub = (uint64_t)i / 32, within = (uint64_t)i % 32;
+    uint64_t packed = b[16 + (sub / 2) * 32 + within];
+    uint64_t code = (packed >> ((sub % 2) * 4)) & 15u;
+    uint64_t low_scale = b[sub + 4] & 63u;
+    uint64_t low_minimum = b[sub + 8] & 63u;
+    uint64_t high_packed = b[sub + 8];
+    uint64_t high_scale = (high_packed & 15u) | ((uint64_t)(b[sub] >> 6) << 4);
+    uint64_t high_minimum = (high_packed >> 4) | ((uint64_t)(b[sub + 4] >> 6) << 4);
+    uint64_t scale_code = sub < 4 ? low_scale : high_scale;
+    uint64_t minimum_code = sub < 4 ? low_minimum : high_minimum;
+    double step = half_at(b, 0) * (double)scale_code;
+    double base = half_at(b, 2) * (double)minimum_code;
+    double product = step * (double)code;
+    return product - base;
+}
+
+/* dequant_q6k (recipe.rs:3743-3780). */
+static double dequant_q6_k(const uint8_t* b, int i) {
+    uint64_t chunk = (uint64_t)i / 128, local = (uint64_t)i % 128;
+    uint64_t group = local / 32, within = local % 32;
+    uint64_t low = b[chunk * 64 + within + 32 * (group & 1u)];
+    uint64_t high = b[chunk * 32 + within + 128];
+    uint64_t low_bits = (low >> (4 * (group / 2))) & 15u;
+    uint64_t high_bits = ((high >> (2 * group)) & 3u) << 4;
+    int64_t code = (int64_t)((low_bits | high_bits) - 32u);
+    int64_t factor = (int8_t)b[192 + chunk * 8 + group * 2 + within / 16];
+    double scaled = half_at(b, 208) * (double)factor;
+    return scaled * (double)code;
+}
+
+double orc_dequant_value(int format, const uint8_t* block, int index) {
+    switch (format) {
+        case ORC_F32: {
+            float f;
+            memcpy(&f, block, 4);
+            return (double)f;
+        }
+        case ORC_F16: return half_at(block, 0);
+        case ORC_Q4_0: return dequant_q4_0(block, index);
+        case ORC_Q8_0: return dequant_q8_0(block, index);
+        case ORC_Q4_K: return dequant_q4_k(block, index);
+        case ORC_Q6_K: return dequant_q6_k(block, index);
+        default: return NAN;
+    }
+}
+
+static int shape_ok(int format, int64_t rows, int64_t cols) {
+    int bv = orc_block_values(format);
+    return bv > 0 && rows >= 0 && cols > 0 && cols % bv == 0;
+}
+
+/* decode_blocks with HostQuantOps (recipe.rs:16141-16157, 3973-4057). */
+int orc_dequant_rows(int format, const uint8_t* bytes, int64_t rows, int64_t cols, float* out) {
+    if (!shape_ok(format, rows, cols)) return -1;
+    const int bv = orc_block_values(format), bb = orc_block_bytes(format);
+    const int64_t blocks = rows * (cols / bv);
+    for (int64_t blk = 0; blk < blocks; ++blk) {
+        const uint8_t* b = bytes + blk * bb;
+        for (int i = 0; i < bv; ++i) out[blk * bv + i] = (float)orc_dequant_value(format, b, i);
+    }
+    return 0;
+}
+
+int orc_matvec_f64(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const double* x, int m_count,
+                   int64_t ldx, double* y, int64_t ldy) {
+    if (!shape_ok(format, rows, cols) || m_count <= 0) return -1;
+    const int bv = orc_block_values(format), bb = orc_block_bytes(format);
+    const int64_t nb = cols / bv;
+    double* w = (double*)malloc(sizeof(double) * (size_t)cols);
+    if (!w) return -2;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t blk = 0; blk < nb; ++blk)
+            for (int i = 0; i < bv; ++i)
+                w[blk * bv + i] = orc_dequant_value(format, bytes + (r * nb + blk) * bb, i);
+        for (int m = 0; m < m_count; ++m) {
+            double s = 0.0;
+            const double* xm = x + (int64_t)m * ldx;
+            for (int64_t k = 0; k < cols; ++k) s += w[k] * xm[k];
+            y[(int64_t)m * ldy + r] = s;
+        }
+    }
+    free(w);
+    return 0;
+}
+
+/* recipe.rs:3216-3218 `dot_run`: a run is a whole block of 32 or more values,
+ * or 32 values of smaller blocks. */
+static int dot_run(int format) {
+    int bv = orc_block_values(format);
+    return bv >= 32 ? bv : 32;
+}
+
+typedef struct {
+    int format;
+    const uint8_t* bytes;
+    int64_t cols, row_begin, row_end;
+    const float* x;
+    int m_count;
+    int64_t ldx, ldy;
+    float* y;
+} recipe_job;
+
+/* emit_run_decoder (recipe.rs:7880-7903): per run, `sum = fma(weight, input,
+ * sum)` for j = 0..run from zero; packed_lanes_body (amd-nv-cpu.ll:3053-3088):
+ * run parts added in order into the row sum, stored in fp32. The weight is the
+ * state-type decode, which equals (float) of the f64 decode for these formats. */
+static void* recipe_rows(void* arg) {
+    const recipe_job* job = (const recipe_job*)arg;
+    const int format = job->format;
+    const int bv = orc_block_values(format), bb = orc_block_bytes(format);
+    const int run = dot_run(format);
+    const int64_t nb = job->cols / bv;
+    float* w = (float*)malloc(sizeof(float) * (size_t)run);
+    float* total = (float*)malloc(sizeof(float) * (size_t)job->m_count);
+    for (int64_t r = job->row_begin; r < job->row_end; ++r) {
+        for (int m = 0; m < job->m_count; ++m) total[m] = 0.0f;
+        for (int64_t k0 = 0; k0 < job->cols; k0 += run) {
+            for (int j = 0; j < run; ++j) {
+                int64_t k = k0 + j;
+                const uint8_t* b = job->bytes + (r * nb + k / bv) * bb;
+                w[j] = (float)orc_dequant_value(format, b, (int)(k % bv));
+            }
+            for (int m = 0; m < job->m_count; ++m) {
+                const float* xm = job->x + (int64_t)m * job->ldx + k0;
+                float part = 0.0f;
+                for (int j = 0; j < run; ++j) part = fmaf(w[j], xm[j], part);
+                total[m] = total[m] + part;
+            }
+        }
+        for (int m = 0; m < job->m_count; ++m) job->y[(int64_t)m * job->ldy + r] = total[m];
+    }
+    free(w);
+    free(total);
+    return NULL;
+}
+
+int orc_matvec_recipe_f32(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const float* x, int m_count,
+                          int64_t ldx, float* y, int64_t ldy, int threads) {
+    if (!shape_ok(format, rows, cols) || m_count <= 0 || cols % dot_run(format) != 0) return -1;
+    if (threads <= 1 || rows < 2) {
+        recipe_job job = {format, bytes, cols, 0, rows, x, m_count, ldx, ldy, y};
+        recipe_rows(&job);
+        return 0;
+    }
+    if (threads > rows) threads = (int)rows;
+    pthread_t* tids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    recipe_job* jobs = (recipe_job*)malloc(sizeof(recipe_job) * (size_t)threads);
+    int64_t per = rows / threads, extra = rows % threads, begin = 0;
+    for (int t = 0; t < threads; ++t) {
+        int64_t count = per + (t < extra ? 1 : 0);
+        recipe_job job = {format, bytes, cols, begin, begin + count, x, m_count, ldx, ldy, y};
+        jobs[t] = job;
+        begin += count;
+        pthread_create(&tids[t], NULL, recipe_rows, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+    free(tids);
+    free(jobs);
+    return 0;
+}
+
+/* @sigmoid (amd-nv-cpu.ll:5007-5009): 1 / (1 + exp(-x)). */
+static double sigmoid_ref(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+/* @topk_score (amd-nv-cpu.ll:4486-4488). */
+static double topk_score(double score, double maximum, int sigmoid) {
+    return sigmoid ? sigmoid_ref(score) : exp(score - maximum);
+}
+
+/* @topk_forward_body (amd-nv-cpu.ll:4653-4716) without a selection bias:
+ * repeated scans pick the highest unmarked score, the lower expert on a tie;
+ * the maximum and total run over the kept set when renormalizing, over every
+ * expert otherwise; softmax (or renormalized sigmoid) divides by the total. */
+int orc_topk(const double* scores, int experts, int top, int scoring, int renormalize, double* weights) {
+    if (experts <= 0 || top <= 0 || top > experts) return -1;
+    const int sigmoid = scoring != 0, renorm = renormalize != 0;
+    const int every = !renorm, divide = renorm || !sigmoid;
+    for (int e = 0; e < experts; ++e) weights[e] = 0.0;
+    for (int pick = 0; pick < top; ++pick) {
+        int best = -1;
+        double best_score = 0.0;
+        for (int c = 0; c < experts; ++c) {
+            int unmarked = weights[c] == 0.0;
+            double key = scores[c];
+            int better = best == -1 || key > best_score;
+            if (unmarked && better) {
+                best = c;
+                best_score = key;
+            }
+        }
+        weights[best] = 1.0;
+    }
+    double maximum = 0.0;
+    int first = 1;
+    for (int m = 0; m < experts; ++m) {
+        int member = weights[m] == 1.0 || every;
+        if (member && (first || scores[m] > maximum)) {
+            maximum = scores[m];
+            first = 0;
+        }
+    }
+    double total = 0.0;
+    for (int s = 0; s < experts; ++s) {
+        int member = weights[s] == 1.0 || every;
+        total = total + (member ? topk_score(scores[s], maximum, sigmoid) : 0.0);
+    }
+    double denominator = divide ? total : 1.0;
+    for (int w = 0; w < experts; ++w) {
+        int marked = weights[w] == 1.0;
+        weights[w] = marked ? topk_score(scores[w], maximum, sigmoid) / denominator : 0.0;
+    }
+    return 0;
+}
+
+/* SiLU and Sigmoid as recipe lowers them (recipe.rs:22662-22668):
+ * sigmoid = 0.5 * (tanh(x / 2) + 1), silu = x * sigmoid. */
+static double act_sigmoid(double x) { return 0.5 * (tanh(0.5 * x) + 1.0); }
+static double act_silu(double x) { return x * act_sigmoid(x); }
+
+static double row_dot_f64(int format, const uint8_t* row_bytes, int64_t cols, const double* x) {
+    const int bv = orc_block_values(format), bb = orc_block_bytes(format);
+    double s = 0.0;
+    for (int64_t k = 0; k < cols; ++k) s += orc_dequant_value(format, row_bytes + (k / bv) * bb, (int)(k % bv)) * x[k];
+    return s;
+}
+
+static int64_t row_bytes_of(int format, int64_t cols) {
+    return cols / orc_block_values(format) * orc_block_bytes(format);
+}
+
+/* One SiLU-GLU expert (recipe.rs:23386-23401 lower_experts + lower_gated):
+ * out += weight * down(silu(gate x) * up x). */
+static void expert_add(int format, int d, int hidden, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       const double* x, double weight, double* h, double* out) {
+    const int64_t in_row = row_bytes_of(format, d), out_row = row_bytes_of(format, hidden);
+    for (int f = 0; f < hidden; ++f) {
+        double g = row_dot_f64(format, gate + f * in_row, d, x);
+        double u = row_dot_f64(format, up + f * in_row, d, x);
+        h[f] = act_silu(g) * u;
+    }
+    for (int n = 0; n < d; ++n) out[n] += weight * row_dot_f64(format, down + n * out_row, hidden, h);
+}
+
+/* lower_gguf_moe (recipe.rs:23415-23459): router contraction over f16 weights,
+ * TopK, routed scale, the routed experts in ascending id, then the sigmoid-gated
+ * shared expert added. */
+int orc_moe_f64(int format, int d_model, int experts, int top, int hidden, int scoring, int renormalize, double scale,
+                const uint16_t* router, const uint8_t* gate_bank, const uint8_t* up_bank, const uint8_t* down_bank,
+                int hidden_shared, const uint16_t* shared_gate_vec, const uint8_t* gate_sh, const uint8_t* up_sh,
+                const uint8_t* down_sh, const double* x, double* y, double* route_weights) {
+    if (!shape_ok(format, 1, d_model) || !shape_ok(format, 1, hidden)) return -1;
+    double* scores = (double*)malloc(sizeof(double) * (size_t)experts);
+    double* weights = (double*)malloc(sizeof(double) * (size_t)experts);
+    int hmax = hidden > hidden_shared ? hidden : hidden_shared;
+    double* h = (double*)malloc(sizeof(double) * (size_t)(hmax > 0 ? hmax : 1));
+    for (int e = 0; e < experts; ++e) {
+        double s = 0.0;
+        for (int k = 0; k < d_model; ++k) s += (double)orc_f32_from_fp16(router[(int64_t)e * d_model + k]) * x[k];
+        scores[e] = s;
+    }
+    int rc = orc_topk(scores, experts, top, scoring, renormalize, weights);
+    if (rc == 0) {
+        for (int n = 0; n < d_model; ++n) y[n] = 0.0;
+        const int64_t bank_in = (int64_t)hidden * row_bytes_of(format, d_model);
+        const int64_t bank_out = (int64_t)d_model * row_bytes_of(format, hidden);
+        for (int e = 0; e < experts; ++e) {
+            weights[e] *= scale;
+            if (weights[e] == 0.0) continue;
+            expert_add(format, d_model, hidden, gate_bank + e * bank_in, up_bank + e * bank_in,
+                       down_bank + e * bank_out, x, weights[e], h, y);
+        }
+        if (route_weights)
+            for (int e = 0; e < experts; ++e) route_weights[e] = weights[e];
+        if (shared_gate_vec && gate_sh && up_sh && down_sh && hidden_shared > 0) {
+            double g = 0.0;
+            for (int k = 0; k < d_model; ++k) g += (double)orc_f32_from_fp16(shared_gate_vec[k]) * x[k];
+            double* shared = (double*)calloc((size_t)d_model, sizeof(double));
+            expert_add(format, d_model, hidden_shared, gate_sh, up_sh, down_sh, x, act_sigmoid(g), h, shared);
+            for (int n = 0; n < d_model; ++n) y[n] = y[n] + shared[n];
+            free(shared);
+        }
+    }
+    free(scores);
+    free(weights);
+    free(h);
+    return rc;
+}
+
+/* evidence/2026-10-10-m60-p2p/bench.rs:193-226, generalised from 4096 columns
+ * to any multiple of 256. */
+int orc_q4k_q81_reference(const uint8_t* w, int64_t rows, int64_t cols, const float* x, float* y, double* x_used) {
+    if (cols <= 0 || cols % 256 != 0) return -1;
+    const int64_t nblk = cols / 32, nsb = cols / 256;
+    int32_t* q = (int32_t*)calloc((size_t)cols, sizeof(int32_t));
+    double* d = (double*)calloc((size_t)nblk, sizeof(double));
+    for (int64_t b = 0; b < nblk; ++b) {
+        float mx = 0.0f;
+        for (int l = 0; l < 32; ++l) mx = fmaxf(mx, fabsf(x[b * 32 + l]));
+        float raw_d = mx / 127.0f;
+        if (mx == 0.0f) continue;
+        uint32_t bits;
+        memcpy(&bits, &raw_d, 4);
+        int e = (int)((bits >> 23) & 255u) - 127;
+        int p = e - 10 > -24 ? e - 10 : -24;
+        float step = ldexpf(1.0f, p);
+        d[b] = (double)(nearbyintf(raw_d / step) * step); /* round half to even in the default mode */
+        for (int l = 0; l < 32; ++l) q[b * 32 + l] = (int32_t)roundf(x[b * 32 + l] / raw_d);
+    }
+    if (x_used)
+        for (int64_t k = 0; k < cols; ++k) x_used[k] = (double)q[k] * d[k / 32];
+    for (int64_t row = 0; row < rows; ++row) {
+        double acc = 0.0;
+        for (int64_t sb = 0; sb < nsb; ++sb) {
+            const uint8_t* blk = w + (row * nsb + sb) * 144;
+            double wd = (double)orc_f32_from_fp16((uint16_t)(blk[0] | (blk[1] << 8)));
+            double wm = (double)orc_f32_from_fp16((uint16_t)(blk[2] | (blk[3] << 8)));
+            for (int sub = 0; sub < 8; ++sub) {
+                int scale, mn;
+                if (sub < 4) {
+                    scale = blk[4 + sub] & 63;
+                    mn = blk[8 + sub] & 63;
+                } else {
+                    scale = (blk[12 + sub - 4] & 15) | ((blk[4 + sub - 4] >> 6) << 4);
+                    mn = (blk[12 + sub - 4] >> 4) | ((blk[8 + sub - 4] >> 6) << 4);
+                }
+                int32_t dot = 0, sum = 0;
+                for (int lane = 0; lane < 32; ++lane) {
+                    uint8_t packed = blk[16 + (sub / 2) * 32 + lane];
+                    int weight = (sub & 1) == 0 ? (packed & 15) : (packed >> 4);
+                    int32_t a = q[sb * 256 + sub * 32 + lane];
+                    dot += weight * a;
+                    sum += a;
+                }
+                acc += ((double)(scale * dot) * wd - (double)(mn * sum) * wm) * d[sb * 8 + sub];
+            }
+        }
+        y[row] = (float)acc;
+    }
+    free(q);
+    free(d);
+    return 0;
+}
+
+/* evidence/2026-10-10-m60-p2p/bench.rs:177-190. */
+void orc_q4k_xorshift_rows(uint32_t seed, int64_t rows, uint16_t scale_bits, uint8_t* out) {
+    uint32_t state = seed;
+    const int64_t blocks = rows * 16;
+    for (int64_t blk = 0; blk < blocks; ++blk) {
+        uint8_t* b = out + blk * 144;
+        b[0] = (uint8_t)(scale_bits & 0xff);
+        b[1] = (uint8_t)(scale_bits >> 8);
+        b[2] = b[0];
+        b[3] = b[1];
+        for (int i = 0; i < 4; ++i) {
+            b[4 + i] = (uint8_t)(1 + ((state >> (i * 2)) % 3));
+            b[8 + i] = (uint8_t)(1 + ((state >> (i * 3)) % 3));
+        }
+        for (int i = 0; i < 4; ++i)
+            b[12 + i] = (uint8_t)((1 + ((state >> (i * 2)) % 3)) | ((1 + ((state >> (i * 3)) % 3)) << 4));
+        for (int j = 16; j < 144; ++j) {
+            state ^= state << 13;
+            state ^= state >> 17;
+            state ^= state << 5;
+            b[j] = (uint8_t)state;
+        }
+    }
+}

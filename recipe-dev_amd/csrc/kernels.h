@@ -1,0 +1,45 @@
+// Internal launch interface between the C-ABI layer and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "chunk.h"
+
+namespace rq {
+
+enum XType : int { X_F32 = 0, X_F16 = 1 };
+
+// A matrix-vector product over a repacked weight: y[m*ldy + n] =
+// sum_k W[n][k] x[m*ldx + k] for n < rows, m < M.
+struct MvParams {
+    Planes P;
+    int64_t rows;
+    int K;
+    const void* x;
+    int64_t ldx;
+    float* y;
+    int64_t ldy;
+    int G;  // lanes that share one row (power of two, 8..64)
+};
+
+struct LaunchShape {
+    int G = 64;       // lanes per row group
+    int R = 1;        // rows per lane group per tile
+    int block = 256;  // threads per workgroup
+    int grid = 0;     // workgroups (0 = derive)
+};
+
+// Chooses G, R, block and grid for a product; honours RQMV_G / RQMV_R /
+// RQMV_BLOCK / RQMV_GRID overrides for tuning sweeps.
+LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus);
+
+// ev0 / ev1 (may be null): events the dispatch records at its start and end.
+hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const LaunchShape& s, hipStream_t stream,
+                         hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+
+// Exact fp32 decode of every weight, rows x cols in GGUF order.
+hipError_t launch_dequant(int fmt, const Planes& P, int64_t rows, int cols, float* out, hipStream_t stream);
+
+size_t matvec_lds_bytes(int fmt, int xtype, int M, int cols);
+
+}  // namespace rq

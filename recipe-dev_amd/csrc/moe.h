@@ -1,0 +1,46 @@
+// gguf_moe decode-step kernels (one position).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "chunk.h"
+
+namespace rq {
+
+// A routed expert bank or a single (shared) expert, as the MoE kernels read it.
+struct MoeBank {
+    Planes P;          // planes of expert 0, row 0
+    int64_t rows;      // rows per expert
+};
+
+struct MoeDims {
+    int d_model, experts, top, hidden, hidden_shared;  // hidden_shared = 0: no shared expert
+    int scoring, renormalize;
+    int shared_gated;  // 1: the shared expert is weighted by sigmoid(gate . x); 0: by one
+    float scale;
+};
+
+// Workspace carve-up (floats unless noted), all in one device buffer.
+struct MoeWorkspace {
+    float* logits;  // experts + 1 (router scores, then the shared gate score)
+    int* ids;       // top (selected experts in ascending id)
+    float* weights; // top + 1 (routing weights, then the shared expert's gate)
+    float* h;       // top * hidden + hidden_shared (SiLU(gate) * up per slot)
+};
+
+size_t moe_workspace_bytes(const MoeDims& d);
+MoeWorkspace moe_workspace(void* base, const MoeDims& d);
+
+// Top-k routing on one wave (amd-nv-cpu.ll:4489-4652 topk_forward_wave_body semantics).
+hipError_t launch_moe_topk(const MoeDims& d, MoeWorkspace ws, float* route_dense, hipStream_t stream);
+
+// h[slot][f] = silu(gate_slot[f] . x) * (up_slot[f] . x) for every routed slot and the shared expert.
+hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
+                          const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws, int cus,
+                          hipStream_t stream);
+
+// y[n] = sum_slot w_slot * (down_slot[n] . h_slot), routed slots in ascending expert id, then the shared expert.
+hipError_t launch_moe_down(int fmt, const MoeDims& d, const MoeBank& down, const MoeBank& down_sh, MoeWorkspace ws,
+                           float* y, int cus, hipStream_t stream);
+
+}  // namespace rq

@@ -1,0 +1,417 @@
+// C-ABI entry points of librqmv (declared in include/rqmv.h).
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/rqmv.h"
+#include "kernels.h"
+#include "moe.h"
+#include "repack.h"
+
+struct rqmv_weight {
+    int fmt;
+    int64_t rows;     // rows of one matrix (of one expert)
+    int64_t cols;
+    int64_t experts;  // 1 for a plain weight
+    rq::RowBytes rb;
+    int64_t nch;
+    uint8_t* dev;
+    size_t dev_bytes;
+    uint8_t* code;
+    uint8_t* meta0;
+    uint8_t* meta1;
+    int device;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(RQMV_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct DeviceInfo {
+    bool ready = false;
+    int cus = 0;
+    size_t lds_limit = 0;
+};
+
+std::mutex g_mutex;
+DeviceInfo g_devices[64];
+
+int current_device(DeviceInfo* out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(RQMV_ESTATE, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!g_devices[dev].ready) return fail(RQMV_ESTATE, "rqmv_init was not called for device " + std::to_string(dev));
+    *out = g_devices[dev];
+    return dev;
+}
+
+rq::Planes planes_of(const rqmv_weight* w, int64_t first_row) {
+    rq::Planes P;
+    P.code = w->code + first_row * w->rb.code;
+    P.meta0 = w->meta0 ? w->meta0 + first_row * w->rb.meta0 : nullptr;
+    P.meta1 = w->meta1 ? w->meta1 + first_row * w->rb.meta1 : nullptr;
+    P.row_code = w->rb.code;
+    P.row_meta0 = w->rb.meta0;
+    P.row_meta1 = w->rb.meta1;
+    P.nch = (int)w->nch;
+    return P;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+int create(int format, int64_t experts, int64_t rows, int64_t cols, const void* bytes, size_t nbytes, rqmv_weight** out) {
+    if (!out) return fail(RQMV_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (!rq::format_supported(format) || format == rq::F32) return fail(RQMV_EINVAL, "unsupported format " + std::to_string(format));
+    if (experts <= 0 || rows <= 0 || cols <= 0) return fail(RQMV_EINVAL, "shape must be positive");
+    if (cols > (1 << 30)) return fail(RQMV_EINVAL, "cols too large");
+    const int64_t total_rows = experts * rows;
+    const int64_t want = rq::gguf_bytes(format, total_rows, cols);
+    if (want < 0) return fail(RQMV_EINVAL, "cols is not a whole number of blocks for this format");
+    if (!bytes || (size_t)want != nbytes)
+        return fail(RQMV_EINVAL, "expected " + std::to_string(want) + " GGUF bytes, got " + std::to_string(nbytes));
+    DeviceInfo info;
+    int dev = current_device(&info);
+    if (dev < 0) return dev;
+    const rq::RowBytes rb = rq::row_bytes(format, cols);
+    const size_t code_b = align256((size_t)(rb.code * total_rows));
+    const size_t m0_b = align256((size_t)(rb.meta0 * total_rows));
+    const size_t m1_b = align256((size_t)(rb.meta1 * total_rows));
+    std::vector<uint8_t> host(code_b + m0_b + m1_b, 0);
+    uint8_t* hc = host.data();
+    uint8_t* h0 = rb.meta0 ? hc + code_b : nullptr;
+    uint8_t* h1 = rb.meta1 ? hc + code_b + m0_b : nullptr;
+    if (rq::repack(format, total_rows, cols, static_cast<const uint8_t*>(bytes), hc, h0, h1) != 0)
+        return fail(RQMV_EINVAL, "repack failed");
+    uint8_t* d = nullptr;
+    hipError_t e = hipMalloc(&d, host.size());
+    if (e != hipSuccess) return fail(RQMV_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    e = hipMemcpy(d, host.data(), host.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return hip_fail(e, "hipMemcpy");
+    }
+    rqmv_weight* w = new rqmv_weight;
+    w->fmt = format;
+    w->rows = rows;
+    w->cols = cols;
+    w->experts = experts;
+    w->rb = rb;
+    w->nch = rq::chunks_per_row(format, cols);
+    w->dev = d;
+    w->dev_bytes = host.size();
+    w->code = d;
+    w->meta0 = rb.meta0 ? d + code_b : nullptr;
+    w->meta1 = rb.meta1 ? d + code_b + m0_b : nullptr;
+    w->device = dev;
+    *out = w;
+    return RQMV_OK;
+}
+
+int check_launch(const rqmv_weight* w, DeviceInfo* info) {
+    if (!w) return fail(RQMV_EINVAL, "weight is NULL");
+    int dev = current_device(info);
+    if (dev < 0) return dev;
+    if (dev != w->device) return fail(RQMV_ESTATE, "weight lives on another device than the current one");
+    return RQMV_OK;
+}
+
+// Runs y = W x over rows [first_row, first_row + rows) of a weight, M rows of x
+// at a time in blocks the VALU kernels take (8, 4, 2, 1) and LDS can hold.
+int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const void* x, int xtype, int m, int64_t ldx,
+                float* y, int64_t ldy, hipStream_t stream, const DeviceInfo& info, hipEvent_t ev0 = nullptr,
+                hipEvent_t ev1 = nullptr) {
+    if (!x || !y) return fail(RQMV_EINVAL, "x or y is NULL");
+    if (xtype != RQMV_DTYPE_F16 && xtype != RQMV_DTYPE_F32) return fail(RQMV_EINVAL, "x_dtype must be F16 or F32");
+    if (m <= 0) return fail(RQMV_EINVAL, "m must be positive");
+    if (m > 1 && (ldx < w->cols || ldy < rows)) return fail(RQMV_EINVAL, "ldx < cols or ldy < rows");
+    const size_t esize = xtype == RQMV_DTYPE_F16 ? 2 : 4;
+    rq::MvParams p;
+    p.P = planes_of(w, first_row);
+    p.rows = rows;
+    p.K = (int)w->cols;
+    p.ldx = ldx;
+    p.ldy = ldy;
+    int done = 0;
+    while (done < m) {
+        int mb = 8;
+        while (mb > m - done) mb >>= 1;
+        while (mb > 1 && rq::matvec_lds_bytes(w->fmt, xtype, mb, (int)w->cols) > info.lds_limit) mb >>= 1;
+        if (rq::matvec_lds_bytes(w->fmt, xtype, mb, (int)w->cols) > info.lds_limit)
+            return fail(RQMV_EINVAL, "cols too large for one LDS stage");
+        p.x = static_cast<const char*>(x) + (size_t)done * (size_t)ldx * esize;
+        p.y = y + (int64_t)done * ldy;
+        rq::LaunchShape s = rq::plan_matvec(w->fmt, rows, w->cols, mb, xtype, info.cus);
+        p.G = s.G;
+        const bool first = done == 0, last = done + mb >= m;
+        hipError_t e = rq::launch_matvec(w->fmt, xtype, mb, p, s, stream, first ? ev0 : nullptr, last ? ev1 : nullptr);
+        if (e != hipSuccess) return hip_fail(e, "matvec launch");
+        done += mb;
+    }
+    return RQMV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rqmv_init(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count || device >= 64) return fail(RQMV_EINVAL, "no such device");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    int cus = 0, lds = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    g_devices[device].cus = cus > 0 ? cus : 1;
+    g_devices[device].lds_limit = lds > 0 ? (size_t)lds : 65536;
+    g_devices[device].ready = true;
+    g_error.clear();
+    return RQMV_OK;
+}
+
+const char* rqmv_last_error(void) { return g_error.c_str(); }
+
+int rqmv_weight_create(int format, int64_t rows, int64_t cols, const void* gguf_bytes, size_t nbytes, rqmv_weight** out) {
+    return create(format, 1, rows, cols, gguf_bytes, nbytes, out);
+}
+
+int rqmv_expert_bank_create(int format, int64_t experts, int64_t rows, int64_t cols, const void* gguf_bytes,
+                            size_t nbytes, rqmv_weight** out) {
+    return create(format, experts, rows, cols, gguf_bytes, nbytes, out);
+}
+
+int rqmv_weight_destroy(rqmv_weight* w) {
+    if (!w) return RQMV_OK;
+    hipError_t e = hipFree(w->dev);
+    delete w;
+    if (e != hipSuccess) return hip_fail(e, "hipFree");
+    return RQMV_OK;
+}
+
+int rqmv_weight_info(const rqmv_weight* w, int* format, int64_t* rows, int64_t* cols, int64_t* experts,
+                     size_t* device_bytes) {
+    if (!w) return fail(RQMV_EINVAL, "weight is NULL");
+    if (format) *format = w->fmt;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (experts) *experts = w->experts;
+    if (device_bytes) *device_bytes = w->dev_bytes;
+    return RQMV_OK;
+}
+
+int rqmv_weight_unpack(const rqmv_weight* w, void* gguf_bytes, size_t nbytes) {
+    if (!w || !gguf_bytes) return fail(RQMV_EINVAL, "NULL argument");
+    const int64_t total_rows = w->rows * w->experts;
+    const int64_t want = rq::gguf_bytes(w->fmt, total_rows, w->cols);
+    if ((size_t)want != nbytes) return fail(RQMV_EINVAL, "nbytes does not match the GGUF size");
+    std::vector<uint8_t> host(w->dev_bytes);
+    hipError_t e = hipMemcpy(host.data(), w->dev, w->dev_bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
+    const uint8_t* hc = host.data();
+    const uint8_t* h0 = w->meta0 ? hc + (w->meta0 - w->dev) : nullptr;
+    const uint8_t* h1 = w->meta1 ? hc + (w->meta1 - w->dev) : nullptr;
+    if (rq::unpack(w->fmt, total_rows, w->cols, hc, h0, h1, static_cast<uint8_t*>(gguf_bytes)) != 0)
+        return fail(RQMV_EINVAL, "unpack failed");
+    return RQMV_OK;
+}
+
+int rqmv_weight_dequantize(const rqmv_weight* w, float* out_dev, void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(w, &info);
+    if (rc != RQMV_OK) return rc;
+    if (!out_dev) return fail(RQMV_EINVAL, "out is NULL");
+    hipError_t e = rq::launch_dequant(w->fmt, planes_of(w, 0), w->rows * w->experts, (int)w->cols, out_dev,
+                                      static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return RQMV_OK;
+}
+
+int rqmv_matvec(const rqmv_weight* w, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev, int64_t ldy,
+                void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(w, &info);
+    if (rc != RQMV_OK) return rc;
+    return matvec_rows(w, 0, w->rows * w->experts, x_dev, x_dtype, m, ldx, y_dev, ldy,
+                       static_cast<hipStream_t>(stream), info);
+}
+
+int rqmv_matvec_timed(const rqmv_weight* w, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev,
+                      int64_t ldy, void* stream, void* start_event, void* stop_event) {
+    DeviceInfo info;
+    int rc = check_launch(w, &info);
+    if (rc != RQMV_OK) return rc;
+    return matvec_rows(w, 0, w->rows * w->experts, x_dev, x_dtype, m, ldx, y_dev, ldy,
+                       static_cast<hipStream_t>(stream), info, static_cast<hipEvent_t>(start_event),
+                       static_cast<hipEvent_t>(stop_event));
+}
+
+int rqmv_expert_matvec(const rqmv_weight* bank, int64_t expert, const void* x_dev, int x_dtype, int m, int64_t ldx,
+                       float* y_dev, int64_t ldy, void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(bank, &info);
+    if (rc != RQMV_OK) return rc;
+    if (expert < 0 || expert >= bank->experts) return fail(RQMV_EINVAL, "expert index out of range");
+    return matvec_rows(bank, expert * bank->rows, bank->rows, x_dev, x_dtype, m, ldx, y_dev, ldy,
+                       static_cast<hipStream_t>(stream), info);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Validates the gguf_moe operands (Builder::expert_planes shape rules,
+// recipe.rs:18274-18316) and fills the kernel-side description.
+int moe_dims(const rqmv_moe_params* p, rq::MoeDims* d, const DeviceInfo& info) {
+    (void)info;
+    if (!p) return fail(RQMV_EINVAL, "params is NULL");
+    if (!p->router || !p->gate_exps || !p->up_exps || !p->down_exps) return fail(RQMV_EINVAL, "router and banks are required");
+    const rqmv_weight *r = p->router, *g = p->gate_exps, *u = p->up_exps, *dn = p->down_exps;
+    if (r->fmt != rq::F16 || r->experts != 1) return fail(RQMV_EINVAL, "router must be a plain F16 weight");
+    const int64_t E = r->rows, D = r->cols;
+    if (g->fmt != u->fmt || g->fmt != dn->fmt) return fail(RQMV_EINVAL, "gate, up and down banks must share a format");
+    if (g->fmt == rq::F16) return fail(RQMV_EINVAL, "expert banks must be quantized");
+    if (g->experts != E || u->experts != E || dn->experts != E) return fail(RQMV_EINVAL, "bank expert count differs from the router rows");
+    const int64_t H = g->rows;
+    if (g->cols != D || u->cols != D || u->rows != H) return fail(RQMV_EINVAL, "gate/up banks must be experts x hidden x d_model");
+    if (dn->rows != D || dn->cols != H) return fail(RQMV_EINVAL, "down bank must be experts x d_model x hidden");
+    const int cw = rq::format_info(g->fmt).chunk_values;
+    if (H % cw != 0 || D % cw != 0) return fail(RQMV_EINVAL, "hidden and d_model must be multiples of the format's chunk");
+    if (p->top_k < 1 || p->top_k > 64 || p->top_k > E) return fail(RQMV_EINVAL, "top_k must be in 1..min(64, experts)");
+    if (E > 2048) return fail(RQMV_EINVAL, "at most 2048 experts");
+    if (p->scoring != RQMV_SCORE_SOFTMAX && p->scoring != RQMV_SCORE_SIGMOID) return fail(RQMV_EINVAL, "bad scoring");
+    int64_t HS = 0;
+    const bool any_shared = p->gate_shexp || p->up_shexp || p->down_shexp;
+    if (any_shared) {
+        const rqmv_weight *gs = p->gate_shexp, *us = p->up_shexp, *ds = p->down_shexp;
+        if (!gs || !us || !ds) return fail(RQMV_EINVAL, "shared expert needs gate, up and down");
+        if (gs->fmt != g->fmt || us->fmt != g->fmt || ds->fmt != g->fmt) return fail(RQMV_EINVAL, "shared expert format differs from the banks");
+        if (gs->experts != 1 || us->experts != 1 || ds->experts != 1) return fail(RQMV_EINVAL, "shared expert weights must be plain");
+        HS = gs->rows;
+        if (gs->cols != D || us->cols != D || us->rows != HS || ds->rows != D || ds->cols != HS)
+            return fail(RQMV_EINVAL, "shared expert shapes must be hidden_shared x d_model and d_model x hidden_shared");
+        if (HS % cw != 0) return fail(RQMV_EINVAL, "hidden_shared must be a multiple of the format's chunk");
+        if (p->shared_gate_inp) {
+            const rqmv_weight* sg = p->shared_gate_inp;
+            if (sg->fmt != rq::F16 || sg->rows != 1 || sg->cols != D || sg->experts != 1)
+                return fail(RQMV_EINVAL, "shared_gate_inp must be a 1 x d_model F16 weight");
+        }
+    } else if (p->shared_gate_inp) {
+        return fail(RQMV_EINVAL, "shared_gate_inp given without a shared expert");
+    }
+    d->d_model = (int)D;
+    d->experts = (int)E;
+    d->top = p->top_k;
+    d->hidden = (int)H;
+    d->hidden_shared = (int)HS;
+    d->scoring = p->scoring;
+    d->renormalize = p->renormalize ? 1 : 0;
+    d->shared_gated = p->shared_gate_inp ? 1 : 0;
+    d->scale = p->scale;
+    return RQMV_OK;
+}
+
+rq::MoeBank bank_of(const rqmv_weight* w) {
+    rq::MoeBank b;
+    if (!w) {
+        b.P = rq::Planes{nullptr, nullptr, nullptr, 0, 0, 0, 0};
+        b.rows = 0;
+        return b;
+    }
+    b.P = planes_of(w, 0);
+    b.rows = w->rows;
+    return b;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rqmv_moe_workspace_size(const rqmv_moe_params* params, size_t* bytes) {
+    DeviceInfo info;
+    if (!bytes) return fail(RQMV_EINVAL, "bytes is NULL");
+    rq::MoeDims d;
+    int rc = moe_dims(params, &d, info);
+    if (rc != RQMV_OK) return rc;
+    *bytes = rq::moe_workspace_bytes(d);
+    return RQMV_OK;
+}
+
+int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,
+             void* workspace, size_t workspace_bytes, void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(params ? params->router : nullptr, &info);
+    if (rc != RQMV_OK) return rc;
+    rq::MoeDims d;
+    rc = moe_dims(params, &d, info);
+    if (rc != RQMV_OK) return rc;
+    if (!x_dev || !y_dev || !workspace) return fail(RQMV_EINVAL, "x, y and workspace are required");
+    if (x_dtype != RQMV_DTYPE_F16 && x_dtype != RQMV_DTYPE_F32) return fail(RQMV_EINVAL, "x_dtype must be F16 or F32");
+    if (workspace_bytes < rq::moe_workspace_bytes(d)) return fail(RQMV_EINVAL, "workspace too small");
+    for (const rqmv_weight* w : {params->gate_exps, params->up_exps, params->down_exps, params->shared_gate_inp,
+                                 params->gate_shexp, params->up_shexp, params->down_shexp})
+        if (w && w->device != params->router->device) return fail(RQMV_ESTATE, "moe weights live on different devices");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rq::MoeWorkspace ws = rq::moe_workspace(workspace, d);
+    rc = matvec_rows(params->router, 0, d.experts, x_dev, x_dtype, 1, d.d_model, ws.logits, d.experts, s, info);
+    if (rc != RQMV_OK) return rc;
+    if (params->shared_gate_inp) {
+        rc = matvec_rows(params->shared_gate_inp, 0, 1, x_dev, x_dtype, 1, d.d_model, ws.logits + d.experts, 1, s, info);
+        if (rc != RQMV_OK) return rc;
+    }
+    hipError_t e = rq::launch_moe_topk(d, ws, route_dev, s);
+    if (e != hipSuccess) return hip_fail(e, "moe top-k launch");
+    const int fmt = params->gate_exps->fmt;
+    e = rq::launch_moe_glu(fmt, x_dtype, d, bank_of(params->gate_exps), bank_of(params->up_exps),
+                           bank_of(params->gate_shexp), bank_of(params->up_shexp), x_dev, ws, info.cus, s);
+    if (e != hipSuccess) return hip_fail(e, "moe gate/up launch");
+    e = rq::launch_moe_down(fmt, d, bank_of(params->down_exps), bank_of(params->down_shexp), ws, y_dev, info.cus, s);
+    if (e != hipSuccess) return hip_fail(e, "moe down launch");
+    return RQMV_OK;
+}
+
+int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* code_bytes, size_t* meta0_bytes,
+                      size_t* meta1_bytes) {
+    if (rq::gguf_bytes(format, rows, cols) < 0 || format == rq::F32) return fail(RQMV_EINVAL, "bad format or shape");
+    const rq::RowBytes rb = rq::row_bytes(format, cols);
+    if (code_bytes) *code_bytes = (size_t)(rb.code * rows);
+    if (meta0_bytes) *meta0_bytes = (size_t)(rb.meta0 * rows);
+    if (meta1_bytes) *meta1_bytes = (size_t)(rb.meta1 * rows);
+    return RQMV_OK;
+}
+
+int rqmv_repack_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, void* code, void* meta0,
+                     void* meta1) {
+    if (!gguf_bytes || !code) return fail(RQMV_EINVAL, "NULL argument");
+    if (rq::repack(format, rows, cols, static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(code),
+                   static_cast<uint8_t*>(meta0), static_cast<uint8_t*>(meta1)) != 0)
+        return fail(RQMV_EINVAL, "bad format or shape");
+    return RQMV_OK;
+}
+
+int rqmv_unpack_host(int format, int64_t rows, int64_t cols, const void* code, const void* meta0, const void* meta1,
+                     void* gguf_bytes) {
+    if (!gguf_bytes || !code) return fail(RQMV_EINVAL, "NULL argument");
+    if (rq::unpack(format, rows, cols, static_cast<const uint8_t*>(code), static_cast<const uint8_t*>(meta0),
+                   static_cast<const uint8_t*>(meta1), static_cast<uint8_t*>(gguf_bytes)) != 0)
+        return fail(RQMV_EINVAL, "bad format or shape");
+    return RQMV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,388 @@
+"""Python binding of librqmv, the gfx950 GGUF quantized matrix-vector library.
+
+A thin ctypes layer over the C ABI in include/rqmv.h plus the few HIP runtime
+calls a host program needs (device buffers, streams, events), taken from the
+same libamdhip64 that librqmv links. Nothing here computes: every product runs
+in librqmv's HIP kernels, and loading fails loudly when the library is absent.
+
+The host-side names mirror recipe's single-op API (recipe.rs:17126-17199):
+`contract(weight, x)` is Gguf::contract (one projection, fp32 out) and
+`expert(bank, index, x)` is Gguf::expert; `moe(...)` runs one gguf_moe block.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
+
+import numpy as np
+
+from . import synth  # noqa: F401
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "librqmv.so")
+
+F16, Q4_0, Q8_0, Q4_K, Q6_K = 1, 2, 8, 12, 14
+FORMATS = {"f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_k": Q4_K, "q6_k": Q6_K}
+DTYPE_F32, DTYPE_F16 = 0, 1
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+
+_H2D, _D2H, _D2D = 1, 2, 3
+
+
+class RqmvError(RuntimeError):
+    pass
+
+
+class _Lib:
+    def __init__(self):
+        if not os.path.exists(LIB_PATH):
+            raise RqmvError(f"librqmv.so is not built ({LIB_PATH}); run __graft_entry__.build()")
+        self.lib = ctypes.CDLL(LIB_PATH)
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        L, H = self.lib, self.hip
+        L.rqmv_init.argtypes = [c_int]
+        L.rqmv_last_error.restype = c_char_p
+        L.rqmv_weight_create.argtypes = [c_int, c_int64, c_int64, c_void_p, c_size_t, POINTER(c_void_p)]
+        L.rqmv_expert_bank_create.argtypes = [c_int, c_int64, c_int64, c_int64, c_void_p, c_size_t, POINTER(c_void_p)]
+        L.rqmv_weight_destroy.argtypes = [c_void_p]
+        L.rqmv_weight_info.argtypes = [c_void_p, POINTER(c_int), POINTER(c_int64), POINTER(c_int64), POINTER(c_int64),
+                                       POINTER(c_size_t)]
+        L.rqmv_weight_unpack.argtypes = [c_void_p, c_void_p, c_size_t]
+        L.rqmv_weight_dequantize.argtypes = [c_void_p, c_void_p, c_void_p]
+        L.rqmv_matvec.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p]
+        L.rqmv_matvec_timed.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p,
+                                        c_void_p, c_void_p]
+        L.rqmv_expert_matvec.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p]
+        L.rqmv_moe_workspace_size.argtypes = [c_void_p, POINTER(c_size_t)]
+        L.rqmv_moe.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t), POINTER(c_size_t), POINTER(c_size_t)]
+        L.rqmv_repack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.rqmv_unpack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
+        H.hipMalloc.argtypes = [POINTER(c_void_p), c_size_t]
+        H.hipFree.argtypes = [c_void_p]
+        H.hipMemcpy.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
+        H.hipMemset.argtypes = [c_void_p, c_int, c_size_t]
+        H.hipDeviceSynchronize.argtypes = []
+        H.hipStreamCreate.argtypes = [POINTER(c_void_p)]
+        H.hipStreamDestroy.argtypes = [c_void_p]
+        H.hipStreamSynchronize.argtypes = [c_void_p]
+        H.hipEventCreate.argtypes = [POINTER(c_void_p)]
+        H.hipEventDestroy.argtypes = [c_void_p]
+        H.hipEventRecord.argtypes = [c_void_p, c_void_p]
+        H.hipEventSynchronize.argtypes = [c_void_p]
+        H.hipEventElapsedTime.argtypes = [POINTER(c_float), c_void_p, c_void_p]
+        H.hipGetErrorString.restype = c_char_p
+        H.hipGetErrorString.argtypes = [c_int]
+        H.hipGetDeviceCount.argtypes = [POINTER(c_int)]
+        H.hipStreamBeginCapture.argtypes = [c_void_p, c_int]
+        H.hipStreamEndCapture.argtypes = [c_void_p, POINTER(c_void_p)]
+        H.hipGraphInstantiate.argtypes = [POINTER(c_void_p), c_void_p, c_void_p, c_char_p, c_size_t]
+        H.hipGraphLaunch.argtypes = [c_void_p, c_void_p]
+        H.hipGraphExecDestroy.argtypes = [c_void_p]
+        H.hipGraphDestroy.argtypes = [c_void_p]
+
+
+_lib = None
+
+
+def lib() -> _Lib:
+    global _lib
+    if _lib is None:
+        _lib = _Lib()
+    return _lib
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise RqmvError(f"{what} failed ({rc}): {lib().lib.rqmv_last_error().decode()}")
+
+
+def _hip(rc: int, what: str):
+    if rc != 0:
+        raise RqmvError(f"{what}: {lib().hip.hipGetErrorString(rc).decode()}")
+
+
+def device_count() -> int:
+    n = c_int(0)
+    rc = lib().hip.hipGetDeviceCount(byref(n))
+    return n.value if rc == 0 else 0
+
+
+def init(device: int = 0):
+    _check(lib().lib.rqmv_init(device), "rqmv_init")
+
+
+def synchronize():
+    _hip(lib().hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class DeviceBuffer:
+    """A device allocation (freed on close/garbage collection)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = c_void_p()
+        _hip(lib().hip.hipMalloc(byref(p), max(self.nbytes, 1)), "hipMalloc")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        _hip(lib().hip.hipMemcpy(self.ptr, arr.ctypes.data, arr.nbytes, _H2D), "hipMemcpy H2D")
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        n = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(n, dtype=dtype)
+        _hip(lib().hip.hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, _D2H), "hipMemcpy D2H")
+        return out
+
+    def fill_zero(self):
+        _hip(lib().hip.hipMemset(self.ptr, 0, self.nbytes), "hipMemset")
+
+    def close(self):
+        if self.ptr:
+            lib().hip.hipFree(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        s = c_void_p()
+        _hip(lib().hip.hipStreamCreate(byref(s)), "hipStreamCreate")
+        self.handle = s.value
+
+    def synchronize(self):
+        _hip(lib().hip.hipStreamSynchronize(self.handle), "hipStreamSynchronize")
+
+    def close(self):
+        if self.handle:
+            lib().hip.hipStreamDestroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        e = c_void_p()
+        _hip(lib().hip.hipEventCreate(byref(e)), "hipEventCreate")
+        self.handle = e.value
+
+    def record(self, stream=None):
+        _hip(lib().hip.hipEventRecord(self.handle, stream.handle if stream else None), "hipEventRecord")
+
+    def synchronize(self):
+        _hip(lib().hip.hipEventSynchronize(self.handle), "hipEventSynchronize")
+
+    def elapsed_ms(self, later: "Event") -> float:
+        ms = c_float(0.0)
+        _hip(lib().hip.hipEventElapsedTime(byref(ms), self.handle, later.handle), "hipEventElapsedTime")
+        return ms.value
+
+    def close(self):
+        if self.handle:
+            lib().hip.hipEventDestroy(self.handle)
+            self.handle = None
+
+
+class Graph:
+    """A HIP graph captured from the work a callable enqueues on `stream`."""
+
+    def __init__(self, stream: Stream, enqueue):
+        H = lib().hip
+        _hip(H.hipStreamBeginCapture(stream.handle, 2), "hipStreamBeginCapture")  # relaxed mode
+        try:
+            enqueue()
+        finally:
+            g = c_void_p()
+            _hip(H.hipStreamEndCapture(stream.handle, byref(g)), "hipStreamEndCapture")
+        self.graph = g.value
+        ex = c_void_p()
+        _hip(H.hipGraphInstantiate(byref(ex), self.graph, None, None, 0), "hipGraphInstantiate")
+        self.exec = ex.value
+
+    def launch(self, stream: Stream):
+        _hip(lib().hip.hipGraphLaunch(self.exec, stream.handle), "hipGraphLaunch")
+
+    def close(self):
+        if self.exec:
+            lib().hip.hipGraphExecDestroy(self.exec)
+            lib().hip.hipGraphDestroy(self.graph)
+            self.exec = None
+
+
+def _fmt(fmt) -> int:
+    return FORMATS[fmt] if isinstance(fmt, str) else int(fmt)
+
+
+class Weight:
+    """A repacked weight (or expert bank) resident on the device."""
+
+    def __init__(self, fmt, rows: int, cols: int, gguf: np.ndarray, experts: int | None = None):
+        gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
+        h = c_void_p()
+        if experts is None:
+            _check(lib().lib.rqmv_weight_create(_fmt(fmt), rows, cols, gguf.ctypes.data, gguf.nbytes, byref(h)),
+                   "rqmv_weight_create")
+        else:
+            _check(lib().lib.rqmv_expert_bank_create(_fmt(fmt), experts, rows, cols, gguf.ctypes.data, gguf.nbytes,
+                                                     byref(h)), "rqmv_expert_bank_create")
+        self.handle = h.value
+        self.fmt, self.rows, self.cols = _fmt(fmt), rows, cols
+        self.experts = 1 if experts is None else experts
+        self.gguf_nbytes = gguf.nbytes
+
+    def info(self):
+        f, r, c, e, b = c_int(), c_int64(), c_int64(), c_int64(), c_size_t()
+        _check(lib().lib.rqmv_weight_info(self.handle, byref(f), byref(r), byref(c), byref(e), byref(b)), "info")
+        return {"format": f.value, "rows": r.value, "cols": c.value, "experts": e.value, "device_bytes": b.value}
+
+    def unpack(self) -> np.ndarray:
+        out = np.empty(self.gguf_nbytes, dtype=np.uint8)
+        _check(lib().lib.rqmv_weight_unpack(self.handle, out.ctypes.data, out.nbytes), "rqmv_weight_unpack")
+        return out
+
+    def dequantize(self, out: DeviceBuffer, stream: Stream | None = None):
+        _check(lib().lib.rqmv_weight_dequantize(self.handle, out.ptr, stream.handle if stream else None),
+               "rqmv_weight_dequantize")
+
+    def matvec(self, x: DeviceBuffer, x_dtype: int, m: int, ldx: int, y: DeviceBuffer, ldy: int,
+               stream: Stream | None = None, x_offset: int = 0, y_offset: int = 0):
+        _check(lib().lib.rqmv_matvec(self.handle, x.ptr + x_offset, x_dtype, m, ldx, y.ptr + y_offset, ldy,
+                                     stream.handle if stream else None), "rqmv_matvec")
+
+    def matvec_timed(self, x: DeviceBuffer, x_dtype: int, m: int, ldx: int, y: DeviceBuffer, ldy: int,
+                     stream: Stream | None, start: "Event", stop: "Event"):
+        """matvec whose kernel dispatch records `start` and `stop` itself."""
+        _check(lib().lib.rqmv_matvec_timed(self.handle, x.ptr, x_dtype, m, ldx, y.ptr, ldy,
+                                           stream.handle if stream else None, start.handle, stop.handle),
+               "rqmv_matvec_timed")
+
+    def expert_matvec(self, expert: int, x: DeviceBuffer, x_dtype: int, m: int, ldx: int, y: DeviceBuffer, ldy: int,
+                      stream: Stream | None = None):
+        _check(lib().lib.rqmv_expert_matvec(self.handle, expert, x.ptr, x_dtype, m, ldx, y.ptr, ldy,
+                                            stream.handle if stream else None), "rqmv_expert_matvec")
+
+    def close(self):
+        if self.handle:
+            lib().lib.rqmv_weight_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _x_host(x: np.ndarray):
+    if x.dtype == np.float16:
+        return x.view(np.uint16), DTYPE_F16
+    if x.dtype == np.uint16:
+        return x, DTYPE_F16
+    return x.astype(np.float32), DTYPE_F32
+
+
+def contract(weight: Weight, x: np.ndarray) -> np.ndarray:
+    """One projection of host activations (Gguf::contract, recipe.rs:17130):
+    x is (K,) or (M, K) as float16 (or uint16 bits) or float32; returns fp32 (M, N)."""
+    x2 = np.atleast_2d(x)
+    xh, dt = _x_host(np.ascontiguousarray(x2))
+    m, k = xh.shape
+    xb = DeviceBuffer.from_array(xh)
+    yb = DeviceBuffer(4 * m * weight.rows * weight.experts)
+    weight.matvec(xb, dt, m, k, yb, weight.rows * weight.experts)
+    synchronize()
+    y = yb.download(np.float32).reshape(m, -1)
+    return y[0] if x.ndim == 1 else y
+
+
+def expert(bank: Weight, index: int, x: np.ndarray) -> np.ndarray:
+    """One expert of a bank (Gguf::expert, recipe.rs:17135)."""
+    x2 = np.atleast_2d(x)
+    xh, dt = _x_host(np.ascontiguousarray(x2))
+    m, k = xh.shape
+    xb = DeviceBuffer.from_array(xh)
+    yb = DeviceBuffer(4 * m * bank.rows)
+    bank.expert_matvec(index, xb, dt, m, k, yb, bank.rows)
+    synchronize()
+    y = yb.download(np.float32).reshape(m, -1)
+    return y[0] if x.ndim == 1 else y
+
+
+class MoeParams(ctypes.Structure):
+    _fields_ = [("router", c_void_p), ("gate_exps", c_void_p), ("up_exps", c_void_p), ("down_exps", c_void_p),
+                ("shared_gate_inp", c_void_p), ("gate_shexp", c_void_p), ("up_shexp", c_void_p),
+                ("down_shexp", c_void_p), ("top_k", c_int), ("scoring", c_int), ("renormalize", c_int),
+                ("scale", c_float)]
+
+
+class Moe:
+    """A gguf_moe block's weights and workspace on the device."""
+
+    def __init__(self, router: Weight, gate: Weight, up: Weight, down: Weight, top_k: int, scoring: int = SCORE_SOFTMAX,
+                 renormalize: bool = True, scale: float = 1.0, shared_gate_inp: Weight | None = None,
+                 gate_sh: Weight | None = None, up_sh: Weight | None = None, down_sh: Weight | None = None):
+        h = lambda w: w.handle if w is not None else None  # noqa: E731
+        self.params = MoeParams(h(router), h(gate), h(up), h(down), h(shared_gate_inp), h(gate_sh), h(up_sh),
+                                h(down_sh), top_k, scoring, 1 if renormalize else 0, scale)
+        self.keep = (router, gate, up, down, shared_gate_inp, gate_sh, up_sh, down_sh)
+        self.d_model = router.cols
+        self.experts = router.rows
+        n = c_size_t()
+        _check(lib().lib.rqmv_moe_workspace_size(byref(self.params), byref(n)), "rqmv_moe_workspace_size")
+        self.workspace = DeviceBuffer(n.value)
+
+    def run(self, x: DeviceBuffer, x_dtype: int, y: DeviceBuffer, route: DeviceBuffer | None = None,
+            stream: Stream | None = None):
+        _check(lib().lib.rqmv_moe(byref(self.params), x.ptr, x_dtype, y.ptr, route.ptr if route else None,
+                                  self.workspace.ptr, self.workspace.nbytes, stream.handle if stream else None),
+               "rqmv_moe")
+
+    def __call__(self, x: np.ndarray):
+        """Host convenience: returns (y fp32 (d_model,), routing weights fp32 (experts,))."""
+        xh, dt = _x_host(np.ascontiguousarray(x))
+        xb = DeviceBuffer.from_array(xh)
+        yb = DeviceBuffer(4 * self.d_model)
+        rb = DeviceBuffer(4 * self.experts)
+        self.run(xb, dt, yb, rb)
+        synchronize()
+        return yb.download(np.float32), rb.download(np.float32)
+
+
+def layout_bytes(fmt, rows: int, cols: int):
+    a, b, c = c_size_t(), c_size_t(), c_size_t()
+    _check(lib().lib.rqmv_layout_bytes(_fmt(fmt), rows, cols, byref(a), byref(b), byref(c)), "rqmv_layout_bytes")
+    return a.value, b.value, c.value
+
+
+def repack_host(fmt, rows: int, cols: int, gguf: np.ndarray):
+    code_n, m0_n, m1_n = layout_bytes(fmt, rows, cols)
+    code = np.zeros(code_n, np.uint8)
+    m0 = np.zeros(max(m0_n, 1), np.uint8)
+    m1 = np.zeros(max(m1_n, 1), np.uint8)
+    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    _check(lib().lib.rqmv_repack_host(_fmt(fmt), rows, cols, g.ctypes.data, code.ctypes.data,
+                                      m0.ctypes.data if m0_n else None, m1.ctypes.data if m1_n else None),
+           "rqmv_repack_host")
+    return code, m0[:m0_n], m1[:m1_n]
+
+
+def unpack_host(fmt, rows: int, cols: int, code, m0, m1, nbytes: int) -> np.ndarray:
+    out = np.zeros(nbytes, np.uint8)
+    _check(lib().lib.rqmv_unpack_host(_fmt(fmt), rows, cols, code.ctypes.data, m0.ctypes.data if m0.size else None,
+                                      m1.ctypes.data if m1.size else None, out.ctypes.data), "rqmv_unpack_host")
+    return out

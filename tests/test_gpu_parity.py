@@ -1,0 +1,273 @@
+"""GPU parity: librqmv's HIP kernels against the CPU oracle, through the C ABI.
+
+Bars: dequantized weights bit-exact against recipe's reference dequantization
+rounded to fp32; matrix-vector outputs within rel-L2 1e-3 of recipe's own
+fp32-accumulate matvec (the oracle's matvec_recipe_f32) on identical seeded
+inputs; MoE routing picks the same experts with weights within 1e-5.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from rqmv import synth
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+THREADS = min(16, os.cpu_count() or 1)
+FMTS = ["q8_0", "q4_0", "q4_k", "q6_k"]
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _weights(fmt, rows, cols, seed):
+    if fmt == "f16":
+        return synth.f16_weights(rows, cols, 0.02, seed=seed)
+    return synth.weights(fmt, rows, cols, seed=seed)
+
+
+def _shapes(fmt):
+    if fmt in ("q4_k", "q6_k"):
+        return [(1, 256), (17, 768), (300, 4096), (77, 14336), (33, 5120)]
+    return [(1, 32), (5, 96), (300, 4096), (77, 14336), (33, 5120), (9, 160)]
+
+
+# ------------------------------------------------------------- dequant ----
+
+@pytest.mark.parametrize("fmt", FMTS + ["f16"])
+def test_dequant_bit_exact(gpu, fmt):
+    shapes = _shapes(fmt) if fmt != "f16" else [(3, 64), (40, 2048)]
+    for rows, cols in shapes:
+        w = _weights(fmt, rows, cols, seed=rows * 7 + cols)
+        W = gpu.Weight(fmt, rows, cols, w)
+        out = gpu.DeviceBuffer(4 * rows * cols)
+        W.dequantize(out)
+        gpu.synchronize()
+        got = out.download(np.float32)
+        ref = oracle.dequant_rows(fmt, w, rows, cols).reshape(-1) if fmt != "f16" else \
+            synth.fp16_to_f32(w.view(np.uint16))
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (fmt, rows, cols)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_extreme_scales_bit_exact(gpu, fmt):
+    rows, cols = 16, 512
+    w = synth.weights(fmt, rows, cols, seed=11).copy()
+    bb = synth.BLOCK[fmt][1]
+    blk = w.reshape(-1, bb)
+    scale_bits = np.array([0x0001, 0x03FF, 0x0000, 0x8001, 0x7BFF, 0xFBFF, 0x3C00, 0x2400], dtype=np.uint16)
+    at = 208 if fmt == "q6_k" else 0
+    for i in range(blk.shape[0]):
+        blk[i, at:at + 2] = scale_bits[i % 8:i % 8 + 1].view(np.uint8)
+        if fmt == "q4_k":
+            blk[i, 2:4] = scale_bits[(i + 3) % 8:(i + 3) % 8 + 1].view(np.uint8)
+    W = gpu.Weight(fmt, rows, cols, w)
+    out = gpu.DeviceBuffer(4 * rows * cols)
+    W.dequantize(out)
+    gpu.synchronize()
+    ref = oracle.dequant_rows(fmt, w, rows, cols).reshape(-1)
+    assert np.array_equal(out.download(np.float32).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_device_unpack_round_trip(gpu, fmt):
+    rows, cols = _shapes(fmt)[3]
+    w = synth.weights(fmt, rows, cols, seed=4)
+    W = gpu.Weight(fmt, rows, cols, w)
+    assert np.array_equal(W.unpack(), w)
+
+
+# -------------------------------------------------------------- matvec ----
+
+def _run_matvec(gpu, W, x_host, dtype, rows):
+    m, k = x_host.shape
+    xb = gpu.DeviceBuffer.from_array(x_host)
+    yb = gpu.DeviceBuffer(4 * m * rows)
+    W.matvec(xb, dtype, m, k, yb, rows)
+    gpu.synchronize()
+    return yb.download(np.float32).reshape(m, rows)
+
+
+def _x(m, k, dtype, seed):
+    if dtype == "f16":
+        bits = synth.activations_f16(m * k, seed=seed).reshape(m, k)
+        return bits, 1, synth.fp16_to_f32(bits)
+    v = synth.activations_f32(m * k, seed=seed).reshape(m, k)
+    return v, 0, v
+
+
+@pytest.mark.parametrize("fmt", FMTS + ["f16"])
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+def test_matvec_parity(gpu, fmt, xdt, m):
+    shapes = _shapes(fmt) if fmt != "f16" else [(3, 64), (257, 2048)]
+    for rows, cols in shapes:
+        w = _weights(fmt, rows, cols, seed=rows + 3 * cols + m)
+        W = gpu.Weight(fmt, rows, cols, w)
+        xh, dt, x32 = _x(m, cols, xdt, seed=cols + m)
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+        err = rel_l2(y, ref)
+        assert err <= REL_L2, (fmt, xdt, m, rows, cols, err)
+        if xdt == "f32":  # exact weights and fp32 fma: far inside the bar
+            assert err <= 1e-5, (fmt, m, rows, cols, err)
+
+
+def test_matvec_is_deterministic(gpu):
+    rows, cols = 4096, 4096
+    w = synth.q4_k(rows, cols, seed=1)
+    W = gpu.Weight("q4_k", rows, cols, w)
+    xh, dt, _ = _x(1, cols, "f16", 2)
+    a = _run_matvec(gpu, W, xh, dt, rows)
+    b = _run_matvec(gpu, W, xh, dt, rows)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_matvec_ldx_ldy_strides(gpu):
+    rows, cols, m = 96, 512, 3
+    w = synth.q4_k(rows, cols, seed=2)
+    W = gpu.Weight("q4_k", rows, cols, w)
+    ldx, ldy = cols + 64, rows + 32
+    bits = synth.activations_f16(m * ldx, seed=3).reshape(m, ldx)
+    xb = gpu.DeviceBuffer.from_array(bits)
+    yb = gpu.DeviceBuffer(4 * m * ldy)
+    yb.fill_zero()
+    W.matvec(xb, 1, m, ldx, yb, ldy)
+    gpu.synchronize()
+    y = yb.download(np.float32).reshape(m, ldy)
+    ref = oracle.matvec_recipe_f32("q4_k", w, rows, cols, synth.fp16_to_f32(bits[:, :cols]))
+    assert rel_l2(y[:, :rows], ref) <= REL_L2
+    assert (y[:, rows:] == 0).all()  # nothing written past the rows
+
+
+# ------------------------------------------------- workload-size configs ----
+
+CONFIGS = [
+    # (name, fmt, rows, cols, x dtype, M values)
+    ("q8_0 4096x4096 fp32 x", "q8_0", 4096, 4096, "f32", [1]),
+    ("q4_0 4096->14336", "q4_0", 14336, 4096, "f16", [1]),
+    ("q4_0 14336->4096", "q4_0", 4096, 14336, "f16", [1]),
+    ("q4_k 4096->14336", "q4_k", 14336, 4096, "f16", [1]),
+    ("q4_k 14336->4096", "q4_k", 4096, 14336, "f16", [1]),
+    ("q6_k 5120->25600", "q6_k", 25600, 5120, "f16", [1, 2, 4, 8, 16, 32]),
+    ("q8_0 5120->5120", "q8_0", 5120, 5120, "f16", [1, 2, 4, 8, 16, 32]),
+]
+
+
+@pytest.mark.parametrize("name,fmt,rows,cols,xdt,ms", CONFIGS, ids=[c[0] for c in CONFIGS])
+def test_workload_size_parity(gpu, name, fmt, rows, cols, xdt, ms):
+    w = synth.weights(fmt, rows, cols)
+    W = gpu.Weight(fmt, rows, cols, w)
+    for m in ms:
+        xh, dt, x32 = _x(m, cols, xdt, seed=100 + m)
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+        err = rel_l2(y, ref)
+        print(f"{name} M={m}: rel-L2 {err:.3e}", flush=True)
+        assert err <= REL_L2, (name, m, err)
+
+
+# -------------------------------------------------------------- expert ----
+
+def test_expert_matvec_reads_its_slice(gpu):
+    E, rows, cols = 5, 512, 2048
+    bank = synth.q4_k(E * rows, cols, seed=8)
+    B = gpu.Weight("q4_k", rows, cols, bank, experts=E)
+    assert B.info()["experts"] == E
+    xh, dt, x32 = _x(1, cols, "f16", 9)
+    row_bytes = cols // 256 * 144
+    for e in (0, 3, 4):
+        xb = gpu.DeviceBuffer.from_array(xh)
+        yb = gpu.DeviceBuffer(4 * rows)
+        B.expert_matvec(e, xb, dt, 1, cols, yb, rows)
+        gpu.synchronize()
+        ref = oracle.matvec_recipe_f32("q4_k", bank[e * rows * row_bytes:(e + 1) * rows * row_bytes], rows, cols, x32)
+        assert rel_l2(yb.download(np.float32), ref[0]) <= REL_L2
+
+
+# ----------------------------------------------------------------- moe ----
+
+def _moe_case(fmt, d, E, top, H, HS, gated, seed):
+    router = synth.f16_weights(E, d, 0.02, seed=seed, tag="router")
+    gate = synth.weights(fmt, E * H, d, seed=seed + 1, tag="gate")
+    up = synth.weights(fmt, E * H, d, seed=seed + 2, tag="up")
+    down = synth.weights(fmt, E * d, H, seed=seed + 3, tag="down")
+    shared = None
+    if HS:
+        sg = synth.f16_weights(1, d, 0.02, seed=seed + 4, tag="sg") if gated else None
+        shared = (sg, synth.weights(fmt, HS, d, seed=seed + 5, tag="gs"), synth.weights(fmt, HS, d, seed=seed + 6, tag="us"),
+                  synth.weights(fmt, d, HS, seed=seed + 7, tag="ds"))
+    return router, gate, up, down, shared
+
+
+@pytest.mark.parametrize("fmt,d,E,top,H,HS,gated,scoring,renorm,xdt", [
+    ("q4_k", 2048, 256, 8, 512, 512, True, 0, True, "f16"),   # the gguf_moe decode workload
+    ("q4_k", 512, 16, 4, 256, 0, False, 1, False, "f32"),
+    ("q6_k", 256, 8, 2, 256, 256, False, 1, True, "f16"),
+    ("q8_0", 256, 12, 3, 128, 64, True, 0, False, "f16"),
+    ("q4_0", 128, 4, 4, 64, 0, False, 0, True, "f32"),
+])
+def test_moe_parity(gpu, fmt, d, E, top, H, HS, gated, scoring, renorm, xdt):
+    router, gate, up, down, shared = _moe_case(fmt, d, E, top, H, HS, gated, seed=E + d)
+    xh, dt, x32 = _x(1, d, xdt, seed=d + 1)
+    Wr = gpu.Weight("f16", E, d, router)
+    Wg = gpu.Weight(fmt, H, d, gate, experts=E)
+    Wu = gpu.Weight(fmt, H, d, up, experts=E)
+    Wd = gpu.Weight(fmt, d, H, down, experts=E)
+    kw = {}
+    okw = {}
+    if shared is not None:
+        sg, gs, us, ds = shared
+        kw = dict(shared_gate_inp=gpu.Weight("f16", 1, d, sg) if gated else None, gate_sh=gpu.Weight(fmt, HS, d, gs),
+                  up_sh=gpu.Weight(fmt, HS, d, us), down_sh=gpu.Weight(fmt, d, HS, ds))
+        okw = dict(hidden_shared=HS, shared_gate_bits=sg.view(np.uint16) if gated else None, gate_sh=gs, up_sh=us,
+                   down_sh=ds)
+    moe = gpu.Moe(Wr, Wg, Wu, Wd, top, scoring=scoring, renormalize=renorm, **kw)
+    y, route = moe(xh[0])
+    y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
+                                   x32[0].astype(np.float64), scoring=scoring, renormalize=renorm, **okw)
+    if shared is not None and not gated:
+        # an ungated shared expert runs at weight one; the oracle's composition takes a gate vector,
+        # so compare against its routed part plus the shared expert computed densely
+        y_r, _ = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
+                                x32[0].astype(np.float64), scoring=scoring, renormalize=renorm)
+        gs_w = oracle.dequant_rows(fmt, shared[1], HS, d).astype(np.float64)
+        us_w = oracle.dequant_rows(fmt, shared[2], HS, d).astype(np.float64)
+        ds_w = oracle.dequant_rows(fmt, shared[3], d, HS).astype(np.float64)
+        xv = x32[0].astype(np.float64)
+        g = gs_w @ xv
+        y_ref = y_r + ds_w @ (g / (1 + np.exp(-g)) * (us_w @ xv))
+    assert np.array_equal(route != 0, rw_ref != 0), "routed experts differ"
+    assert np.allclose(route, rw_ref, rtol=1e-5, atol=1e-7)
+    err = rel_l2(y, y_ref)
+    print(f"moe {fmt} d={d} E={E} top={top}: rel-L2 {err:.3e}", flush=True)
+    assert err <= REL_L2
+
+
+# -------------------------------------------------------- error paths ----
+
+def test_bad_arguments_return_errors(gpu):
+    rows, cols = 64, 256
+    W = gpu.Weight("q4_k", rows, cols, synth.q4_k(rows, cols, seed=1))
+    xb = gpu.DeviceBuffer(2 * cols)
+    yb = gpu.DeviceBuffer(4 * rows)
+    with pytest.raises(gpu.RqmvError):
+        W.matvec(xb, 1, 0, cols, yb, rows)  # m = 0
+    with pytest.raises(gpu.RqmvError):
+        W.matvec(xb, 7, 1, cols, yb, rows)  # bad dtype
+    with pytest.raises(gpu.RqmvError):
+        W.matvec(xb, 1, 2, cols - 1, yb, rows)  # ldx < cols
+    B = gpu.Weight("q4_k", rows, cols, synth.q4_k(2 * rows, cols, seed=2), experts=2)
+    with pytest.raises(gpu.RqmvError):
+        B.expert_matvec(2, xb, 1, 1, cols, yb, rows)
+    with pytest.raises(gpu.RqmvError):
+        gpu.Weight("q4_k", rows, cols, synth.q4_k(rows, cols, seed=1)[:-1])  # short bytes
+    Wr = gpu.Weight("f16", 8, cols, synth.f16_weights(8, cols, 0.02, seed=3))
+    with pytest.raises(gpu.RqmvError):
+        gpu.Moe(Wr, W, W, W, 2)  # banks are not 8-expert banks
