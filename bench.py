@@ -97,7 +97,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs the matvec on a "
-              f"single MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+              f"single MI355X; rows would shard across GPUs with no collective on the hot path)", file=sys.stderr)
         sys.exit(2)
 
     import rqmv

@@ -23,7 +23,8 @@
  *   - Activations x are M rows of K values, row m at x + m*ldx elements
  *     (recipe stores positions contiguously per channel, x[k*length + p],
  *     amd-nv-cpu.ll:1161-1165; pass the transpose). Outputs y are fp32, row m
- *     of N values at y + m*ldy.
+ *     of N values at y + m*ldy. Rows of x start 16-byte aligned (x and
+ *     ldx * element size multiples of 16), as device allocations are.
  */
 #ifndef RQMV_H
 #define RQMV_H
@@ -141,12 +142,9 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
 
 /* Host-only loader functions (no device needed): the repacked layout's size
  * and the repack / unpack themselves, for inspection and testing. */
-int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* code_bytes, size_t* meta0_bytes,
-                      size_t* meta1_bytes);
-int rqmv_repack_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, void* code, void* meta0,
-                     void* meta1);
-int rqmv_unpack_host(int format, int64_t rows, int64_t cols, const void* code, const void* meta0, const void* meta1,
-                     void* gguf_bytes);
+int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* bytes);
+int rqmv_repack_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, void* out);
+int rqmv_unpack_host(int format, int64_t rows, int64_t cols, const void* in, void* gguf_bytes);
 
 #ifdef __cplusplus
 }

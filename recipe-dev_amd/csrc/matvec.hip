@@ -8,10 +8,11 @@
 // no scratch) and the first lane writes the rows. Waves stride over row tiles,
 // so a fixed, occupancy-sized grid covers any row count.
 //
-// Activations are staged once per workgroup into LDS, in a part-major layout
-// ([m][part][chunk] 16-byte units) that makes the lanes' LDS reads
-// conflict-free, together with the per-chunk activation sums that the fp16
-// form needs (chunk.h).
+// Activations are staged once per workgroup into LDS as 16-bit integer digit
+// words per 32-value block (stage.h), in a part-major layout ([m][part][chunk]
+// 16-byte units) that makes the lanes' LDS reads conflict-free; the chunk
+// products are exact int32 v_dot8_i32_i4 / v_dot4_i32_i8 sums scaled once per
+// block (chunk.h).
 //
 // Reference counterparts: packed_lanes_body / packed_lanes4_body / packed_unit_dot
 // (amd-nv-cpu.ll:2421-2664, 2674-3126, 2304-2364), where each lane of a wave
@@ -25,100 +26,181 @@
 
 namespace rq {
 
-template <int FMT, int M, int R>
-__global__ void __launch_bounds__(256) matvec_f16(MvParams p) {
-    constexpr int XP = xparts16<FMT>(), NS = nsums<FMT>();
-    extern __shared__ uint4 smem[];
-    const int nch = p.P.nch;
-    uint4* xq = smem;
-    float* sums = reinterpret_cast<float*>(smem + M * XP * nch);
-    stage_f16<FMT>(nch, p.K, p.x, p.ldx, M, xq, sums);
-    __syncthreads();
+// Walks this wave's (tile, step) pairs in order: step s of a tile takes chunk
+// c = g + s*G of the tile's rows, for s < ceil(nch / G) on every lane (a lane
+// whose chunk lies past the row does no work), so the whole wave reaches each
+// tile's cross-lane reduction together.
+struct StepWalk {
+    int64_t tile, tiles, tile_stride, rows_per_wave;
+    int s, steps, g, G, nch;
+    __device__ bool valid() const { return tile < tiles; }
+    __device__ int chunk() const { return g + s * G; }
+    __device__ void next() {
+        if (++s == steps) {
+            s = 0;
+            tile += tile_stride;
+        }
+    }
+};
 
-    const int G = p.G;
-    const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
+__device__ __forceinline__ StepWalk make_walk(const MvParams& p, int R, int g) {
+    StepWalk w;
     const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
-    const int64_t rows_per_wave = (int64_t)(64 / G) * R;
-    const int64_t tiles = (p.rows + rows_per_wave - 1) / rows_per_wave;
-    for (int64_t tile = (int64_t)blockIdx.x * wpb + wave; tile < tiles; tile += (int64_t)gridDim.x * wpb) {
-        const int64_t row0 = tile * rows_per_wave + (int64_t)sub * R;
-        float acc[R][M];
+    w.rows_per_wave = (int64_t)(64 / p.G) * R;
+    w.tiles = (p.rows + w.rows_per_wave - 1) / w.rows_per_wave;
+    w.tile = (int64_t)blockIdx.x * wpb + wave;
+    w.tile_stride = (int64_t)gridDim.x * wpb;
+    w.s = 0;
+    w.steps = (p.P.nch + p.G - 1) / p.G;
+    w.g = g;
+    w.G = p.G;
+    w.nch = p.P.nch;
+    return w;
+}
+
+// Loads step `w` for the lane's R rows. Rows or chunks past the end (and the
+// steps of a wave without a tile) load from a clamped in-range address
+// instead; their results are never added.
+template <int FMT, int R>
+__device__ __forceinline__ void load_rows(const MvParams& p, const StepWalk& w, int sub, ChunkData<FMT> (&d)[R]) {
+    const int64_t tile = w.tile < w.tiles ? w.tile : w.tiles - 1;
+    const int64_t row0 = tile * w.rows_per_wave + (int64_t)sub * R;
+    const int c = w.chunk() < w.nch ? w.chunk() : w.nch - 1;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
-        for (int c = g; c < nch; c += G) {
-            uint4 xv[M][XP];
-            float sv[M][NS];
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-#pragma unroll
-                for (int j = 0; j < XP; ++j) xv[m][j] = xq[(m * XP + j) * nch + c];
-#pragma unroll
-                for (int s = 0; s < NS; ++s) sv[m][s] = (Traits<FMT>::NS > 0) ? sums[(m * NS + s) * nch + c] : 0.f;
-            }
-            ChunkData<FMT> d[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows) load_chunk<FMT>(p.P, row0 + r, c, d[r]);
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows) dot_f16<FMT, M>(d[r], c, xv, sv, acc[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int m = 0; m < M; ++m) acc[r][m] = group_sum(acc[r][m], G);
-        if (g == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows)
-#pragma unroll
-                    for (int m = 0; m < M; ++m) p.y[(int64_t)m * p.ldy + row0 + r] = acc[r][m];
-        }
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + r < p.rows ? row0 + r : p.rows - 1;
+        load_chunk<FMT>(p.P, row, c, d[r]);
     }
 }
 
-template <int FMT, int M, int R>
-__global__ void __launch_bounds__(256) matvec_f32(MvParams p) {
-    extern __shared__ float4 smemf[];
+template <int M, int R>
+__device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int g, float (&acc)[R][M]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) acc[r][mm] = group_sum(acc[r][mm], p.G);
+    if (g == p.G - 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < p.rows)
+#pragma unroll
+                for (int mm = 0; mm < M; ++mm) p.y[(int64_t)mm * p.ldy + row0 + r] = acc[r][mm];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
+}
+
+// Quantized weights, integer dot of staged activation digits (chunk.h,
+// stage.h). Each wave loads one step's chunks and computes them; the waves
+// resident on a CU keep the memory system busy between them. The first
+// step's weight loads are issued before the activations are staged.
+template <int FMT, int M, int R, bool XF32>
+__global__ void __launch_bounds__(512) matvec_int(MvParams p) {
+    constexpr int XP = Traits<FMT>::XP;
+    extern __shared__ uint4 smem[];
     const int nch = p.P.nch;
-    stage_f32<FMT>(nch, p.K, p.x, p.ldx, M, smemf);
+    uint4* xd = smem;
+    uint4* xb = smem + M * XP * nch;
+    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane / p.G;
+    StepWalk w = make_walk(p, R, g);
+
+    ChunkData<FMT> cur[R];
+    if (stage_items<FMT>(nch, M) <= kStageNJ * (int)blockDim.x) {
+        StageItem<XF32> it[kStageNJ];
+        stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, M, it);
+        // keep the activation loads ahead of the weight loads: waiting for them
+        // then leaves the weight loads in flight
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        load_rows<FMT, R>(p, w, sub, cur);
+        stage_multi_finish<FMT, XF32>(nch, p.K, M, it, xd, reinterpret_cast<float*>(xb));
+    } else {
+        load_rows<FMT, R>(p, w, sub, cur);
+        stage_all<FMT, XF32>(nch, p.K, p.x, p.ldx, M, xd, reinterpret_cast<float*>(xb));
+    }
     __syncthreads();
 
-    const int G = p.G;
-    const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
-    const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
-    const int64_t rows_per_wave = (int64_t)(64 / G) * R;
-    const int64_t tiles = (p.rows + rows_per_wave - 1) / rows_per_wave;
-    for (int64_t tile = (int64_t)blockIdx.x * wpb + wave; tile < tiles; tile += (int64_t)gridDim.x * wpb) {
-        const int64_t row0 = tile * rows_per_wave + (int64_t)sub * R;
-        float acc[R][M];
+    float acc[R][M];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
-        for (int c = g; c < nch; c += G) {
+        for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
+    bool loaded = true;
+    while (w.valid()) {
+        if (!loaded) load_rows<FMT, R>(p, w, sub, cur);
+        loaded = false;
+        const int c = w.chunk();
+        const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+        if (c < nch) {
+            // one activation row's digits live at a time; the weights stay in registers
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if (row0 + r >= p.rows) continue;
-                ChunkData<FMT> d;
-                load_chunk<FMT>(p.P, row0 + r, c, d);
+            for (int mm = 0; mm < M; ++mm) {
+                uint4 xv[1][XP];
+                uint4 bv[1][2];
 #pragma unroll
-                for (int m = 0; m < M; ++m) acc[r][m] += chunk_dot_f32<FMT>(d, c, smemf, nch, c, m);
+                for (int j = 0; j < XP; ++j) xv[0][j] = xd[(mm * XP + j) * nch + c];
+                bv[0][0] = xb[(mm * 2 + 0) * nch + c];
+                bv[0][1] = xb[(mm * 2 + 1) * nch + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (row0 + r < p.rows) dot_int<FMT, 1>(cur[r], c, xv, bv, &acc[r][mm]);
             }
         }
+        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
+        w.next();
+    }
+}
+
+// F16 weights (router-sized): fp16 activations through v_dot2_f32_f16, fp32
+// activations through exact fp32 fma.
+template <int M, int R, bool XF32>
+__global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
+    extern __shared__ uint4 smem[];
+    const int nch = p.P.nch;
+    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane / p.G;
+    StepWalk w = make_walk(p, R, g);
+    ChunkData<F16> cur[R];
+    load_rows<F16, R>(p, w, sub, cur);
+    if constexpr (XF32)
+        stage_f32_quads(nch, p.K, p.x, p.ldx, M, reinterpret_cast<float4*>(smem));
+    else
+        stage_f16_pairs(nch, p.K, p.x, p.ldx, M, smem);
+    __syncthreads();
+
+    float acc[R][M];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[r][m] = group_sum(acc[r][m], G);
-        if (g == 0) {
+        for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
+    bool loaded = true;
+    while (w.valid()) {
+        if (!loaded) load_rows<F16, R>(p, w, sub, cur);
+        loaded = false;
+        const int c = w.chunk();
+        const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+        if (c < nch) {
+            if constexpr (XF32) {
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows)
+                for (int r = 0; r < R; ++r)
+                    if (row0 + r < p.rows)
 #pragma unroll
-                    for (int m = 0; m < M; ++m) p.y[(int64_t)m * p.ldy + row0 + r] = acc[r][m];
+                        for (int mm = 0; mm < M; ++mm)
+                            acc[r][mm] += chunk_dot_f32(cur[r], reinterpret_cast<const float4*>(smem), nch, c, mm);
+            } else {
+                uint4 xv[M][8];
+#pragma unroll
+                for (int mm = 0; mm < M; ++mm)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xv[mm][j] = smem[(mm * 8 + j) * nch + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (row0 + r < p.rows) dot_f16w<M>(cur[r], xv, acc[r]);
+            }
         }
+        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
+        w.next();
     }
 }
 
@@ -143,7 +225,9 @@ __global__ void __launch_bounds__(256) dequant_kernel(Planes P, int64_t rows, in
 
 size_t matvec_lds_bytes(int fmt, int xtype, int M, int cols) {
     if (!format_info(fmt).chunk_values) return 0;
-    return stage_bytes(fmt, xtype == X_F32, M, (int)chunks_per_row(fmt, cols));
+    const int nch = (int)chunks_per_row(fmt, cols);
+    if (fmt == F16) return stage_bytes_f16w(xtype == X_F32, M, nch);
+    return stage_bytes_int(fmt, M, nch);
 }
 
 static int env_int(const char* name, int fallback) {
@@ -157,9 +241,13 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     int G = 64;
     while (G > 8 && G > nch) G >>= 1;
     s.G = G;
-    s.R = M == 1 ? 4 : (M == 2 ? 2 : 1);
+    s.R = M <= 2 ? 2 : 1;
     if (xtype == X_F32) s.R = M == 1 ? 2 : 1;
-    s.block = 256;
+    // Long rows stage a large activation slice per block: fewer, wider blocks
+    // amortise it. Short rows favour more resident blocks per CU.
+    const bool long_rows = nch > 128;
+    s.block = long_rows ? 512 : 256;
+    int per_cu = long_rows ? 1 : 4;
     s.G = env_int("RQMV_G", s.G);
     s.R = env_int("RQMV_R", s.R);
     s.block = env_int("RQMV_BLOCK", s.block);
@@ -167,37 +255,39 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     const int64_t tiles = (rows + rows_per_wave - 1) / rows_per_wave;
     const int wpb = s.block / 64;
     int64_t grid = (tiles + wpb - 1) / wpb;
-    const int64_t cap = (int64_t)cus * env_int("RQMV_BLOCKS_PER_CU", 8);
+    const int64_t cap = (int64_t)cus * env_int("RQMV_BLOCKS_PER_CU", per_cu);
     if (grid > cap) grid = cap;
     s.grid = env_int("RQMV_GRID", (int)grid);
     if (s.grid < 1) s.grid = 1;
     return s;
 }
 
+template <typename K>
+static hipError_t launch_kernel(K kernel, const MvParams& p, const LaunchShape& s, size_t lds, hipStream_t stream,
+                                hipEvent_t ev0, hipEvent_t ev1) {
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    if (ev0 || ev1)  // events recorded by the dispatch itself: its start and completion
+        hipExtLaunchKernelGGL(kernel, dim3(s.grid), dim3(s.block), (uint32_t)lds, stream, ev0, ev1, 0u, p);
+    else
+        hipLaunchKernelGGL(kernel, dim3(s.grid), dim3(s.block), lds, stream, p);
+    return hipGetLastError();
+}
+
 template <int FMT, int M, int R>
 static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s, hipStream_t stream, hipEvent_t ev0,
                              hipEvent_t ev1) {
     const size_t lds = matvec_lds_bytes(FMT, xtype, M, p.K);
-    const void* fn = xtype == X_F16 ? reinterpret_cast<const void*>(&matvec_f16<FMT, M, R>)
-                                    : reinterpret_cast<const void*>(&matvec_f32<FMT, M, R>);
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    if (ev0 || ev1) {
-        // Events recorded by the dispatch itself: its start and completion times.
-        if (xtype == X_F16)
-            hipExtLaunchKernelGGL((matvec_f16<FMT, M, R>), dim3(s.grid), dim3(s.block), (uint32_t)lds, stream, ev0, ev1,
-                                  0u, p);
-        else
-            hipExtLaunchKernelGGL((matvec_f32<FMT, M, R>), dim3(s.grid), dim3(s.block), (uint32_t)lds, stream, ev0, ev1,
-                                  0u, p);
-    } else if (xtype == X_F16) {
-        hipLaunchKernelGGL((matvec_f16<FMT, M, R>), dim3(s.grid), dim3(s.block), lds, stream, p);
+    if constexpr (FMT == F16) {
+        if (xtype == X_F16) return launch_kernel(matvec_f16w<M, R, false>, p, s, lds, stream, ev0, ev1);
+        return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
-        hipLaunchKernelGGL((matvec_f32<FMT, M, R>), dim3(s.grid), dim3(s.block), lds, stream, p);
+        if (xtype == X_F16) return launch_kernel(matvec_int<FMT, M, R, false>, p, s, lds, stream, ev0, ev1);
+        return launch_kernel(matvec_int<FMT, M, R, true>, p, s, lds, stream, ev0, ev1);
     }
-    return hipGetLastError();
 }
 
 template <int FMT>

@@ -138,16 +138,12 @@ __global__ void __launch_bounds__(64) moe_topk_kernel(MoeDims d, MoeWorkspace ws
 template <int FMT, bool XF32>
 __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
                                                        MoeBank up_sh, const void* x, MoeWorkspace ws, int G) {
-    constexpr int XP = xparts16<FMT>(), NS = nsums<FMT>();
+    constexpr int XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
     const int nch = gate.P.nch;
-    uint4* xq = smem;
-    float* sums = reinterpret_cast<float*>(smem + XP * nch);
-    float4* xf = reinterpret_cast<float4*>(smem);
-    if constexpr (XF32)
-        stage_f32<FMT>(nch, d.d_model, x, 0, 1, xf);
-    else
-        stage_f16<FMT>(nch, d.d_model, x, 0, 1, xq, sums);
+    uint4* xd = smem;
+    uint4* xb = smem + XP * nch;
+    stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, xd, reinterpret_cast<float*>(xb));
     __syncthreads();
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
     const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
@@ -157,7 +153,7 @@ __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, M
     const int tiles = (total_rows + rows_per_wave - 1) / rows_per_wave;
     for (int tile = blockIdx.x * wpb + wave; tile < tiles; tile += gridDim.x * wpb) {
         const int r = tile * rows_per_wave + sub;
-        if (r >= total_rows) continue;  // whole lane group idles; shuffles stay inside the group
+        if (r >= total_rows) continue;  // whole lane group idles; reductions stay inside the group
         Planes pg, pu;
         int64_t rg, ru;
         if (r < routed) {
@@ -179,36 +175,33 @@ __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, M
             ChunkData<FMT> dg, du;
             load_chunk<FMT>(pg, rg, c, dg);
             load_chunk<FMT>(pu, ru, c, du);
-            if constexpr (XF32) {
-                ag += chunk_dot_f32<FMT>(dg, c, xf, nch, c, 0);
-                au += chunk_dot_f32<FMT>(du, c, xf, nch, c, 0);
-            } else {
-                uint4 xv[1][XP];
-                float sv[1][NS];
+            uint4 xv[1][XP];
+            uint4 bv[1][2];
 #pragma unroll
-                for (int j = 0; j < XP; ++j) xv[0][j] = xq[j * nch + c];
-#pragma unroll
-                for (int s = 0; s < NS; ++s) sv[0][s] = (Traits<FMT>::NS > 0) ? sums[s * nch + c] : 0.f;
-                dot_f16<FMT, 1>(dg, c, xv, sv, &ag);
-                dot_f16<FMT, 1>(du, c, xv, sv, &au);
-            }
+            for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
+            bv[0][0] = xb[c];
+            bv[0][1] = xb[nch + c];
+            dot_int<FMT, 1>(dg, c, xv, bv, &ag);
+            dot_int<FMT, 1>(du, c, xv, bv, &au);
         }
         ag = group_sum(ag, G);
         au = group_sum(au, G);
-        if (g == 0) ws.h[r] = ag * sigmoidf_dev(ag) * au;
+        if (g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
     }
 }
 
 template <int FMT>
 __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
                                                         float* y, int G) {
-    constexpr int CW = Traits<FMT>::CW;
-    extern __shared__ float4 smemf[];
+    constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
+    extern __shared__ uint4 smem[];
     const int K = d.top * d.hidden + d.hidden_shared;
     const int nch = K / CW;            // chunks of all slots back to back
     const int cps = d.hidden / CW;     // chunks per routed slot
     const int routed_ch = d.top * cps;
-    stage_f32<FMT>(nch, K, ws.h, 0, 1, smemf);
+    uint4* xd = smem;
+    uint4* xb = smem + XP * nch;
+    stage_all<FMT, true>(nch, K, ws.h, 0, 1, xd, reinterpret_cast<float*>(xb));
     __syncthreads();
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
     const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
@@ -232,10 +225,18 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, 
                 load_chunk<FMT>(down_sh.P, n, lc, cd);
                 w = ws.weights[d.top];
             }
-            acc = fmaf(w, chunk_dot_f32<FMT>(cd, lc, smemf, nch, c, 0), acc);
+            uint4 xv[1][XP];
+            uint4 bv[1][2];
+#pragma unroll
+            for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
+            bv[0][0] = xb[c];
+            bv[0][1] = xb[nch + c];
+            float part = 0.f;
+            dot_int<FMT, 1>(cd, lc, xv, bv, &part);
+            acc = fmaf(w, part, acc);
         }
         acc = group_sum(acc, G);
-        if (g == 0) y[n] = acc;
+        if (g == G - 1) y[n] = acc;
     }
 }
 
@@ -260,7 +261,13 @@ static hipError_t glu_fmt(int xtype, const MoeDims& d, const MoeBank& gate, cons
     const int rows_per_block = 4 * (64 / G);
     int grid = (total_rows + rows_per_block - 1) / rows_per_block;
     if (grid > cus * 8) grid = cus * 8;
-    const size_t lds = stage_bytes(FMT, xtype == 0, 1, nch);
+    const size_t lds = stage_bytes_int(FMT, 1, nch);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(xtype == 0 ? reinterpret_cast<const void*>(&moe_glu_kernel<FMT, true>)
+                                                       : reinterpret_cast<const void*>(&moe_glu_kernel<FMT, false>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
     if (xtype == 0)
         hipLaunchKernelGGL((moe_glu_kernel<FMT, true>), dim3(grid), dim3(256), lds, stream, d, gate, up, gate_sh, up_sh,
                            x, ws, G);
@@ -291,7 +298,7 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
     const int rows_per_block = 4 * (64 / G);
     int grid = (d.d_model + rows_per_block - 1) / rows_per_block;
     if (grid > cus * 8) grid = cus * 8;
-    const size_t lds = stage_bytes(FMT, 1, 1, nch);
+    const size_t lds = stage_bytes_int(FMT, 1, nch);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_down_kernel<FMT>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

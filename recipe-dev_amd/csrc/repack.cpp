@@ -1,12 +1,13 @@
 // Host-side loader repack: GGUF block bytes <-> the kernel's HBM layout
-// (layout.h). Both directions are exact byte permutations (plus the Q8_0 code
-// bias and Q4_0 odd-row padding), so unpack(repack(b)) == b.
+// (layout.h). Both directions are exact bijections on the bits (plus Q4_0's
+// odd-row padding and 16-byte row alignment), so unpack(repack(b)) == b.
 //
 // Reference counterpart: recipe's batch-1 loader interleaves rows four bytes at
 // a time across the lanes of a wave (recipe.rs:3162-3212 row_interleave /
 // interleave_rows, applied by Buffer::fill_weights at recipe.rs:26980-27010).
-// This layout instead gives each lane whole 16-byte parts of one row and makes
-// every load instruction of a wave one contiguous 1 KiB run.
+// This layout instead gives each lane whole 16-byte parts of one row, makes
+// every load instruction of a wave one contiguous 1 KiB run, and keeps each
+// group's scales beside its codes.
 #include "repack.h"
 
 #include <string.h>
@@ -31,28 +32,33 @@ static inline void q6_store(uint8_t* blk, int i, int q) {
     hi = (uint8_t)((hi & ~(3 << hs)) | (((q >> 4) & 3) << hs));
 }
 
-// One Q6_K scale group (16 weights, codes q[e]) -> words A, B, H (layout.h).
-static void q6k_pack_group(const uint8_t* q, uint32_t& A, uint32_t& B, uint32_t& H) {
-    A = B = H = 0;
-    for (int j = 0; j < 8; ++j) {
-        A |= (uint32_t)(q[kQ6EA[j]] & 15) << kQ6NibA[j];
-        B |= (uint32_t)(q[kQ6EB[j]] & 15) << kQ6NibB[j];
-    }
-    for (int e = 0; e < 16; ++e) H |= (uint32_t)((q[e] >> 4) & 3) << kQ6High[e];
+// 32 four-bit codes in natural order, XOR 8, two per byte (layout.h).
+static void pack_nibbles(const uint8_t* q, uint8_t* out16) {
+    for (int j = 0; j < 16; ++j) out16[j] = (uint8_t)(((q[2 * j] ^ 8) & 15) | (((q[2 * j + 1] ^ 8) & 15) << 4));
 }
 
-static void q6k_unpack_group(uint32_t A, uint32_t B, uint32_t H, uint8_t* q) {
-    for (int j = 0; j < 8; ++j) {
-        q[kQ6EA[j]] = (uint8_t)((A >> kQ6NibA[j]) & 15);
-        q[kQ6EB[j]] = (uint8_t)((B >> kQ6NibB[j]) & 15);
+static void unpack_nibbles(const uint8_t* in16, uint8_t* q) {
+    for (int j = 0; j < 16; ++j) {
+        q[2 * j] = (uint8_t)((in16[j] & 15) ^ 8);
+        q[2 * j + 1] = (uint8_t)((in16[j] >> 4) ^ 8);
     }
-    for (int e = 0; e < 16; ++e) q[e] = (uint8_t)(q[e] | (((H >> kQ6High[e]) & 3) << 4));
+}
+
+// Q6_K high fields of one 16-weight group as one word (layout.h).
+static uint32_t q6_high_word(const uint8_t* q6) {
+    uint32_t w = 0;
+    for (int j = 0; j < 8; ++j) {
+        w |= (uint32_t)((q6[j] >> 4) & 3) << (4 * j);
+        w |= (uint32_t)((q6[8 + j] >> 4) & 3) << (4 * j + 2);
+    }
+    return w;
 }
 
 static bool shape_ok(int fmt, int64_t rows, int64_t cols) {
     FormatInfo f = format_info(fmt);
     if (f.block_values == 0 || rows <= 0 || cols <= 0) return false;
     if (cols % f.block_values != 0) return false;
+    if (cols % 32 != 0) return false;
     if (fmt == F16 && cols % 64 != 0) return false;
     return true;
 }
@@ -63,152 +69,161 @@ int64_t gguf_bytes(int fmt, int64_t rows, int64_t cols) {
     return rows * (cols / f.block_values) * f.block_bytes;
 }
 
-int repack(int fmt, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* code, uint8_t* meta0, uint8_t* meta1) {
+int64_t layout_bytes(int fmt, int64_t rows, int64_t cols) {
+    if (!shape_ok(fmt, rows, cols)) return -1;
+    return rows * row_bytes(fmt, cols);
+}
+
+// Copies one chunk between its GGUF blocks (a row's block bytes) and the
+// layout (a row's repacked bytes): TO_LAYOUT reads `blocks` and writes `row`,
+// otherwise it reads `row` and writes `blocks`.
+template <bool TO_LAYOUT>
+static void chunk_copy(int fmt, const uint8_t* src_blocks, uint8_t* dst_blocks, const uint8_t* src_row, uint8_t* dst_row,
+                       int64_t c, int64_t nch, int64_t nblk) {
+    const ChunkPlace pl = chunk_place(fmt, c, nch);
+    const int64_t meta = meta_offset(fmt, c, nch);
+    auto part = [&](int p) { return code_offset(fmt, c, p, nch); };
+    switch (fmt) {
+        case Q8_0: {
+            if (TO_LAYOUT) {
+                const uint8_t* blk = src_blocks + c * 34;
+                memcpy(dst_row + meta + 2 * pl.within, blk, 2);
+                for (int p = 0; p < 2; ++p) memcpy(dst_row + part(p), blk + 2 + 16 * p, 16);
+            } else {
+                uint8_t* blk = dst_blocks + c * 34;
+                memcpy(blk, src_row + meta + 2 * pl.within, 2);
+                for (int p = 0; p < 2; ++p) memcpy(blk + 2 + 16 * p, src_row + part(p), 16);
+            }
+            break;
+        }
+        case Q4_0: {
+            for (int p = 0; p < 2; ++p) {
+                const int64_t b = 2 * c + p;
+                const int64_t d_at = meta + 4 * pl.within + 2 * p;
+                if (TO_LAYOUT) {
+                    if (b < nblk) {
+                        const uint8_t* blk = src_blocks + b * 18;
+                        memcpy(dst_row + d_at, blk, 2);
+                        uint8_t q[32];
+                        for (int i = 0; i < 16; ++i) {
+                            q[i] = blk[2 + i] & 15;  // byte i: weight i low nibble, i + 16 high
+                            q[i + 16] = blk[2 + i] >> 4;
+                        }
+                        pack_nibbles(q, dst_row + part(p));
+                    } else {
+                        memset(dst_row + d_at, 0, 2);
+                        memset(dst_row + part(p), 0, 16);  // q = 8: (q - 8) * d = 0
+                    }
+                } else if (b < nblk) {
+                    uint8_t* blk = dst_blocks + b * 18;
+                    memcpy(blk, src_row + d_at, 2);
+                    uint8_t q[32];
+                    unpack_nibbles(src_row + part(p), q);
+                    for (int i = 0; i < 16; ++i) blk[2 + i] = (uint8_t)((q[i] & 15) | ((q[i + 16] & 15) << 4));
+                }
+            }
+            break;
+        }
+        case Q4_K: {
+            const int64_t sb = c / 4;
+            const int p = (int)(c % 4);
+            const int64_t m_at = meta + (pl.within / 4) * 16;
+            if (TO_LAYOUT) {
+                const uint8_t* blk = src_blocks + sb * 144;
+                if (p == 0) memcpy(dst_row + m_at, blk, 16);
+                for (int h = 0; h < 2; ++h) {  // sub-block 2p + h: low or high nibbles of bytes 32p..32p+31
+                    uint8_t q[32];
+                    for (int i = 0; i < 32; ++i) q[i] = (blk[16 + 32 * p + i] >> (4 * h)) & 15;
+                    pack_nibbles(q, dst_row + part(h));
+                }
+            } else {
+                uint8_t* blk = dst_blocks + sb * 144;
+                if (p == 0) memcpy(blk, src_row + m_at, 16);
+                uint8_t lo[32], hi[32];
+                unpack_nibbles(src_row + part(0), lo);
+                unpack_nibbles(src_row + part(1), hi);
+                for (int i = 0; i < 32; ++i) blk[16 + 32 * p + i] = (uint8_t)(lo[i] | (hi[i] << 4));
+            }
+            break;
+        }
+        case Q6_K: {
+            const int64_t sb = c / 4;
+            const int t = (int)(c % 4);
+            const int64_t sc_at = meta + (pl.within / 4) * 16;
+            const int64_t d_at = meta + (pl.nb / 4) * 16 + (pl.within / 4) * 2;
+            if (TO_LAYOUT) {
+                const uint8_t* blk = src_blocks + sb * 210;
+                if (t == 0) {
+                    memcpy(dst_row + sc_at, blk + 192, 16);
+                    memcpy(dst_row + d_at, blk + 208, 2);
+                }
+                uint8_t q6[64], lo[64];
+                for (int e = 0; e < 64; ++e) {
+                    q6[e] = q6_code(blk, 64 * t + e);
+                    lo[e] = q6[e] & 15;
+                }
+                pack_nibbles(lo, dst_row + part(0));
+                pack_nibbles(lo + 32, dst_row + part(1));
+                uint32_t hi[4];
+                for (int g = 0; g < 4; ++g) hi[g] = q6_high_word(q6 + 16 * g);
+                memcpy(dst_row + part(2), hi, 16);
+            } else {
+                uint8_t* blk = dst_blocks + sb * 210;
+                if (t == 0) {
+                    memset(blk, 0, 192);
+                    memcpy(blk + 192, src_row + sc_at, 16);
+                    memcpy(blk + 208, src_row + d_at, 2);
+                }
+                uint8_t lo[64];
+                unpack_nibbles(src_row + part(0), lo);
+                unpack_nibbles(src_row + part(1), lo + 32);
+                uint32_t hi[4];
+                memcpy(hi, src_row + part(2), 16);
+                for (int e = 0; e < 64; ++e) {
+                    const int g = e / 16, j = e % 16;
+                    const int sh = j < 8 ? 4 * j : 4 * (j - 8) + 2;
+                    q6_store(blk, 64 * t + e, lo[e] | (int)(((hi[g] >> sh) & 3) << 4));
+                }
+            }
+            break;
+        }
+        case F16: {
+            for (int p = 0; p < 8; ++p) {
+                if (TO_LAYOUT)
+                    memcpy(dst_row + part(p), src_blocks + c * 128 + 16 * p, 16);
+                else
+                    memcpy(dst_blocks + c * 128 + 16 * p, src_row + part(p), 16);
+            }
+            break;
+        }
+        default: break;
+    }
+}
+
+int repack(int fmt, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* dst) {
     if (!shape_ok(fmt, rows, cols)) return -1;
     const FormatInfo f = format_info(fmt);
-    const RowBytes rb = row_bytes(fmt, cols);
+    const int64_t rb = row_bytes(fmt, cols);
     const int64_t nch = chunks_per_row(fmt, cols);
     const int64_t nblk = cols / f.block_values;
     const int64_t src_row = nblk * f.block_bytes;
-    for (int64_t r = 0; r < rows; ++r) {
-        const uint8_t* s = src + r * src_row;
-        uint8_t* cr = code + r * rb.code;
-        uint8_t* m0 = meta0 ? meta0 + r * rb.meta0 : nullptr;
-        uint8_t* m1 = meta1 ? meta1 + r * rb.meta1 : nullptr;
-        for (int64_t c = 0; c < nch; ++c) {
-            switch (fmt) {
-                case Q8_0: {
-                    const uint8_t* blk = s + c * 34;
-                    memcpy(m0 + c * 2, blk, 2);
-                    for (int p = 0; p < 2; ++p) {
-                        uint8_t* dst = cr + code_offset(c, p, nch, 2);
-                        for (int i = 0; i < 16; ++i) dst[i] = (uint8_t)(blk[2 + 16 * p + i] ^ 0x80);
-                    }
-                    break;
-                }
-                case Q4_0: {
-                    for (int p = 0; p < 2; ++p) {
-                        int64_t b = 2 * c + p;
-                        uint8_t* dst = cr + code_offset(c, p, nch, 2);
-                        if (b < nblk) {
-                            const uint8_t* blk = s + b * 18;
-                            memcpy(m0 + c * 4 + 2 * p, blk, 2);
-                            memcpy(dst, blk + 2, 16);
-                        } else {
-                            memset(m0 + c * 4 + 2 * p, 0, 2);
-                            memset(dst, 0, 16);
-                        }
-                    }
-                    break;
-                }
-                case Q4_K: {
-                    int64_t sb = c / 4;
-                    int p = (int)(c % 4);
-                    const uint8_t* blk = s + sb * 144;
-                    if (p == 0) memcpy(m0 + sb * 16, blk, 16);
-                    for (int h = 0; h < 2; ++h) memcpy(cr + code_offset(c, h, nch, 2), blk + 16 + 32 * p + 16 * h, 16);
-                    break;
-                }
-                case Q6_K: {
-                    int64_t sb = c / 4;
-                    int t = (int)(c % 4);
-                    const uint8_t* blk = s + sb * 210;
-                    if (t == 0) {
-                        memcpy(m0 + sb * 16, blk + 192, 16);
-                        memcpy(m1 + sb * 2, blk + 208, 2);
-                    }
-                    uint32_t lo[8], hi[4];
-                    for (int g = 0; g < 4; ++g) {
-                        uint8_t q[16];
-                        for (int e = 0; e < 16; ++e) q[e] = q6_code(blk, 64 * t + 16 * g + e);
-                        q6k_pack_group(q, lo[2 * g], lo[2 * g + 1], hi[g]);
-                    }
-                    memcpy(cr + code_offset(c, 0, nch, 3), lo, 16);
-                    memcpy(cr + code_offset(c, 1, nch, 3), lo + 4, 16);
-                    memcpy(cr + code_offset(c, 2, nch, 3), hi, 16);
-                    break;
-                }
-                case F16: {
-                    for (int p = 0; p < 8; ++p) memcpy(cr + code_offset(c, p, nch, 8), s + c * 128 + 16 * p, 16);
-                    break;
-                }
-                default: return -1;
-            }
-        }
-    }
+    memset(dst, 0, (size_t)(rows * rb));
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < nch; ++c)
+            chunk_copy<true>(fmt, src + r * src_row, nullptr, nullptr, dst + r * rb, c, nch, nblk);
     return 0;
 }
 
-int unpack(int fmt, int64_t rows, int64_t cols, const uint8_t* code, const uint8_t* meta0, const uint8_t* meta1,
-           uint8_t* dst) {
+int unpack(int fmt, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* dst) {
     if (!shape_ok(fmt, rows, cols)) return -1;
     const FormatInfo f = format_info(fmt);
-    const RowBytes rb = row_bytes(fmt, cols);
+    const int64_t rb = row_bytes(fmt, cols);
     const int64_t nch = chunks_per_row(fmt, cols);
     const int64_t nblk = cols / f.block_values;
     const int64_t dst_row = nblk * f.block_bytes;
-    for (int64_t r = 0; r < rows; ++r) {
-        uint8_t* d = dst + r * dst_row;
-        const uint8_t* cr = code + r * rb.code;
-        const uint8_t* m0 = meta0 ? meta0 + r * rb.meta0 : nullptr;
-        const uint8_t* m1 = meta1 ? meta1 + r * rb.meta1 : nullptr;
-        for (int64_t c = 0; c < nch; ++c) {
-            switch (fmt) {
-                case Q8_0: {
-                    uint8_t* blk = d + c * 34;
-                    memcpy(blk, m0 + c * 2, 2);
-                    for (int p = 0; p < 2; ++p) {
-                        const uint8_t* src = cr + code_offset(c, p, nch, 2);
-                        for (int i = 0; i < 16; ++i) blk[2 + 16 * p + i] = (uint8_t)(src[i] ^ 0x80);
-                    }
-                    break;
-                }
-                case Q4_0: {
-                    for (int p = 0; p < 2; ++p) {
-                        int64_t b = 2 * c + p;
-                        if (b >= nblk) continue;
-                        uint8_t* blk = d + b * 18;
-                        memcpy(blk, m0 + c * 4 + 2 * p, 2);
-                        memcpy(blk + 2, cr + code_offset(c, p, nch, 2), 16);
-                    }
-                    break;
-                }
-                case Q4_K: {
-                    int64_t sb = c / 4;
-                    int p = (int)(c % 4);
-                    uint8_t* blk = d + sb * 144;
-                    if (p == 0) memcpy(blk, m0 + sb * 16, 16);
-                    for (int h = 0; h < 2; ++h) memcpy(blk + 16 + 32 * p + 16 * h, cr + code_offset(c, h, nch, 2), 16);
-                    break;
-                }
-                case Q6_K: {
-                    int64_t sb = c / 4;
-                    int t = (int)(c % 4);
-                    uint8_t* blk = d + sb * 210;
-                    if (t == 0) {
-                        memset(blk, 0, 192);
-                        memcpy(blk + 192, m0 + sb * 16, 16);
-                        memcpy(blk + 208, m1 + sb * 2, 2);
-                    }
-                    uint32_t lo[8], hi[4];
-                    memcpy(lo, cr + code_offset(c, 0, nch, 3), 16);
-                    memcpy(lo + 4, cr + code_offset(c, 1, nch, 3), 16);
-                    memcpy(hi, cr + code_offset(c, 2, nch, 3), 16);
-                    for (int g = 0; g < 4; ++g) {
-                        uint8_t q[16];
-                        q6k_unpack_group(lo[2 * g], lo[2 * g + 1], hi[g], q);
-                        for (int e = 0; e < 16; ++e) q6_store(blk, 64 * t + 16 * g + e, q[e]);
-                    }
-                    break;
-                }
-                case F16: {
-                    for (int p = 0; p < 8; ++p) memcpy(d + c * 128 + 16 * p, cr + code_offset(c, p, nch, 8), 16);
-                    break;
-                }
-                default: return -1;
-            }
-        }
-    }
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < nch; ++c)
+            chunk_copy<false>(fmt, nullptr, dst + r * dst_row, src + r * rb, nullptr, c, nch, nblk);
     return 0;
 }
 

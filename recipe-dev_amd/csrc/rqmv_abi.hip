@@ -13,13 +13,10 @@ struct rqmv_weight {
     int64_t rows;     // rows of one matrix (of one expert)
     int64_t cols;
     int64_t experts;  // 1 for a plain weight
-    rq::RowBytes rb;
+    int64_t row_bytes;
     int64_t nch;
     uint8_t* dev;
     size_t dev_bytes;
-    uint8_t* code;
-    uint8_t* meta0;
-    uint8_t* meta1;
     int device;
 };
 
@@ -58,12 +55,8 @@ int current_device(DeviceInfo* out) {
 
 rq::Planes planes_of(const rqmv_weight* w, int64_t first_row) {
     rq::Planes P;
-    P.code = w->code + first_row * w->rb.code;
-    P.meta0 = w->meta0 ? w->meta0 + first_row * w->rb.meta0 : nullptr;
-    P.meta1 = w->meta1 ? w->meta1 + first_row * w->rb.meta1 : nullptr;
-    P.row_code = w->rb.code;
-    P.row_meta0 = w->rb.meta0;
-    P.row_meta1 = w->rb.meta1;
+    P.base = w->dev + first_row * w->row_bytes;
+    P.row_bytes = w->row_bytes;
     P.nch = (int)w->nch;
     return P;
 }
@@ -84,15 +77,11 @@ int create(int format, int64_t experts, int64_t rows, int64_t cols, const void* 
     DeviceInfo info;
     int dev = current_device(&info);
     if (dev < 0) return dev;
-    const rq::RowBytes rb = rq::row_bytes(format, cols);
-    const size_t code_b = align256((size_t)(rb.code * total_rows));
-    const size_t m0_b = align256((size_t)(rb.meta0 * total_rows));
-    const size_t m1_b = align256((size_t)(rb.meta1 * total_rows));
-    std::vector<uint8_t> host(code_b + m0_b + m1_b, 0);
-    uint8_t* hc = host.data();
-    uint8_t* h0 = rb.meta0 ? hc + code_b : nullptr;
-    uint8_t* h1 = rb.meta1 ? hc + code_b + m0_b : nullptr;
-    if (rq::repack(format, total_rows, cols, static_cast<const uint8_t*>(bytes), hc, h0, h1) != 0)
+    const int64_t layout = rq::layout_bytes(format, total_rows, cols);
+    if (layout >= (int64_t(1) << 32))
+        return fail(RQMV_EINVAL, "a weight's repacked bytes must stay below 4 GiB; split the tensor");
+    std::vector<uint8_t> host((size_t)layout);
+    if (rq::repack(format, total_rows, cols, static_cast<const uint8_t*>(bytes), host.data()) != 0)
         return fail(RQMV_EINVAL, "repack failed");
     uint8_t* d = nullptr;
     hipError_t e = hipMalloc(&d, host.size());
@@ -107,13 +96,10 @@ int create(int format, int64_t experts, int64_t rows, int64_t cols, const void* 
     w->rows = rows;
     w->cols = cols;
     w->experts = experts;
-    w->rb = rb;
+    w->row_bytes = rq::row_bytes(format, cols);
     w->nch = rq::chunks_per_row(format, cols);
     w->dev = d;
     w->dev_bytes = host.size();
-    w->code = d;
-    w->meta0 = rb.meta0 ? d + code_b : nullptr;
-    w->meta1 = rb.meta1 ? d + code_b + m0_b : nullptr;
     w->device = dev;
     *out = w;
     return RQMV_OK;
@@ -137,6 +123,8 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     if (m <= 0) return fail(RQMV_EINVAL, "m must be positive");
     if (m > 1 && (ldx < w->cols || ldy < rows)) return fail(RQMV_EINVAL, "ldx < cols or ldy < rows");
     const size_t esize = xtype == RQMV_DTYPE_F16 ? 2 : 4;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || (m > 1 && ((size_t)ldx * esize) % 16 != 0))
+        return fail(RQMV_EINVAL, "x rows must start 16-byte aligned (x and ldx * element size)");
     rq::MvParams p;
     p.P = planes_of(w, first_row);
     p.rows = rows;
@@ -224,10 +212,7 @@ int rqmv_weight_unpack(const rqmv_weight* w, void* gguf_bytes, size_t nbytes) {
     std::vector<uint8_t> host(w->dev_bytes);
     hipError_t e = hipMemcpy(host.data(), w->dev, w->dev_bytes, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
-    const uint8_t* hc = host.data();
-    const uint8_t* h0 = w->meta0 ? hc + (w->meta0 - w->dev) : nullptr;
-    const uint8_t* h1 = w->meta1 ? hc + (w->meta1 - w->dev) : nullptr;
-    if (rq::unpack(w->fmt, total_rows, w->cols, hc, h0, h1, static_cast<uint8_t*>(gguf_bytes)) != 0)
+    if (rq::unpack(w->fmt, total_rows, w->cols, host.data(), static_cast<uint8_t*>(gguf_bytes)) != 0)
         return fail(RQMV_EINVAL, "unpack failed");
     return RQMV_OK;
 }
@@ -330,7 +315,7 @@ int moe_dims(const rqmv_moe_params* p, rq::MoeDims* d, const DeviceInfo& info) {
 rq::MoeBank bank_of(const rqmv_weight* w) {
     rq::MoeBank b;
     if (!w) {
-        b.P = rq::Planes{nullptr, nullptr, nullptr, 0, 0, 0, 0};
+        b.P = rq::Planes{nullptr, 0, 0};
         b.rows = 0;
         return b;
     }
@@ -364,6 +349,8 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
     if (!x_dev || !y_dev || !workspace) return fail(RQMV_EINVAL, "x, y and workspace are required");
     if (x_dtype != RQMV_DTYPE_F16 && x_dtype != RQMV_DTYPE_F32) return fail(RQMV_EINVAL, "x_dtype must be F16 or F32");
     if (workspace_bytes < rq::moe_workspace_bytes(d)) return fail(RQMV_EINVAL, "workspace too small");
+    if (reinterpret_cast<uintptr_t>(x_dev) % 16 != 0 || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(RQMV_EINVAL, "x must be 16-byte and workspace 256-byte aligned");
     for (const rqmv_weight* w : {params->gate_exps, params->up_exps, params->down_exps, params->shared_gate_inp,
                                  params->gate_shexp, params->up_shexp, params->down_shexp})
         if (w && w->device != params->router->device) return fail(RQMV_ESTATE, "moe weights live on different devices");
@@ -386,30 +373,23 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
     return RQMV_OK;
 }
 
-int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* code_bytes, size_t* meta0_bytes,
-                      size_t* meta1_bytes) {
-    if (rq::gguf_bytes(format, rows, cols) < 0 || format == rq::F32) return fail(RQMV_EINVAL, "bad format or shape");
-    const rq::RowBytes rb = rq::row_bytes(format, cols);
-    if (code_bytes) *code_bytes = (size_t)(rb.code * rows);
-    if (meta0_bytes) *meta0_bytes = (size_t)(rb.meta0 * rows);
-    if (meta1_bytes) *meta1_bytes = (size_t)(rb.meta1 * rows);
+int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* bytes) {
+    const int64_t n = rq::layout_bytes(format, rows, cols);
+    if (n < 0 || format == rq::F32) return fail(RQMV_EINVAL, "bad format or shape");
+    if (bytes) *bytes = (size_t)n;
     return RQMV_OK;
 }
 
-int rqmv_repack_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, void* code, void* meta0,
-                     void* meta1) {
-    if (!gguf_bytes || !code) return fail(RQMV_EINVAL, "NULL argument");
-    if (rq::repack(format, rows, cols, static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(code),
-                   static_cast<uint8_t*>(meta0), static_cast<uint8_t*>(meta1)) != 0)
+int rqmv_repack_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, void* out) {
+    if (!gguf_bytes || !out) return fail(RQMV_EINVAL, "NULL argument");
+    if (rq::repack(format, rows, cols, static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(out)) != 0)
         return fail(RQMV_EINVAL, "bad format or shape");
     return RQMV_OK;
 }
 
-int rqmv_unpack_host(int format, int64_t rows, int64_t cols, const void* code, const void* meta0, const void* meta1,
-                     void* gguf_bytes) {
-    if (!gguf_bytes || !code) return fail(RQMV_EINVAL, "NULL argument");
-    if (rq::unpack(format, rows, cols, static_cast<const uint8_t*>(code), static_cast<const uint8_t*>(meta0),
-                   static_cast<const uint8_t*>(meta1), static_cast<uint8_t*>(gguf_bytes)) != 0)
+int rqmv_unpack_host(int format, int64_t rows, int64_t cols, const void* in, void* gguf_bytes) {
+    if (!gguf_bytes || !in) return fail(RQMV_EINVAL, "NULL argument");
+    if (rq::unpack(format, rows, cols, static_cast<const uint8_t*>(in), static_cast<uint8_t*>(gguf_bytes)) != 0)
         return fail(RQMV_EINVAL, "bad format or shape");
     return RQMV_OK;
 }

@@ -1,98 +1,265 @@
 // Activation staging into LDS, shared by the matvec and MoE kernels.
 //
-// fp16 activations: [m][part][chunk] 16-byte units of eight halves (pairs
-// permuted a,c,b,d per run of four when the format's code words hold values
-// 4i, 4i+2 / 4i+1, 4i+3 in their two halves), then [m][sum][chunk] fp32 sums of
-// consecutive runs of CW/NS activations. fp32 activations: [m][part][chunk]
-// 16-byte units of four floats in natural order. Columns at or beyond K read
-// as zero. Lanes that take consecutive chunks read consecutive LDS addresses.
+// Quantized weights (integer kernels). Each 32-value block b of an activation
+// row becomes 16-bit integers x = rint(v * 30583 / max|v|) with scale
+// s_b = max|v| / 30583. For 4-bit formats each x is split into four balanced
+// hex digits (x + 0x8888 has hex digits d_i + 8, so (x + 0x8888) ^ 0x8888 holds
+// every d_i as a signed nibble) and the digits are transposed into words of
+// eight values per digit, the weights' nibble order. For Q8_0 x is split into
+// two balanced bytes ((x + 0x8080) ^ 0x8080) and transposed into words of four.
+//   LDS: xd [m][part][chunk] 16-byte digit words (Traits::XP parts per chunk:
+//        nibble formats: part 2i + b holds digit i of the chunk's block b;
+//        Q8_0: parts 0-1 low bytes, parts 2-3 high bytes),
+//        xb [m][2][chunk] block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -),
+//        sx = s * sum x over the block (Q4_K) or the 16-value group (Q6_K).
+// F16 weights: fp16 activations as [m][part][chunk] 16-byte units of natural
+// pairs, or fp32 activations as [m][part][chunk] units of four floats.
+// Columns at or beyond K read as zero; lanes on consecutive chunks read
+// consecutive LDS addresses.
 #pragma once
 
 #include "chunk.h"
 
 namespace rq {
 
-template <int FMT>
-constexpr int xparts16() { return Traits<FMT>::CW / 8; }
-template <int FMT>
-constexpr int xparts32() { return Traits<FMT>::CW / 4; }
-template <int FMT>
-constexpr int nsums() { return Traits<FMT>::NS > 0 ? Traits<FMT>::NS : 1; }
+constexpr float kXMax = 30583.f;  // 7 * (1 + 16 + 256 + 4096): four balanced hex digits
 
+// Work item u = ((m * nch + c) * BLK + b) * 4 + q stages the eight values
+// 8q..8q+7 of block b of chunk c of row m. The four items of a block sit in an
+// aligned lane quad, which shares the block's maximum and sums through DPP.
 template <int FMT>
-__device__ __forceinline__ void stage_f16(int nch, int K, const void* xv, int64_t ldx, int M, uint4* xq, float* sums) {
-    constexpr int CW = Traits<FMT>::CW, XP = xparts16<FMT>(), NS = Traits<FMT>::NS;
+__device__ __forceinline__ int stage_items(int nch, int M) {
+    return M * nch * Traits<FMT>::BLK * 4;
+}
+
+template <bool XF32>
+struct StageItem {
+    uint4 raw[XF32 ? 2 : 1];
+};
+
+template <int FMT, bool XF32>
+__device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* xv, int64_t ldx, StageItem<XF32>& it) {
+    constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK;
+    const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
+    int k0 = c * CW + b * 32 + q * 8;
+    k0 = k0 < K ? k0 : K - 8;
+    if constexpr (XF32) {
+        const float* xm = static_cast<const float*>(xv) + (int64_t)m * ldx + k0;
+        it.raw[0] = *reinterpret_cast<const uint4*>(xm);
+        it.raw[1] = *reinterpret_cast<const uint4*>(xm + 4);
+    } else {
+        it.raw[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xv) + (int64_t)m * ldx + k0);
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_quad_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Four signed-nibble digit words (one per digit) from eight 16-bit patterns.
+__device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* out) {
+    uint32_t t[4], v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t p = (u[2 * k] & 0xffffu) | (u[2 * k + 1] << 16);
+        const uint32_t q = p & 0x0F0F0F0Fu, r = (p >> 4) & 0x0F0F0F0Fu;
+        t[k] = q | (q >> 12);  // byte 0: digit 0 pair, byte 1: digit 2 pair
+        v[k] = r | (r >> 12);  // byte 0: digit 1 pair, byte 1: digit 3 pair
+    }
+    const uint32_t A = __builtin_amdgcn_perm(t[1], t[0], 0x05040100u), B = __builtin_amdgcn_perm(t[3], t[2], 0x05040100u);
+    const uint32_t C = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u), D = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+    out[0] = __builtin_amdgcn_perm(B, A, 0x06040200u);
+    out[2] = __builtin_amdgcn_perm(B, A, 0x07050301u);
+    out[1] = __builtin_amdgcn_perm(D, C, 0x06040200u);
+    out[3] = __builtin_amdgcn_perm(D, C, 0x07050301u);
+}
+
+// Encodes item u and stores it into LDS. Every lane of the item's quad must
+// run it together (the block maximum and sums move through DPP).
+template <int FMT, bool XF32>
+__device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageItem<XF32>& it, uint4* xd, float* xbf) {
+    constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP;
+    const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
+    const bool live = c * CW + b * 32 < K;
+    float v[8];
+    if constexpr (XF32) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            v[t] = __builtin_bit_cast(float, word(it.raw[0], t));
+            v[4 + t] = __builtin_bit_cast(float, word(it.raw[1], t));
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = half_lo(word(it.raw[0], e));
+            v[2 * e + 1] = half_hi(word(it.raw[0], e));
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    amax = fmaxf(amax, dpp_quad_f32<0xB1>(amax));  // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_quad_f32<0x4E>(amax));  // quad_perm [2,3,0,1]
+    if (!live) amax = 0.f;
+    const float inv = amax > 0.f ? kXMax / amax : 0.f;
+    const float s = amax * (1.0f / kXMax);
+    int xi[8];
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int t = (int)__builtin_rintf(v[k] * inv);
+        xi[k] = t < -30583 ? -30583 : (t > 30583 ? 30583 : t);
+        sum += xi[k];
+    }
+    uint32_t* xdw = reinterpret_cast<uint32_t*>(xd);
+    if constexpr (FMT == Q8_0) {
+        uint32_t lo[2], hi[2];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            uint32_t uu[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) uu[e] = ((uint32_t)(xi[4 * w + e] + 0x8080) ^ 0x8080u) & 0xffffu;
+            const uint32_t pa = uu[0] | (uu[1] << 16), pb = uu[2] | (uu[3] << 16);
+            lo[w] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
+            hi[w] = __builtin_amdgcn_perm(pb, pa, 0x07050301u);
+        }
+        // low-byte words 2q, 2q+1 in parts 0-1, high-byte words in parts 2-3
+        const int part = q >> 1, comp = (q & 1) * 2;
+        uint32_t* lo_at = xdw + ((m * XP + part) * nch + c) * 4 + comp;
+        uint32_t* hi_at = xdw + ((m * XP + 2 + part) * nch + c) * 4 + comp;
+        lo_at[0] = lo[0];
+        lo_at[1] = lo[1];
+        hi_at[0] = hi[0];
+        hi_at[1] = hi[1];
+    } else {
+        uint32_t uu[8], o[4];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) uu[e] = (uint32_t)(xi[e] + 0x8888) ^ 0x8888u;
+        nibble_transpose(uu, o);
+        // digit i, word 4b + q of the chunk: part 2i + b, component q
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xdw[((m * XP + 2 * i + b) * nch + c) * 4 + q] = o[i];
+    }
+    // block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -)
+    const int pair = sum + dpp_i32<0xB1>(sum);   // this half block (16 values)
+    const int whole = pair + dpp_i32<0x4E>(pair);  // the block
+    float* b0 = xbf + ((m * 2 + 0) * nch + c) * 4;
+    float* b1 = xbf + ((m * 2 + 1) * nch + c) * 4;
+    if (q == 0) b0[b] = s;
+    if constexpr (FMT == Q4_K) {
+        if (q == 0) b0[2 + b] = s * (float)whole;
+    } else if constexpr (FMT == Q6_K) {
+        if ((q & 1) == 0) {  // groups 2b (q = 0) and 2b + 1 (q = 2)
+            const int g = 2 * b + (q >> 1);
+            const float sx = s * (float)pair;
+            if (g < 2) b0[2 + g] = sx; else b1[g - 2] = sx;
+        }
+    }
+}
+
+// Staging with up to NJ items per thread: all activation loads are issued
+// before the caller's weight loads (stage_multi_issue), encoded afterwards
+// (stage_multi_finish).
+constexpr int kStageNJ = 4;
+
+template <int FMT, bool XF32>
+__device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x, int64_t ldx, int M,
+                                                  StageItem<XF32> (&it)[kStageNJ]) {
+    const int total = stage_items<FMT>(nch, M);
+#pragma unroll
+    for (int j = 0; j < kStageNJ; ++j) {
+        const int u = (int)threadIdx.x + j * (int)blockDim.x;
+        stage_issue<FMT, XF32>(u < total ? u : (int)threadIdx.x % 4, nch, K, x, ldx, it[j]);
+    }
+}
+
+template <int FMT, bool XF32>
+__device__ __forceinline__ void stage_multi_finish(int nch, int K, int M, const StageItem<XF32> (&it)[kStageNJ],
+                                                   uint4* xd, float* xbf) {
+    const int total = stage_items<FMT>(nch, M);
+#pragma unroll
+    for (int j = 0; j < kStageNJ; ++j) {
+        const int u = (int)threadIdx.x + j * (int)blockDim.x;
+        if (u < total) stage_finish<FMT, XF32>(u, nch, K, it[j], xd, xbf);
+    }
+}
+
+// Plain loop (used when a block has more items than kStageNJ per thread).
+template <int FMT, bool XF32>
+__device__ __forceinline__ void stage_all(int nch, int K, const void* x, int64_t ldx, int M, uint4* xd, float* xbf) {
+    const int total = stage_items<FMT>(nch, M);
+    for (int u = threadIdx.x; u < total; u += blockDim.x) {
+        StageItem<XF32> it;
+        stage_issue<FMT, XF32>(u, nch, K, x, ldx, it);
+        stage_finish<FMT, XF32>(u, nch, K, it, xd, xbf);
+    }
+}
+
+// LDS bytes of a staged activation block for the integer kernels.
+__host__ __device__ inline size_t stage_bytes_int(int fmt, int M, int nch) {
+    const int xp = fmt == Q8_0 ? 4 : 8;
+    return (size_t)M * nch * (size_t)(xp + 2) * 16;
+}
+
+// F16 weights: fp16 activations as natural pairs, or fp32 activations.
+__device__ __forceinline__ void stage_f16_pairs(int nch, int K, const void* xv, int64_t ldx, int M, uint4* xq) {
     const uint16_t* x = static_cast<const uint16_t*>(xv);
-    const int total = M * XP * nch;
+    const int total = M * 8 * nch;
     for (int u = threadIdx.x; u < total; u += blockDim.x) {
-        const int c = u % nch, mj = u / nch, j = mj % XP, m = mj / XP;
-        const int k0 = c * CW + j * 8;
-        const uint16_t* xm = x + (int64_t)m * ldx;
-        uint32_t h[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) h[t] = (k0 + t < K) ? xm[k0 + t] : 0u;
-        uint4 v;
-        if constexpr (Traits<FMT>::PERM4) {
-            v = make_uint4(h[0] | (h[2] << 16), h[1] | (h[3] << 16), h[4] | (h[6] << 16), h[5] | (h[7] << 16));
-        } else {
-            v = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-        }
-        xq[u] = v;
-    }
-    if constexpr (NS > 0) {
-        constexpr int GS = CW / NS;
-        const int ts = M * NS * nch;
-        for (int u = threadIdx.x; u < ts; u += blockDim.x) {
-            const int c = u % nch, ms = u / nch, s = ms % NS, m = ms / NS;
-            const int k0 = c * CW + s * GS;
-            const uint16_t* xm = x + (int64_t)m * ldx;
-            float acc = 0.f;
-            for (int t = 0; t < GS; ++t)
-                if (k0 + t < K) acc += (float)__builtin_bit_cast(_Float16, xm[k0 + t]);
-            sums[u] = acc;
-        }
+        const int c = u % nch, mj = u / nch, j = mj % 8, m = mj / 8;
+        const int k0 = c * 64 + j * 8;
+        xq[u] = k0 < K ? *reinterpret_cast<const uint4*>(x + (int64_t)m * ldx + k0) : make_uint4(0, 0, 0, 0);
     }
 }
 
-template <int FMT>
-__device__ __forceinline__ void stage_f32(int nch, int K, const void* xv, int64_t ldx, int M, float4* xf) {
-    constexpr int CW = Traits<FMT>::CW, XP = xparts32<FMT>();
+__device__ __forceinline__ void stage_f32_quads(int nch, int K, const void* xv, int64_t ldx, int M, float4* xf) {
     const float* x = static_cast<const float*>(xv);
-    const int total = M * XP * nch;
+    const int total = M * 16 * nch;
     for (int u = threadIdx.x; u < total; u += blockDim.x) {
-        const int c = u % nch, mj = u / nch, j = mj % XP, m = mj / XP;
-        const int k0 = c * CW + j * 4;
-        const float* xm = x + (int64_t)m * ldx;
-        float v[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = (k0 + t < K) ? xm[k0 + t] : 0.f;
-        xf[u] = make_float4(v[0], v[1], v[2], v[3]);
+        const int c = u % nch, mj = u / nch, j = mj % 16, m = mj / 16;
+        const int k0 = c * 64 + j * 4;
+        xf[u] = k0 < K ? *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
-// LDS bytes of a staged activation block.
-__host__ __device__ inline size_t stage_bytes(int fmt, int xtype_f32, int M, int nch) {
-    FormatInfo f = format_info(fmt);
-    if (xtype_f32) return (size_t)M * nch * (size_t)(f.chunk_values / 4) * 16;
-    return (size_t)M * nch * ((size_t)(f.chunk_values / 8) * 16 + (size_t)(f.sums > 0 ? f.sums : 0) * 4);
+__host__ __device__ inline size_t stage_bytes_f16w(int xtype_f32, int M, int nch) {
+    return (size_t)M * nch * (xtype_f32 ? 16 : 8) * 16;
 }
 
+// DPP lane moves (VALU modifiers, no LDS traffic). Lanes outside row_mask
+// read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the G lanes of each aligned lane group (G = 8, 16, 32 or 64); the
+// total lands in the group's last lane (g == G - 1; for G <= 16 in every lane).
+// quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror, then
+// row_bcast:15 (rows 1, 3) and row_bcast:31 (rows 2, 3).
 __device__ __forceinline__ float group_sum(float v, int G) {
-    for (int off = G >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    v += dpp_f32<0xB1, 0xf>(v);
+    v += dpp_f32<0x4E, 0xf>(v);
+    v += dpp_f32<0x141, 0xf>(v);
+    if (G >= 16) v += dpp_f32<0x140, 0xf>(v);
+    if (G >= 32) v += dpp_f32<0x142, 0xa>(v);
+    if (G >= 64) v += dpp_f32<0x143, 0xc>(v);
     return v;
 }
 
-// Dot of one chunk against staged fp32 activations (exact weights, fma): chunk
-// `c` of its weight row, whose activations sit at staged chunk `cx`.
-template <int FMT>
-__device__ __forceinline__ float chunk_dot_f32(const ChunkData<FMT>& d, int c, const float4* xf, int nch, int cx, int m) {
-    constexpr int CW = Traits<FMT>::CW, XP = xparts32<FMT>();
-    float w[CW];
-    decode_chunk<FMT>(d, c, w);
+// Dot of one F16-weight chunk against staged fp32 activations (exact products).
+__device__ __forceinline__ float chunk_dot_f32(const ChunkData<F16>& d, const float4* xf, int nch, int c, int m) {
+    float w[64];
+    decode_chunk<F16>(d, c, w);
     float a = 0.f;
 #pragma unroll
-    for (int j = 0; j < XP; ++j) {
-        const float4 xv = xf[(m * XP + j) * nch + cx];
+    for (int j = 0; j < 16; ++j) {
+        const float4 xv = xf[(m * 16 + j) * nch + c];
         a = fmaf(w[4 * j], xv.x, a);
         a = fmaf(w[4 * j + 1], xv.y, a);
         a = fmaf(w[4 * j + 2], xv.z, a);

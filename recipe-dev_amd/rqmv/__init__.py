@@ -56,9 +56,9 @@ class _Lib:
         L.rqmv_expert_matvec.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p]
         L.rqmv_moe_workspace_size.argtypes = [c_void_p, POINTER(c_size_t)]
         L.rqmv_moe.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
-        L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t), POINTER(c_size_t), POINTER(c_size_t)]
-        L.rqmv_repack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
-        L.rqmv_unpack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t)]
+        L.rqmv_repack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
+        L.rqmv_unpack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
         H.hipMalloc.argtypes = [POINTER(c_void_p), c_size_t]
         H.hipFree.argtypes = [c_void_p]
         H.hipMemcpy.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
@@ -363,26 +363,22 @@ class Moe:
         return yb.download(np.float32), rb.download(np.float32)
 
 
-def layout_bytes(fmt, rows: int, cols: int):
-    a, b, c = c_size_t(), c_size_t(), c_size_t()
-    _check(lib().lib.rqmv_layout_bytes(_fmt(fmt), rows, cols, byref(a), byref(b), byref(c)), "rqmv_layout_bytes")
-    return a.value, b.value, c.value
+def layout_bytes(fmt, rows: int, cols: int) -> int:
+    n = c_size_t()
+    _check(lib().lib.rqmv_layout_bytes(_fmt(fmt), rows, cols, byref(n)), "rqmv_layout_bytes")
+    return n.value
 
 
-def repack_host(fmt, rows: int, cols: int, gguf: np.ndarray):
-    code_n, m0_n, m1_n = layout_bytes(fmt, rows, cols)
-    code = np.zeros(code_n, np.uint8)
-    m0 = np.zeros(max(m0_n, 1), np.uint8)
-    m1 = np.zeros(max(m1_n, 1), np.uint8)
+def repack_host(fmt, rows: int, cols: int, gguf: np.ndarray) -> np.ndarray:
+    """GGUF bytes -> the kernels' repacked layout, on the host."""
+    out = np.zeros(layout_bytes(fmt, rows, cols), np.uint8)
     g = np.ascontiguousarray(gguf, dtype=np.uint8)
-    _check(lib().lib.rqmv_repack_host(_fmt(fmt), rows, cols, g.ctypes.data, code.ctypes.data,
-                                      m0.ctypes.data if m0_n else None, m1.ctypes.data if m1_n else None),
-           "rqmv_repack_host")
-    return code, m0[:m0_n], m1[:m1_n]
+    _check(lib().lib.rqmv_repack_host(_fmt(fmt), rows, cols, g.ctypes.data, out.ctypes.data), "rqmv_repack_host")
+    return out
 
 
-def unpack_host(fmt, rows: int, cols: int, code, m0, m1, nbytes: int) -> np.ndarray:
+def unpack_host(fmt, rows: int, cols: int, packed: np.ndarray, nbytes: int) -> np.ndarray:
     out = np.zeros(nbytes, np.uint8)
-    _check(lib().lib.rqmv_unpack_host(_fmt(fmt), rows, cols, code.ctypes.data, m0.ctypes.data if m0.size else None,
-                                      m1.ctypes.data if m1.size else None, out.ctypes.data), "rqmv_unpack_host")
+    pk = np.ascontiguousarray(packed, dtype=np.uint8)
+    _check(lib().lib.rqmv_unpack_host(_fmt(fmt), rows, cols, pk.ctypes.data, out.ctypes.data), "rqmv_unpack_host")
     return out

@@ -38,46 +38,63 @@ def _shapes(fmt):
 def test_host_repack_round_trip(fmt):
     for rows, cols in _shapes(fmt):
         w = synth.weights(fmt, rows, cols, seed=rows + cols)
-        code, m0, m1 = rqmv.repack_host(fmt, rows, cols, w)
-        back = rqmv.unpack_host(fmt, rows, cols, code, m0, m1, w.nbytes)
+        packed = rqmv.repack_host(fmt, rows, cols, w)
+        back = rqmv.unpack_host(fmt, rows, cols, packed, w.nbytes)
         assert np.array_equal(back, w), (fmt, rows, cols)
 
 
 def test_host_repack_f16_round_trip():
     rows, cols = 7, 2048
     w = synth.f16_weights(rows, cols, 0.02, seed=1)
-    code, m0, m1 = rqmv.repack_host("f16", rows, cols, w)
-    assert m0.size == 0 and m1.size == 0
-    assert np.array_equal(rqmv.unpack_host("f16", rows, cols, code, m0, m1, w.nbytes), w)
+    packed = rqmv.repack_host("f16", rows, cols, w)
+    assert packed.nbytes == w.nbytes
+    assert np.array_equal(rqmv.unpack_host("f16", rows, cols, packed, w.nbytes), w)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_layout_carries_gguf_bytes_without_padding(fmt):
-    """The repacked planes hold exactly the GGUF bytes (Q4_0 pads an odd block)."""
+def test_layout_carries_gguf_bytes(fmt):
+    """The repacked rows hold exactly the GGUF bytes when rows are whole 16-byte
+    multiples; otherwise only row padding is added."""
     rows, cols = 9, 4096
-    code, m0, m1 = rqmv.layout_bytes(fmt, rows, cols)
-    assert code + m0 + m1 == synth.gguf_bytes(fmt, rows, cols)
+    assert rqmv.layout_bytes(fmt, rows, cols) == synth.gguf_bytes(fmt, rows, cols)
+    rows, cols = 5, 96 if fmt in ("q8_0", "q4_0") else 768
+    extra = rqmv.layout_bytes(fmt, rows, cols) - synth.gguf_bytes(fmt, rows, cols)
+    assert 0 <= extra <= rows * (16 + 18)
+
+
+def _nibbles(b16):
+    """32 four-bit codes in natural order from 16 packed bytes (each XOR 8)."""
+    b = np.asarray(b16, np.uint8)
+    out = np.empty(32, np.int64)
+    out[0::2] = (b & 15) ^ 8
+    out[1::2] = (b >> 4) ^ 8
+    return out
 
 
 def test_layout_parts_are_contiguous_per_wave():
-    """Part p of 64 consecutive chunks forms one contiguous 1 KiB run."""
+    """Part h of 64 consecutive chunks forms one contiguous 1 KiB run; part h of
+    Q4_K chunk c holds sub-block 2(c % 4) + h's codes in order."""
     rows, cols = 1, 4096  # Q4_K: 64 chunks of 64 weights, 2 parts each
     w = synth.q4_k(rows, cols, seed=5)
-    code, m0, _ = rqmv.repack_host("q4_k", rows, cols, w)
+    code = rqmv.repack_host("q4_k", rows, cols, w)
     blk = w.reshape(16, 144)
     for c in range(64):
         sb, p = divmod(c, 4)
         for h in range(2):
-            got = code[(h * 64 + c) * 16:(h * 64 + c) * 16 + 16]
-            assert np.array_equal(got, blk[sb, 16 + 32 * p + 16 * h:16 + 32 * p + 16 * h + 16])
-    assert np.array_equal(m0.reshape(16, 16), blk[:, :16])
+            got = _nibbles(code[(h * 64 + c) * 16:(h * 64 + c) * 16 + 16])
+            want = (blk[sb, 16 + 32 * p:16 + 32 * p + 32].astype(np.int64) >> (4 * h)) & 15
+            assert np.array_equal(got, want), (c, h)
+    # the group's scale bytes follow its two code parts
+    assert np.array_equal(code[2048:2304].reshape(16, 16), blk[:, :16])
 
 
-def test_q6k_group_packing_decodes_each_code():
-    """Every 6-bit code lands where the kernels' mask-and-or reads it back."""
+def test_q6k_layout_decodes_each_code():
+    """Every 6-bit code is its low nibble (parts 0-1) plus 16 times its high
+    field (part 2, expanded by H & 0x33333333 and (H >> 2) & 0x33333333)."""
     rows, cols = 1, 256
     w = synth.q6_k(rows, cols, seed=9)
-    code, _, _ = rqmv.repack_host("q6_k", rows, cols, w)
+    code = rqmv.repack_host("q6_k", rows, cols, w)
+    assert np.array_equal(code[192:208], w[192:208]) and np.array_equal(code[208:210], w[208:210])
     blk = w.reshape(210)
     ql, qh = blk[:128].astype(np.int64), blk[128:192].astype(np.int64)
 
@@ -88,26 +105,16 @@ def test_q6k_group_packing_decodes_each_code():
         hi = (qh[32 * ch + j] >> (2 * g)) & 3
         return lo | (hi << 4)
 
-    def rotr(v, s):
-        return ((v >> s) | (v << (32 - s))) & 0xFFFFFFFF
-
-    for c in range(4):
-        words = [int(v) for v in code[c * 16:(c + 1) * 16].view(np.uint32)]  # part 0 (one 64-chunk group)
-        words += [int(v) for v in code[(4 + c) * 16:(4 + c + 1) * 16].view(np.uint32)]  # part 1
-        H = [int(v) for v in code[(8 + c) * 16:(8 + c + 1) * 16].view(np.uint32)]  # part 2
+    for c in range(4):  # one 64-chunk group of 4 chunks: part p of chunk c at (p * 4 + c) * 16
+        lo = np.concatenate([_nibbles(code[(0 * 4 + c) * 16:(0 * 4 + c + 1) * 16]),
+                             _nibbles(code[(1 * 4 + c) * 16:(1 * 4 + c + 1) * 16])])
+        H = code[(2 * 4 + c) * 16:(2 * 4 + c + 1) * 16].view(np.uint32).astype(np.int64)
         for g in range(4):
-            A, B, h = words[2 * g], words[2 * g + 1], H[g]
-            pairs = [
-                (A & 0x000F000F) | (h & 0x00300030), ((A >> 8) & 0x000F000F) | ((h >> 2) & 0x00300030),
-                (B & 0x000F000F) | (rotr(h, 8) & 0x00300030), ((B >> 8) & 0x000F000F) | (rotr(h, 10) & 0x00300030),
-                (A & 0x00F000F0) | (h & 0x03000300), ((A >> 8) & 0x00F000F0) | ((h >> 2) & 0x03000300),
-                (B & 0x00F000F0) | (rotr(h, 8) & 0x03000300), ((B >> 8) & 0x00F000F0) | (rotr(h, 10) & 0x03000300)]
-            for j, v in enumerate(pairs):
-                lo, hi = v & 0xFFFF, v >> 16
-                if j >= 4:
-                    lo, hi = lo // 16, hi // 16
-                e = 64 * c + 16 * g + 2 * j
-                assert (lo, hi) == (q_of(e), q_of(e + 1)), (c, g, j)
+            he, ho = H[g] & 0x33333333, (H[g] >> 2) & 0x33333333
+            for j in range(16):
+                h = ((he >> (4 * j)) & 15) if j < 8 else ((ho >> (4 * (j - 8))) & 15)
+                e = 16 * g + j
+                assert lo[e] + 16 * h == q_of(64 * c + e), (c, g, j)
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 4, 100), ("q8_0", 2, 31), ("q6_k", 0, 256), (99, 2, 256)])

@@ -115,8 +115,11 @@ def test_matvec_parity(gpu, fmt, xdt, m):
         ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
         err = rel_l2(y, ref)
         assert err <= REL_L2, (fmt, xdt, m, rows, cols, err)
-        if xdt == "f32":  # exact weights and fp32 fma: far inside the bar
-            assert err <= 1e-5, (fmt, m, rows, cols, err)
+        # Quantized weights dot 16-bit integer activations (per-32 block scale),
+        # F16 weights dot the activations unrounded: both far inside the bar.
+        # (a single short row has few terms to average its rounding over)
+        limit = 1e-5 if fmt == "f16" and xdt == "f32" else (5e-4 if rows * cols < 4096 else 2e-4)
+        assert err <= limit, (fmt, xdt, m, rows, cols, err)
 
 
 def test_matvec_is_deterministic(gpu):
