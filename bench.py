@@ -83,6 +83,22 @@ def cpu_baseline(fmt, rows, cols, x32, seconds, weights_bytes, alg_bytes):
                       f"{per * 1e3:.2f} ms each, fp32 recipe-order restatement, {cores} threads"}
 
 
+def copy_calibration(mb, steps):
+    """A plain copy of known size, so that rocprofv3's FETCH_SIZE / WRITE_SIZE
+    per dispatch can be converted to bytes (factor = known bytes / counter)."""
+    import torch
+
+    n = mb * 2 ** 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    src.fill_(7)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "steps": steps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,11 +110,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MB per step (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs the matvec on a "
               f"single MI355X; rows would shard across GPUs with no collective on the hot path)", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_mb:
+        copy_calibration(args.copy_mb, args.steps)
+        return
 
     import rqmv
     from rqmv import synth
