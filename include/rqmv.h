@@ -5,8 +5,7 @@
  * tensors to projections by name and lowers each to a Contraction (or
  * ExpertIn/ExpertOut/TopK) node whose packed StoredWeight its device code reads
  * (recipe.rs:4532-4832); this library takes over those nodes' storage and
- * arithmetic for batch 1 and small M. A Rust FFI binding of these entry points
- * is shown in INTEGRATION.md.
+ * arithmetic for batch 1 and small M.
  *
  * Conventions
  *   - Every entry point returns 0 on success and a negative RQMV_E* code on

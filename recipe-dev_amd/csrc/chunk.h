@@ -79,8 +79,13 @@ template <int FMT> struct ChunkData {
 struct Planes {
     const uint8_t* base;
     int64_t row_bytes;
-    int nch;  // chunks per row
+    int nch;         // chunks per row
+    uint32_t bytes;  // bytes readable from base (buffer loads past them return zeros)
 };
+
+// Offset that every buffer load treats as out of range: such a load returns
+// zeros and touches no memory. Weights are kept below it (the loader checks).
+constexpr uint32_t kOobOffset = 0xFFFFFF00u;
 
 // Bytes of a full 64-chunk group (layout.h group_bytes(64)).
 template <int FMT>
@@ -118,6 +123,46 @@ __device__ __forceinline__ void load_chunk(const Planes& P, int64_t row, int c, 
         d.meta = make_uint4(*reinterpret_cast<const uint32_t*>(P.base + (meta + within * 4u)), 0, 0, 0);
     } else if constexpr (FMT == Q8_0) {
         d.meta = make_uint4(*reinterpret_cast<const uint16_t*>(P.base + (meta + within * 2u)), 0, 0, 0);
+    } else {
+        d.meta = make_uint4(0, 0, 0, 0);
+    }
+}
+
+// Buffer resource over a weight's bytes: raw (stride 0) addressing with
+// 32-bit data format, so a dword load at or past `bytes` returns zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t planes_rsrc(const Planes& P) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.base), (short)0, (int)P.bytes, 0x00020000);
+}
+
+// load_chunk through a buffer resource. A lane with `valid` false loads from
+// kOobOffset: zeros, no memory traffic, and the same instruction count as
+// every other lane, so the waits on earlier loads stay exact.
+template <int FMT>
+__device__ __forceinline__ void load_chunk_rs(__amdgpu_buffer_rsrc_t rs, const Planes& P, uint32_t row, int c, bool valid,
+                                              ChunkData<FMT>& d) {
+    constexpr int QP = Traits<FMT>::QP;
+    const uint32_t group = (uint32_t)c >> 6, within = (uint32_t)c & 63u;
+    const uint32_t rest = (uint32_t)P.nch - (group << 6);
+    const uint32_t nb = rest > 64u ? 64u : rest;
+    const uint32_t gb = row * (uint32_t)P.row_bytes + group * full_group_bytes<FMT>();
+    auto at = [&](uint32_t off) { return valid ? off : kOobOffset; };
+#pragma unroll
+    for (int h = 0; h < QP; ++h) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, at(gb + ((uint32_t)h * nb + within) * 16u), 0, 0);
+        d.q[h] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    const uint32_t meta = gb + (uint32_t)QP * nb * 16u;
+    if constexpr (FMT == Q4_K) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, at(meta + (within >> 2) * 16u), 0, 0);
+        d.meta = make_uint4(v.x, v.y, v.z, v.w);
+    } else if constexpr (FMT == Q6_K) {
+        const uint32_t sc = __builtin_amdgcn_raw_buffer_load_b32(rs, at(meta + (within >> 2) * 16u + (within & 3u) * 4u), 0, 0);
+        const uint32_t dd = __builtin_amdgcn_raw_buffer_load_b16(rs, at(meta + (nb >> 2) * 16u + (within >> 2) * 2u), 0, 0);
+        d.meta = make_uint4(sc, dd, 0, 0);
+    } else if constexpr (FMT == Q4_0) {
+        d.meta = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(rs, at(meta + within * 4u), 0, 0), 0, 0, 0);
+    } else if constexpr (FMT == Q8_0) {
+        d.meta = make_uint4(__builtin_amdgcn_raw_buffer_load_b16(rs, at(meta + within * 2u), 0, 0), 0, 0, 0);
     } else {
         d.meta = make_uint4(0, 0, 0, 0);
     }

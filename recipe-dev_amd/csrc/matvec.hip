@@ -3,10 +3,12 @@
 // Work mapping. A wave's 64 lanes are split into 64/G groups of G lanes; a
 // group owns R consecutive rows and its lanes take chunks g, g+G, g+2G, ...
 // of those rows, so every load instruction of the wave reads contiguous 16-byte
-// parts of the code plane (layout.h). Each lane keeps R x M fp32 partial sums;
-// the G lanes of a group are reduced with cross-lane xor shuffles (no atomics,
-// no scratch) and the first lane writes the rows. Waves stride over row tiles,
-// so a fixed, occupancy-sized grid covers any row count.
+// parts of a row (layout.h). Weights are read with buffer loads whose
+// out-of-range form returns zeros without touching memory, so every lane
+// issues the same loads and the waits stay exact. Each lane keeps R x M fp32
+// partial sums; the G lanes of a group are reduced with DPP row operations (no
+// atomics, no scratch) and the group's last lane writes the rows. Waves stride
+// over row tiles, so a fixed, occupancy-sized grid covers any row count.
 //
 // Activations are staged once per workgroup into LDS as 16-bit integer digit
 // words per 32-value block (stage.h), in a part-major layout ([m][part][chunk]
@@ -92,10 +94,50 @@ __device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int
         for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
 }
 
+// load_rows through the weight's buffer resource: lanes whose row, chunk or
+// tile lies past the end (and every lane of a step past the wave's last)
+// load nothing and get zeros.
+template <int FMT, int R>
+__device__ __forceinline__ void load_rows_rs(const MvParams& p, __amdgpu_buffer_rsrc_t rs, const StepWalk& w, int sub,
+                                             ChunkData<FMT> (&d)[R]) {
+    const bool live = w.tile < w.tiles && w.chunk() < w.nch;
+    const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) load_chunk_rs<FMT>(rs, p.P, (uint32_t)(row0 + r), w.chunk(), live && row0 + r < p.rows, d[r]);
+}
+
+// One step of matvec_int: the lane's chunk of its R rows against the staged
+// digits of every activation row; the tile's reduction after its last step.
+template <int FMT, int M, int R>
+__device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, int sub, int g, const ChunkData<FMT> (&d)[R],
+                                         float (&acc)[R][M], const uint4* xd, const uint4* xb) {
+    constexpr int XP = Traits<FMT>::XP;
+    const int nch = p.P.nch;
+    const int c = w.chunk();
+    const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+    if (c < nch) {
+        // one activation row's digits live at a time; the weights stay in registers
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            uint4 xv[1][XP];
+            uint4 bv[1][2];
+#pragma unroll
+            for (int j = 0; j < XP; ++j) xv[0][j] = xd[(mm * XP + j) * nch + c];
+            bv[0][0] = xb[(mm * 2 + 0) * nch + c];
+            bv[0][1] = xb[(mm * 2 + 1) * nch + c];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row0 + r < p.rows) dot_int<FMT, 1>(d[r], c, xv, bv, &acc[r][mm]);
+        }
+    }
+    if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
+}
+
 // Quantized weights, integer dot of staged activation digits (chunk.h,
-// stage.h). Each wave loads one step's chunks and computes them; the waves
-// resident on a CU keep the memory system busy between them. The first
-// step's weight loads are issued before the activations are staged.
+// stage.h). Two register buffers alternate: while one step is computed, the
+// loads of the next are in flight, and the buffer just computed is refilled
+// for the step after that. The first two steps' weight loads are issued
+// before the activations are staged.
 template <int FMT, int M, int R, bool XF32>
 __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     constexpr int XP = Traits<FMT>::XP;
@@ -104,9 +146,12 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     uint4* xd = smem;
     uint4* xb = smem + M * XP * nch;
     const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane / p.G;
-    StepWalk w = make_walk(p, R, g);
+    const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
+    StepWalk wa = make_walk(p, R, g);
+    StepWalk wb = wa;
+    wb.next();
 
-    ChunkData<FMT> cur[R];
+    ChunkData<FMT> A[R], B[R];
     if (stage_items<FMT>(nch, M) <= kStageNJ * (int)blockDim.x) {
         StageItem<XF32> it[kStageNJ];
         stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, M, it);
@@ -114,10 +159,12 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
         // then leaves the weight loads in flight
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
-        load_rows<FMT, R>(p, w, sub, cur);
+        load_rows_rs<FMT, R>(p, rs, wa, sub, A);
+        load_rows_rs<FMT, R>(p, rs, wb, sub, B);
         stage_multi_finish<FMT, XF32>(nch, p.K, M, it, xd, reinterpret_cast<float*>(xb));
     } else {
-        load_rows<FMT, R>(p, w, sub, cur);
+        load_rows_rs<FMT, R>(p, rs, wa, sub, A);
+        load_rows_rs<FMT, R>(p, rs, wb, sub, B);
         stage_all<FMT, XF32>(nch, p.K, p.x, p.ldx, M, xd, reinterpret_cast<float*>(xb));
     }
     __syncthreads();
@@ -127,29 +174,16 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
-    bool loaded = true;
-    while (w.valid()) {
-        if (!loaded) load_rows<FMT, R>(p, w, sub, cur);
-        loaded = false;
-        const int c = w.chunk();
-        const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
-        if (c < nch) {
-            // one activation row's digits live at a time; the weights stay in registers
-#pragma unroll
-            for (int mm = 0; mm < M; ++mm) {
-                uint4 xv[1][XP];
-                uint4 bv[1][2];
-#pragma unroll
-                for (int j = 0; j < XP; ++j) xv[0][j] = xd[(mm * XP + j) * nch + c];
-                bv[0][0] = xb[(mm * 2 + 0) * nch + c];
-                bv[0][1] = xb[(mm * 2 + 1) * nch + c];
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    if (row0 + r < p.rows) dot_int<FMT, 1>(cur[r], c, xv, bv, &acc[r][mm]);
-            }
-        }
-        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
-        w.next();
+    while (wa.valid()) {
+        step_int<FMT, M, R>(p, wa, sub, g, A, acc, xd, xb);
+        wa = wb;
+        wa.next();
+        load_rows_rs<FMT, R>(p, rs, wa, sub, A);
+        if (!wb.valid()) break;
+        step_int<FMT, M, R>(p, wb, sub, g, B, acc, xd, xb);
+        wb = wa;
+        wb.next();
+        load_rows_rs<FMT, R>(p, rs, wb, sub, B);
     }
 }
 
@@ -247,7 +281,7 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     // amortise it. Short rows favour more resident blocks per CU.
     const bool long_rows = nch > 128;
     s.block = long_rows ? 512 : 256;
-    int per_cu = long_rows ? 1 : 4;
+    int per_cu = long_rows ? 1 : 2;
     s.G = env_int("RQMV_G", s.G);
     s.R = env_int("RQMV_R", s.R);
     s.block = env_int("RQMV_BLOCK", s.block);

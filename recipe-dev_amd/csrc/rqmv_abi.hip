@@ -58,6 +58,7 @@ rq::Planes planes_of(const rqmv_weight* w, int64_t first_row) {
     P.base = w->dev + first_row * w->row_bytes;
     P.row_bytes = w->row_bytes;
     P.nch = (int)w->nch;
+    P.bytes = (uint32_t)(w->dev_bytes - (size_t)(first_row * w->row_bytes));
     return P;
 }
 
@@ -78,8 +79,8 @@ int create(int format, int64_t experts, int64_t rows, int64_t cols, const void* 
     int dev = current_device(&info);
     if (dev < 0) return dev;
     const int64_t layout = rq::layout_bytes(format, total_rows, cols);
-    if (layout >= (int64_t(1) << 32))
-        return fail(RQMV_EINVAL, "a weight's repacked bytes must stay below 4 GiB; split the tensor");
+    if (layout >= (int64_t)rq::kOobOffset)
+        return fail(RQMV_EINVAL, "a weight's repacked bytes must stay below 4 GiB - 256 B; split the tensor");
     std::vector<uint8_t> host((size_t)layout);
     if (rq::repack(format, total_rows, cols, static_cast<const uint8_t*>(bytes), host.data()) != 0)
         return fail(RQMV_EINVAL, "repack failed");
@@ -315,7 +316,7 @@ int moe_dims(const rqmv_moe_params* p, rq::MoeDims* d, const DeviceInfo& info) {
 rq::MoeBank bank_of(const rqmv_weight* w) {
     rq::MoeBank b;
     if (!w) {
-        b.P = rq::Planes{nullptr, 0, 0};
+        b.P = rq::Planes{nullptr, 0, 0, 0};
         b.rows = 0;
         return b;
     }
