@@ -99,12 +99,114 @@ def copy_calibration(mb, steps):
     print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "steps": steps}), flush=True)
 
 
+def moe_bench(args):
+    """The gguf_moe decode step at batch 1: d_model 2048, 256 experts of hidden
+    512 in Q4_K, top-8 softmax routing with renormalisation, fp16 router
+    2048x256, and a sigmoid-gated shared expert of the same shape. A step is
+    one rqmv_moe call (router, top-k, gate/up, down). Two copies of every
+    weight (about 0.9 GB) and 16 different tokens rotate, so the selected
+    experts change from step to step and the banks do not stay in the
+    Infinity Cache."""
+    import rqmv
+    from rqmv import synth
+
+    d, E, top, H = 2048, 256, 8, 512
+    rqmv.init(0)
+    log(f"bench: moe_c4 d={d} E={E} top={top} hidden={H} steps={args.steps}")
+    sets, hosts = [], []
+    for c in range(2):
+        seed = 17 + 100 * c
+        router = synth.f16_weights(E, d, 0.02, seed=seed, tag="router")
+        gate = synth.q4_k(E * H, d, seed=seed + 1, tag="gate")
+        up = synth.q4_k(E * H, d, seed=seed + 2, tag="up")
+        down = synth.q4_k(E * d, H, seed=seed + 3, tag="down")
+        sg = synth.f16_weights(1, d, 0.02, seed=seed + 4, tag="sg")
+        gs, us = synth.q4_k(H, d, seed=seed + 5, tag="gs"), synth.q4_k(H, d, seed=seed + 6, tag="us")
+        ds = synth.q4_k(d, H, seed=seed + 7, tag="ds")
+        moe = rqmv.Moe(rqmv.Weight("f16", E, d, router), rqmv.Weight("q4_k", H, d, gate, experts=E),
+                       rqmv.Weight("q4_k", H, d, up, experts=E), rqmv.Weight("q4_k", d, H, down, experts=E), top,
+                       scoring=rqmv.SCORE_SOFTMAX, renormalize=True, shared_gate_inp=rqmv.Weight("f16", 1, d, sg),
+                       gate_sh=rqmv.Weight("q4_k", H, d, gs), up_sh=rqmv.Weight("q4_k", H, d, us),
+                       down_sh=rqmv.Weight("q4_k", d, H, ds))
+        sets.append(moe)
+        hosts.append((router, gate, up, down, sg, gs, us, ds))
+    tokens = [synth.activations_f16(d, seed=1000 + t) for t in range(16)]
+    xbs = [rqmv.DeviceBuffer.from_array(t) for t in tokens]
+    yb = rqmv.DeviceBuffer(4 * d)
+    stream = rqmv.Stream()
+    expert_bytes = 3 * (H * d // 256 * 144)
+    alg_bytes = E * d * 2 + d * 2 + expert_bytes * (top + 1) + d * 2 + d * 4
+
+    rel = None
+    if not args.no_check:
+        import oracle
+
+        sets[0].run(xbs[0], rqmv.DTYPE_F16, yb, stream=stream)
+        stream.synchronize()
+        y = yb.download(np.float32)
+        router, gate, up, down, sg, gs, us, ds = hosts[0]
+        x64 = synth.fp16_to_f32(tokens[0]).astype(np.float64)
+        ref, _ = oracle.moe_f64("q4_k", d, E, top, H, router.view(np.uint16), gate, up, down, x64, scoring=0,
+                                renormalize=True, hidden_shared=H, shared_gate_bits=sg.view(np.uint16), gate_sh=gs,
+                                up_sh=us, down_sh=ds)
+        rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+        log(f"bench: parity rel-L2 {rel:.3e}")
+        if not rel <= 1e-3:
+            log("bench: parity check failed")
+            sys.exit(1)
+
+    def enqueue_steps(count):
+        for i in range(count):
+            sets[i % 2].run(xbs[i % 16], rqmv.DTYPE_F16, yb, stream=stream)
+
+    graph = rqmv.Graph(stream, lambda: enqueue_steps(args.steps))
+    graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = rqmv.Event(), rqmv.Event()
+    e0.record(stream)
+    graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    ms_per_step = e0.elapsed_ms(e1) / args.steps
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"bench: graph {args.steps} steps -> {ms_per_step * 1e3:.2f} us/step")
+    out = {
+        "metric": "gguf_moe decode step effective HBM GB/s at batch 1",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "gguf_moe decode step: d_model 2048, 256 Q4_K experts of hidden 512, top-8 softmax "
+                               "renormalised, fp16 router, sigmoid-gated shared expert", "bytes_per_step": alg_bytes,
+                   "launches_per_step": 4, "weight_sets": 2, "tokens": 16, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "note": "whole step (four launches) from the graph replay"},
+        "parity_rel_l2": rel,
+    }
+    if not args.no_cpu:
+        import oracle
+
+        router, gate, up, down, sg, gs, us, ds = hosts[0]
+        runs, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            x64 = synth.fp16_to_f32(tokens[runs % 16]).astype(np.float64)
+            oracle.moe_f64("q4_k", d, E, top, H, router.view(np.uint16), gate, up, down, x64, scoring=0,
+                           renormalize=True, hidden_shared=H, shared_gate_bits=sg.view(np.uint16), gate_sh=gs,
+                           up_sh=us, down_sh=ds)
+            runs += 1
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(alg_bytes * runs / el / 1e9, 3), "unit": "GB/s", "cores": 1,
+                               "kind": "port", "sample": f"{runs} moe steps in {el:.1f} s (f64 restatement, one thread)"}
+    print(json.dumps(out), flush=True)
+    graph.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="q4_k_up", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="q4_k_up", choices=sorted(WORKLOADS) + ["moe_c4"])
     ap.add_argument("--m", type=int, default=1, help="activation rows")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -120,6 +222,10 @@ def main():
 
     if args.copy_mb:
         copy_calibration(args.copy_mb, args.steps)
+        return
+
+    if args.workload == "moe_c4":
+        moe_bench(args)
         return
 
     import rqmv
