@@ -21,6 +21,11 @@ FORMATS = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_k": Q4_K, "q6
 _lib = None
 
 
+
+def _as_bytes(a) -> np.ndarray:
+    """The array's bytes as stored (a view, never a value conversion)."""
+    return np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+
 def lib():
     global _lib
     if _lib is None:
@@ -69,7 +74,7 @@ def f32_from_fp16(bits) -> np.ndarray:
 
 
 def dequant_rows(fmt, gguf: np.ndarray, rows: int, cols: int) -> np.ndarray:
-    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    g = _as_bytes(gguf)
     out = np.empty(rows * cols, np.float32)
     rc = lib().orc_dequant_rows(_fmt(fmt), g.ctypes.data, rows, cols, out.ctypes.data)
     assert rc == 0, rc
@@ -77,13 +82,13 @@ def dequant_rows(fmt, gguf: np.ndarray, rows: int, cols: int) -> np.ndarray:
 
 
 def dequant_value(fmt, block: np.ndarray, index: int) -> float:
-    b = np.ascontiguousarray(block, dtype=np.uint8)
+    b = _as_bytes(block)
     return lib().orc_dequant_value(_fmt(fmt), b.ctypes.data, index)
 
 
 def matvec_f64(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
     """x (M, K) float64 -> y (M, N) float64."""
-    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    g = _as_bytes(gguf)
     x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float64)
     m = x2.shape[0]
     y = np.empty((m, rows), np.float64)
@@ -94,7 +99,7 @@ def matvec_f64(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np
 
 def matvec_recipe_f32(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 1) -> np.ndarray:
     """recipe's fp32 float packed path: x (M, K) float32 -> y (M, N) float32."""
-    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    g = _as_bytes(gguf)
     x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
     m = x2.shape[0]
     y = np.empty((m, rows), np.float32)
@@ -131,7 +136,7 @@ def moe_f64(fmt, d_model, experts, top, hidden, router_bits, gate, up, down, x, 
 
 def q4k_q81_reference(w: np.ndarray, rows: int, cols: int, x: np.ndarray):
     """evidence bench.rs algebra: returns (y float32 (rows,), x as used float64 (cols,))."""
-    g = np.ascontiguousarray(w, dtype=np.uint8)
+    g = _as_bytes(w)
     xs = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty(rows, np.float32)
     xu = np.empty(cols, np.float64)

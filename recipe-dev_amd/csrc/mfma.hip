@@ -1,0 +1,419 @@
+// Small-M (2 <= M <= 32) quantized products on the matrix cores of gfx950.
+//
+// y[m][n] = sum_k W[n][k] x[m][k] is a real contraction once M > 1: each
+// weight is used M times. Here the weights are decoded to their exact
+// integer codes in fp16 (q, q - 8 or q - 32 are small integers, exact in
+// fp16) and multiplied with the fp16 activations on v_mfma_f32_16x16x32_f16
+// (v_mfma_f32_16x16x16_f16 for Q6_K, whose scales cover 16 weights). Every
+// product is exact and the matrix core accumulates one scale block in fp32;
+// the block's scale is applied to that block's 16x16 result in fp32 (and for
+// Q4_K the minimum through a second product of x with a block of ones), so
+// the arithmetic matches the batch-1 kernels' per-block epilogue. fp32
+// activations are split into an fp16 high and low part (x = hi + lo to 2^-22)
+// and multiplied as two tiles.
+//
+// Work mapping. A workgroup of four waves owns 64 rows (16 per wave, the
+// matrix core's N) and walks K in sub-steps of four chunks (256 weights, 128
+// for Q8_0):
+//   * the sub-step's activations, all M rows, are staged once per workgroup
+//     into LDS in the matrix core's A-operand order (double-buffered);
+//   * each wave loads its 16 rows x 256 weights with the same 16-byte,
+//     row-contiguous loads as the batch-1 kernels (lane = row, chunk), four
+//     sub-steps ahead of their use, decodes them and writes them to its own LDS
+//     tile in the B-operand order (the transpose from chunk-per-lane to
+//     k-slice-per-lane), with one fp32 scale pair per (block, row);
+//   * each 32-weight block (16 for Q6_K) is one MFMA per 16 activation rows
+//     into a zeroed accumulator, added into the running sums with its scale.
+// Reference counterpart: packed_lanes4_body (amd-nv-cpu.ll:2674-3126) and the
+// general contraction body (amd-nv-cpu.ll:3509-3649), which take M > 1 in fp32
+// fma on the vector units.
+#include <hip/hip_ext.h>
+
+#include "kernels.h"
+
+namespace rq {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 hv2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// A sub-step is four chunks of every row (SUBK weights of K: 256, or 128 for
+// Q8_0), one chunk per loader lane; NB matrix-core blocks per sub-step, KB
+// weights per block (the MFMA's K).
+template <int FMT> struct MfmaTraits;
+template <> struct MfmaTraits<Q4_0> { static constexpr int SUBK = 256, NB = 8, KB = 32; };
+template <> struct MfmaTraits<Q4_K> { static constexpr int SUBK = 256, NB = 8, KB = 32; };
+template <> struct MfmaTraits<Q8_0> { static constexpr int SUBK = 128, NB = 4, KB = 32; };
+template <> struct MfmaTraits<Q6_K> { static constexpr int SUBK = 256, NB = 16, KB = 16; };
+
+constexpr int kMfmaWaves = 4;   // waves (16-row stripes) per workgroup
+constexpr int kWeightDepth = 4; // sub-steps of weights in flight per wave
+constexpr int kUnitPad = 17;    // B-tile units per (block, k-slice): 16 rows + 1 against bank conflicts
+
+template <int FMT, int NT, bool XF32>
+struct MfmaLds {
+    using T = MfmaTraits<FMT>;
+    static constexpr int NTA = NT * (XF32 ? 2 : 1);           // A tiles per block (hi/lo for fp32 x)
+    static constexpr int UB = T::KB == 32 ? 16 : 8;           // bytes per operand unit (8 or 4 halves)
+    static constexpr int XBUF = T::NB * NTA * 64 * UB;        // one staged activation sub-step
+    static constexpr int BTILE = T::NB * 4 * kUnitPad * UB + 128;   // one wave's decoded weights (+ skew)
+    static constexpr int SCALES = T::NB * 16 * 8 + 128;             // one wave's (scale, min) pairs (+ skew)
+    static constexpr int WAVE = BTILE + SCALES;
+    static constexpr int TOTAL = 2 * XBUF + kMfmaWaves * WAVE;
+};
+
+__device__ __forceinline__ uint32_t pk_add_h(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(hv2_t, a) + __builtin_bit_cast(hv2_t, b));
+}
+
+// Eight 4-bit codes u (weight i in bits 4i..4i+3) -> four words of fp16 pairs
+// (u_2t - off, u_2t+1 - off). The even code goes into the mantissa of 1024.0
+// (0x6400 | u), the odd one, left in its byte's high nibble, into the mantissa
+// of 64.0 (0x5400 | 16u), and one packed fp16 add of (-1024 - off, -64 - off)
+// removes both offsets exactly.
+__device__ __forceinline__ void nibbles_to_h(uint32_t w, uint32_t neg, uint32_t (&o)[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t sel = (uint32_t)t | 0x0c00u | ((uint32_t)t << 16) | 0x0c000000u;
+        const uint32_t b = __builtin_amdgcn_perm(0u, w, sel);  // [byte t, 0, byte t, 0]
+        o[t] = pk_add_h((b & 0x00F0000Fu) | 0x54006400u, neg);
+    }
+}
+
+// Four int8 codes -> two words of fp16 pairs: q + 128 in the mantissa of
+// 1024.0, then - 1152.
+__device__ __forceinline__ void bytes_to_h(uint32_t w, uint32_t& o0, uint32_t& o1) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t neg = 0xE480E480u;  // (-1152, -1152)
+    o0 = pk_add_h(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), neg);
+    o1 = pk_add_h(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), neg);
+}
+
+// Q6_K: eight low nibbles L (codes already un-XORed) and their high fields
+// as nibbles Hx -> four words of fp16 pairs (l + 16h - 32).
+__device__ __forceinline__ void q6_to_h(uint32_t L, uint32_t Hx, uint32_t (&o)[4]) {
+    const uint32_t ev = (L & 0x0F0F0F0Fu) | ((Hx & 0x03030303u) << 4);   // byte t: code of weight 2t
+    const uint32_t od = ((L >> 4) & 0x0F0F0F0Fu) | (Hx & 0x30303030u);   // byte t: code of weight 2t+1
+    const uint32_t neg = 0xE420E420u;  // (-1056, -1056)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t sel = (uint32_t)t | 0x0c00u | ((uint32_t)(4 + t) << 16) | 0x0c000000u;
+        o[t] = pk_add_h(__builtin_amdgcn_perm(od, ev, sel) | 0x64006400u, neg);
+    }
+}
+
+// Byte offset of B-tile unit (block b, k-slice q, row n). The blocks of one
+// loader chunk are shifted by 32 bytes per chunk, so that the four loader
+// lanes of a row (same n, different chunk) write to different LDS banks.
+template <int FMT>
+__device__ __forceinline__ int bt_unit(int b, int q, int n) {
+    using T = MfmaTraits<FMT>;
+    constexpr int UB = T::KB == 32 ? 16 : 8, PER_CHUNK = T::NB / 4;
+    return ((b * 4 + q) * kUnitPad + n) * UB + (b / PER_CHUNK) * 32;
+}
+template <int FMT>
+__device__ __forceinline__ int scl_index(int b, int n) {
+    constexpr int PER_CHUNK = MfmaTraits<FMT>::NB / 4;
+    return b * 16 + n + (b / PER_CHUNK) * 4;  // float2 units: 32-byte shift per chunk
+}
+
+template <int FMT, int NT, bool XF32>
+__global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x_bytes) {
+    using TR = MfmaTraits<FMT>;
+    using L = MfmaLds<FMT, NT, XF32>;
+    constexpr int SUBK = TR::SUBK, NB = TR::NB, NTA = L::NTA, UB = L::UB;
+    constexpr int XI = 16 * NT * (SUBK / 8) / (64 * kMfmaWaves);  // activation items per thread
+    constexpr int XW = XF32 ? 2 : 1;                                // 16-byte loads per item
+    extern __shared__ uint4 smem[];
+    uint8_t* lds = reinterpret_cast<uint8_t*>(smem);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint8_t* const xbuf[2] = {lds, lds + L::XBUF};
+    uint8_t* const bt = lds + 2 * L::XBUF + wave * L::WAVE;
+    float2* const scl = reinterpret_cast<float2*>(bt + L::BTILE);
+
+    const int64_t row0 = ((int64_t)blockIdx.x * kMfmaWaves + wave) * 16;
+    const int nch = p.P.nch;
+    const int steps = (nch + 3) / 4;
+    const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), (short)0, (int)x_bytes, 0x00020000);
+    const int ln = lane >> 2, lj = lane & 3;          // loader: row, chunk of the sub-step
+    const int mn = lane & 15, mq = lane >> 4;         // matrix core: B column (row n), k-slice
+    const int64_t lrow = row0 + ln;
+    const bool lrow_ok = lrow < p.rows;
+
+    auto load_w = [&](int t, ChunkData<FMT>& d) {
+        const int c = t * 4 + lj;
+        load_chunk_rs<FMT>(rs, p.P, (uint32_t)lrow, c, lrow_ok && c < nch, d);
+    };
+    // Activation item of a sub-step: eight values at k8 * 8 of row mm = 16 tm
+    // + m, with m fastest so that consecutive lanes write consecutive LDS units.
+    constexpr int K8 = SUBK / 8;
+    auto load_x = [&](int t, uint4 (&v)[XI][XW]) {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int item = (int)threadIdx.x + 256 * i;
+            const int mm = ((item >> 4) / K8) * 16 + (item & 15), k = t * SUBK + 8 * ((item >> 4) % K8);
+            const bool ok = mm < M && k < p.K;
+            const uint32_t off = (uint32_t)(((int64_t)mm * p.ldx + k) * (XF32 ? 4 : 2));
+#pragma unroll
+            for (int h = 0; h < XW; ++h) {
+                const u32x4_t r = __builtin_amdgcn_raw_buffer_load_b128(xrs, ok ? off + 16u * h : kOobOffset, 0, 0);
+                v[i][h] = make_uint4(r.x, r.y, r.z, r.w);
+            }
+        }
+    };
+    auto store_x = [&](const uint4 (&v)[XI][XW], uint8_t* xb) {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int item = (int)threadIdx.x + 256 * i;
+            const int m = item & 15, k8 = (item >> 4) % K8, tm = (item >> 4) / K8;
+            uint4 parts[2];  // [0] = fp16 values (or the high parts), [1] = low parts
+            if constexpr (XF32) {
+                uint32_t hi[4], lo[4];
+                const float f[8] = {__builtin_bit_cast(float, v[i][0].x), __builtin_bit_cast(float, v[i][0].y),
+                                    __builtin_bit_cast(float, v[i][0].z), __builtin_bit_cast(float, v[i][0].w),
+                                    __builtin_bit_cast(float, v[i][1].x), __builtin_bit_cast(float, v[i][1].y),
+                                    __builtin_bit_cast(float, v[i][1].z), __builtin_bit_cast(float, v[i][1].w)};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const _Float16 h0 = (_Float16)f[2 * e], h1 = (_Float16)f[2 * e + 1];
+                    const _Float16 l0 = (_Float16)(f[2 * e] - (float)h0), l1 = (_Float16)(f[2 * e + 1] - (float)h1);
+                    hi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                    lo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+                }
+                parts[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                parts[1] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            } else {
+                parts[0] = v[i][0];
+            }
+#pragma unroll
+            for (int h = 0; h < XW; ++h) {
+                const int ta = tm * XW + h;
+                if constexpr (TR::KB == 32) {
+                    const int b = k8 >> 2, q = k8 & 3;
+                    *reinterpret_cast<uint4*>(xb + (((b * NTA + ta) * 64) + q * 16 + m) * 16) = parts[h];
+                } else {
+                    const int g = k8 >> 1, q = 2 * (k8 & 1);
+                    *reinterpret_cast<uint2*>(xb + (((g * NTA + ta) * 64) + q * 16 + m) * 8) = make_uint2(parts[h].x, parts[h].y);
+                    *reinterpret_cast<uint2*>(xb + (((g * NTA + ta) * 64) + (q + 1) * 16 + m) * 8) = make_uint2(parts[h].z, parts[h].w);
+                }
+            }
+        }
+    };
+    // Decodes this lane's chunk(s) into the wave's B tile and scale table.
+    auto store_b = [&](const ChunkData<FMT>& d0) {
+        if constexpr (FMT == Q4_0 || FMT == Q4_K) {
+            const uint32_t neg = FMT == Q4_0 ? 0xD480E408u : 0xD400E400u;  // (-1032, -72) or (-1024, -64)
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                const int b = 2 * lj + part;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uint32_t o[4];
+                    nibbles_to_h(word(d0.q[part], q) ^ 0x88888888u, neg, o);
+                    *reinterpret_cast<uint4*>(bt + bt_unit<FMT>(b, q, ln)) = make_uint4(o[0], o[1], o[2], o[3]);
+                }
+            }
+            if constexpr (FMT == Q4_K) {
+                uint32_t sc0, m0, sc1, m1;
+                q4k_scales(d0.meta, lj, sc0, m0, sc1, m1);
+                const float dd = half_lo(d0.meta.x), dmin = half_hi(d0.meta.x);
+                scl[scl_index<FMT>(2 * lj, ln)] = make_float2(dd * (float)sc0, dmin * (float)m0);
+                scl[scl_index<FMT>(2 * lj + 1, ln)] = make_float2(dd * (float)sc1, dmin * (float)m1);
+            } else {
+                scl[scl_index<FMT>(2 * lj, ln)] = make_float2(half_lo(d0.meta.x), 0.f);
+                scl[scl_index<FMT>(2 * lj + 1, ln)] = make_float2(half_hi(d0.meta.x), 0.f);
+            }
+        } else if constexpr (FMT == Q8_0) {
+            const int b = lj;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t o[4];
+                bytes_to_h(word(d0.q[q >> 1], 2 * (q & 1)), o[0], o[1]);
+                bytes_to_h(word(d0.q[q >> 1], 2 * (q & 1) + 1), o[2], o[3]);
+                *reinterpret_cast<uint4*>(bt + bt_unit<FMT>(b, q, ln)) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+            scl[scl_index<FMT>(b, ln)] = make_float2(half_lo(d0.meta.x), 0.f);
+        } else {  // Q6_K: four 16-weight scale groups per chunk
+            const float dd = half_lo(d0.meta.y);
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                const int g = 4 * lj + gg;
+                const uint32_t L0 = word(d0.q[gg >> 1], (gg & 1) * 2) ^ 0x88888888u;
+                const uint32_t L1 = word(d0.q[gg >> 1], (gg & 1) * 2 + 1) ^ 0x88888888u;
+                const uint32_t H = word(d0.q[2], gg);
+                uint32_t o[4], o2[4];
+                q6_to_h(L0, H & 0x33333333u, o);
+                q6_to_h(L1, (H >> 2) & 0x33333333u, o2);
+                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 0, ln)) = make_uint2(o[0], o[1]);
+                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 1, ln)) = make_uint2(o[2], o[3]);
+                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 2, ln)) = make_uint2(o2[0], o2[1]);
+                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 3, ln)) = make_uint2(o2[2], o2[3]);
+                scl[scl_index<FMT>(g, ln)] = make_float2(dd * (float)(int8_t)((d0.meta.x >> (8 * gg)) & 0xffu), 0.f);
+            }
+        }
+    };
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int ta = 0; ta < NT; ++ta) acc[ta] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    // The sub-step's products: one matrix-core block at a time, scaled into acc.
+    auto multiply = [&](const uint8_t* xb) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float2 s = scl[scl_index<FMT>(b, mn)];
+            if constexpr (TR::KB == 32) {
+                const h8_t B = *reinterpret_cast<const h8_t*>(bt + bt_unit<FMT>(b, mq, mn));
+#pragma unroll
+                for (int ta = 0; ta < NT; ++ta) {
+                    const f4_t z = {0.f, 0.f, 0.f, 0.f};
+                    f4_t D, D2;
+                    if constexpr (XF32) {
+                        const h8_t Ah = *reinterpret_cast<const h8_t*>(xb + ((b * NTA + 2 * ta) * 64 + lane) * 16);
+                        const h8_t Al = *reinterpret_cast<const h8_t*>(xb + ((b * NTA + 2 * ta + 1) * 64 + lane) * 16);
+                        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B, __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B, z, 0, 0, 0), 0, 0, 0);
+                        if constexpr (FMT == Q4_K) {
+                            const h8_t one = {1, 1, 1, 1, 1, 1, 1, 1};
+                            D2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, one, __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, one, z, 0, 0, 0), 0, 0, 0);
+                        }
+                    } else {
+                        const h8_t A = *reinterpret_cast<const h8_t*>(xb + ((b * NTA + ta) * 64 + lane) * 16);
+                        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, z, 0, 0, 0);
+                        if constexpr (FMT == Q4_K) {
+                            const h8_t one = {1, 1, 1, 1, 1, 1, 1, 1};
+                            D2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, one, z, 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float a = fmaf(s.x, D[j], acc[ta][j]);
+                        if constexpr (FMT == Q4_K) a = fmaf(-s.y, D2[j], a);
+                        acc[ta][j] = a;
+                    }
+                }
+            } else {
+                const h4_t B = *reinterpret_cast<const h4_t*>(bt + bt_unit<FMT>(b, mq, mn));
+#pragma unroll
+                for (int ta = 0; ta < NT; ++ta) {
+                    const f4_t z = {0.f, 0.f, 0.f, 0.f};
+                    f4_t D;
+                    if constexpr (XF32) {
+                        const h4_t Ah = *reinterpret_cast<const h4_t*>(xb + ((b * NTA + 2 * ta) * 64 + lane) * 8);
+                        const h4_t Al = *reinterpret_cast<const h4_t*>(xb + ((b * NTA + 2 * ta + 1) * 64 + lane) * 8);
+                        D = __builtin_amdgcn_mfma_f32_16x16x16f16(Al, B, __builtin_amdgcn_mfma_f32_16x16x16f16(Ah, B, z, 0, 0, 0), 0, 0, 0);
+                    } else {
+                        const h4_t A = *reinterpret_cast<const h4_t*>(xb + ((b * NTA + ta) * 64 + lane) * 8);
+                        D = __builtin_amdgcn_mfma_f32_16x16x16f16(A, B, z, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[ta][j] = fmaf(s.x, D[j], acc[ta][j]);
+                }
+            }
+        }
+    };
+
+    // Weights run kWeightDepth sub-steps ahead in rotating register sets and
+    // activations two sub-steps ahead (a register set, then an LDS buffer), so
+    // that enough bytes are in flight to cover HBM latency. A set is refilled
+    // only after it has been decoded, never copied while its loads are pending.
+    ChunkData<FMT> w[kWeightDepth];
+    uint4 xr[2][XI][XW];
+    load_x(0, xr[0]);
+    load_x(1, xr[1]);
+#pragma unroll
+    for (int i = 0; i < kWeightDepth; ++i) load_w(i, w[i]);
+    store_x(xr[0], xbuf[0]);
+    __syncthreads();
+    // whole rounds of kWeightDepth sub-steps: the ones past K load nothing
+    // (out-of-range buffer loads) and add zero
+    const int rounds = (steps + kWeightDepth - 1) / kWeightDepth;
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+        for (int u = 0; u < kWeightDepth; ++u) {
+            const int t = r * kWeightDepth + u;
+            load_x(t + 2, xr[u & 1]);
+            store_b(w[u]);
+            asm volatile("" ::: "memory");  // the tile is read back under other types
+            multiply(xbuf[u & 1]);
+            load_w(t + kWeightDepth, w[u]);
+            store_x(xr[(u + 1) & 1], xbuf[(u + 1) & 1]);
+            __syncthreads();
+        }
+    }
+
+    const int64_t row = row0 + mn;
+    if (row < p.rows) {
+#pragma unroll
+        for (int ta = 0; ta < NT; ++ta)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = 16 * ta + 4 * mq + j;
+                if (m < M) p.y[(int64_t)m * p.ldy + row] = acc[ta][j];
+            }
+    }
+}
+
+size_t mfma_lds_bytes(int fmt, int xtype, int M) {
+    const bool f32 = xtype == X_F32, two = M > 16;
+    switch (fmt) {
+        case Q4_0: return two ? (f32 ? MfmaLds<Q4_0, 2, true>::TOTAL : MfmaLds<Q4_0, 2, false>::TOTAL)
+                              : (f32 ? MfmaLds<Q4_0, 1, true>::TOTAL : MfmaLds<Q4_0, 1, false>::TOTAL);
+        case Q4_K: return two ? (f32 ? MfmaLds<Q4_K, 2, true>::TOTAL : MfmaLds<Q4_K, 2, false>::TOTAL)
+                              : (f32 ? MfmaLds<Q4_K, 1, true>::TOTAL : MfmaLds<Q4_K, 1, false>::TOTAL);
+        case Q8_0: return two ? (f32 ? MfmaLds<Q8_0, 2, true>::TOTAL : MfmaLds<Q8_0, 2, false>::TOTAL)
+                              : (f32 ? MfmaLds<Q8_0, 1, true>::TOTAL : MfmaLds<Q8_0, 1, false>::TOTAL);
+        case Q6_K: return two ? (f32 ? MfmaLds<Q6_K, 2, true>::TOTAL : MfmaLds<Q6_K, 2, false>::TOTAL)
+                              : (f32 ? MfmaLds<Q6_K, 1, true>::TOTAL : MfmaLds<Q6_K, 1, false>::TOTAL);
+        default: return 0;
+    }
+}
+
+template <int FMT, int NT, bool XF32>
+static hipError_t launch_mfma_one(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
+                                  hipEvent_t ev1) {
+    const size_t lds = MfmaLds<FMT, NT, XF32>::TOTAL;
+    auto kernel = matvec_mfma<FMT, NT, XF32>;
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const int64_t stripes = (p.rows + 15) / 16;
+    const int grid = (int)((stripes + kMfmaWaves - 1) / kMfmaWaves);
+    if (ev0 || ev1)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), (uint32_t)lds, stream, ev0, ev1, 0u, p, M, x_bytes);
+    else
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p, M, x_bytes);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t launch_mfma_fmt(int xtype, const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream,
+                                  hipEvent_t ev0, hipEvent_t ev1) {
+    if (M > 16) {
+        if (xtype == X_F32) return launch_mfma_one<FMT, 2, true>(p, M, x_bytes, stream, ev0, ev1);
+        return launch_mfma_one<FMT, 2, false>(p, M, x_bytes, stream, ev0, ev1);
+    }
+    if (xtype == X_F32) return launch_mfma_one<FMT, 1, true>(p, M, x_bytes, stream, ev0, ev1);
+    return launch_mfma_one<FMT, 1, false>(p, M, x_bytes, stream, ev0, ev1);
+}
+
+hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, hipStream_t stream, hipEvent_t ev0,
+                              hipEvent_t ev1) {
+    if (M < 1 || M > 32) return hipErrorInvalidValue;
+    const size_t esize = xtype == X_F32 ? 4 : 2;
+    const int64_t x_bytes = ((int64_t)(M - 1) * p.ldx + p.K) * (int64_t)esize;
+    if (x_bytes >= (int64_t)kOobOffset) return hipErrorInvalidValue;
+    switch (fmt) {
+        case Q4_0: return launch_mfma_fmt<Q4_0>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q4_K: return launch_mfma_fmt<Q4_K>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q8_0: return launch_mfma_fmt<Q8_0>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q6_K: return launch_mfma_fmt<Q6_K>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace rq

@@ -1,4 +1,6 @@
 // C-ABI entry points of librqmv (declared in include/rqmv.h).
+#include <stdlib.h>
+
 #include <mutex>
 #include <string>
 #include <vector>
@@ -60,6 +62,11 @@ rq::Planes planes_of(const rqmv_weight* w, int64_t first_row) {
     P.nch = (int)w->nch;
     P.bytes = (uint32_t)(w->dev_bytes - (size_t)(first_row * w->row_bytes));
     return P;
+}
+
+int env_int(const char* name, int fallback) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : fallback;
 }
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -133,6 +140,22 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     p.ldx = ldx;
     p.ldy = ldy;
     int done = 0;
+    // Two or more activation rows of a quantized weight go to the matrix
+    // cores, up to 32 rows per launch.
+    const int mfma_min = env_int("RQMV_MFMA_MIN", 2);
+    if (w->fmt != rq::F16 && m >= mfma_min) {
+        while (done < m) {
+            const int mb = m - done > 32 ? 32 : m - done;
+            if (rq::mfma_lds_bytes(w->fmt, xtype, mb) > info.lds_limit) return fail(RQMV_EINVAL, "LDS too small");
+            p.x = static_cast<const char*>(x) + (size_t)done * (size_t)ldx * esize;
+            p.y = y + (int64_t)done * ldy;
+            const bool first = done == 0, last = done + mb >= m;
+            hipError_t e = rq::launch_matvec_mfma(w->fmt, xtype, mb, p, stream, first ? ev0 : nullptr, last ? ev1 : nullptr);
+            if (e != hipSuccess) return hip_fail(e, "matvec launch");
+            done += mb;
+        }
+        return RQMV_OK;
+    }
     while (done < m) {
         int mb = 8;
         while (mb > m - done) mb >>= 1;

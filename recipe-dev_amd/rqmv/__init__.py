@@ -86,6 +86,11 @@ class _Lib:
 _lib = None
 
 
+
+def _as_bytes(a) -> np.ndarray:
+    """The array's bytes as stored (a view, never a value conversion)."""
+    return np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+
 def lib() -> _Lib:
     global _lib
     if _lib is None:
@@ -232,7 +237,8 @@ class Weight:
     """A repacked weight (or expert bank) resident on the device."""
 
     def __init__(self, fmt, rows: int, cols: int, gguf: np.ndarray, experts: int | None = None):
-        gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
+        # the tensor's bytes as stored (an F16 tensor may come as uint16 or float16 values)
+        gguf = np.ascontiguousarray(gguf).view(np.uint8).reshape(-1)
         h = c_void_p()
         if experts is None:
             _check(lib().lib.rqmv_weight_create(_fmt(fmt), rows, cols, gguf.ctypes.data, gguf.nbytes, byref(h)),
@@ -372,13 +378,13 @@ def layout_bytes(fmt, rows: int, cols: int) -> int:
 def repack_host(fmt, rows: int, cols: int, gguf: np.ndarray) -> np.ndarray:
     """GGUF bytes -> the kernels' repacked layout, on the host."""
     out = np.zeros(layout_bytes(fmt, rows, cols), np.uint8)
-    g = np.ascontiguousarray(gguf, dtype=np.uint8)
+    g = _as_bytes(gguf)
     _check(lib().lib.rqmv_repack_host(_fmt(fmt), rows, cols, g.ctypes.data, out.ctypes.data), "rqmv_repack_host")
     return out
 
 
 def unpack_host(fmt, rows: int, cols: int, packed: np.ndarray, nbytes: int) -> np.ndarray:
     out = np.zeros(nbytes, np.uint8)
-    pk = np.ascontiguousarray(packed, dtype=np.uint8)
+    pk = _as_bytes(packed)
     _check(lib().lib.rqmv_unpack_host(_fmt(fmt), rows, cols, pk.ctypes.data, out.ctypes.data), "rqmv_unpack_host")
     return out

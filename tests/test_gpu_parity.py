@@ -122,6 +122,37 @@ def test_matvec_parity(gpu, fmt, xdt, m):
         assert err <= limit, (fmt, xdt, m, rows, cols, err)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("m", [16, 17, 32, 33, 40])
+def test_matvec_parity_matrix_core_sizes(gpu, fmt, xdt, m):
+    """Two or more activation rows run on the matrix cores, up to 32 rows per
+    launch: full and partial 16-row tiles, and more rows than one launch."""
+    shapes = [(17, 768), (300, 4096)] if fmt in ("q4_k", "q6_k") else [(5, 96), (300, 4096), (9, 160)]
+    for rows, cols in shapes:
+        w = _weights(fmt, rows, cols, seed=rows + 5 * cols + m)
+        W = gpu.Weight(fmt, rows, cols, w)
+        xh, dt, x32 = _x(m, cols, xdt, seed=cols + 2 * m)
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+        err = rel_l2(y, ref)
+        assert err <= 2e-4, (fmt, xdt, m, rows, cols, err)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_small_m_vector_path(gpu, fmt, monkeypatch):
+    """RQMV_MFMA_MIN moves small M back to the vector kernels; both paths agree with the oracle."""
+    monkeypatch.setenv("RQMV_MFMA_MIN", "99")
+    rows, cols = (300, 4096)
+    w = _weights(fmt, rows, cols, seed=11)
+    W = gpu.Weight(fmt, rows, cols, w)
+    for m in (2, 8, 13):
+        xh, dt, x32 = _x(m, cols, "f16", seed=m)
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+        assert rel_l2(y, ref) <= 2e-4, (fmt, m)
+
+
 def test_matvec_is_deterministic(gpu):
     rows, cols = 4096, 4096
     w = synth.q4_k(rows, cols, seed=1)
