@@ -128,6 +128,13 @@ __device__ __forceinline__ void load_chunk(const Planes& P, int64_t row, int c, 
     }
 }
 
+// `off` where `keep` is all ones, kOobOffset where it is zero. Written as a
+// bit select so that the compiler keeps one unconditional load instead of
+// branching around it.
+__device__ __forceinline__ uint32_t oob_unless(uint32_t off, uint32_t keep) {
+    return (off & keep) | (kOobOffset & ~keep);
+}
+
 // Buffer resource over a weight's bytes: raw (stride 0) addressing with
 // 32-bit data format, so a dword load at or past `bytes` returns zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t planes_rsrc(const Planes& P) {
@@ -145,7 +152,8 @@ __device__ __forceinline__ void load_chunk_rs(__amdgpu_buffer_rsrc_t rs, const P
     const uint32_t rest = (uint32_t)P.nch - (group << 6);
     const uint32_t nb = rest > 64u ? 64u : rest;
     const uint32_t gb = row * (uint32_t)P.row_bytes + group * full_group_bytes<FMT>();
-    auto at = [&](uint32_t off) { return valid ? off : kOobOffset; };
+    const uint32_t keep = valid ? 0xFFFFFFFFu : 0u;
+    auto at = [&](uint32_t off) { return oob_unless(off, keep); };
 #pragma unroll
     for (int h = 0; h < QP; ++h) {
         const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, at(gb + ((uint32_t)h * nb + within) * 16u), 0, 0);

@@ -43,8 +43,8 @@ hipError_t launch_dequant(int fmt, const Planes& P, int64_t rows, int cols, floa
 size_t matvec_lds_bytes(int fmt, int xtype, int M, int cols);
 
 // Matrix-core product for 1 <= M <= 32 activation rows (quantized formats).
-hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, hipStream_t stream,
+hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, int cus, hipStream_t stream,
                               hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
-size_t mfma_lds_bytes(int fmt, int xtype, int M);
+size_t mfma_lds_bytes(int fmt, int xtype, int M, int64_t rows, int cus);
 
 }  // namespace rq

@@ -12,8 +12,8 @@
 // activations are split into an fp16 high and low part (x = hi + lo to 2^-22)
 // and multiplied as two tiles.
 //
-// Work mapping. A workgroup of four waves owns 64 rows (16 per wave, the
-// matrix core's N) and walks K in sub-steps of four chunks (256 weights, 128
+// Work mapping. A workgroup of W waves (four, or fewer for short matrices)
+// owns 16 W rows (16 per wave, the matrix core's N) and walks K in sub-steps of four chunks (256 weights, 128
 // for Q8_0):
 //   * the sub-step's activations, all M rows, are staged once per workgroup
 //     into LDS in the matrix core's A-operand order (double-buffered);
@@ -28,6 +28,9 @@
 // general contraction body (amd-nv-cpu.ll:3509-3649), which take M > 1 in fp32
 // fma on the vector units.
 #include <hip/hip_ext.h>
+#include <stdlib.h>
+
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -47,11 +50,10 @@ template <> struct MfmaTraits<Q4_K> { static constexpr int SUBK = 256, NB = 8, K
 template <> struct MfmaTraits<Q8_0> { static constexpr int SUBK = 128, NB = 4, KB = 32; };
 template <> struct MfmaTraits<Q6_K> { static constexpr int SUBK = 256, NB = 16, KB = 16; };
 
-constexpr int kMfmaWaves = 4;   // waves (16-row stripes) per workgroup
 constexpr int kWeightDepth = 4; // sub-steps of weights in flight per wave
 constexpr int kUnitPad = 17;    // B-tile units per (block, k-slice): 16 rows + 1 against bank conflicts
 
-template <int FMT, int NT, bool XF32>
+template <int FMT, int NT, bool XF32, int W>
 struct MfmaLds {
     using T = MfmaTraits<FMT>;
     static constexpr int NTA = NT * (XF32 ? 2 : 1);           // A tiles per block (hi/lo for fp32 x)
@@ -60,7 +62,7 @@ struct MfmaLds {
     static constexpr int BTILE = T::NB * 4 * kUnitPad * UB + 128;   // one wave's decoded weights (+ skew)
     static constexpr int SCALES = T::NB * 16 * 8 + 128;             // one wave's (scale, min) pairs (+ skew)
     static constexpr int WAVE = BTILE + SCALES;
-    static constexpr int TOTAL = 2 * XBUF + kMfmaWaves * WAVE;
+    static constexpr int TOTAL = 2 * XBUF + W * WAVE;
 };
 
 __device__ __forceinline__ uint32_t pk_add_h(uint32_t a, uint32_t b) {
@@ -118,12 +120,68 @@ __device__ __forceinline__ int scl_index(int b, int n) {
     return b * 16 + n + (b / PER_CHUNK) * 4;  // float2 units: 32-byte shift per chunk
 }
 
-template <int FMT, int NT, bool XF32>
-__global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x_bytes) {
+// Decodes one loader lane's chunk (row ln, chunk lj of the sub-step) into a
+// wave's B tile and scale table.
+template <int FMT>
+__device__ __forceinline__ void decode_to_tile(const ChunkData<FMT>& d0, int ln, int lj, uint8_t* bt, float2* scl) {
+    if constexpr (FMT == Q4_0 || FMT == Q4_K) {
+        const uint32_t neg = FMT == Q4_0 ? 0xD480E408u : 0xD400E400u;  // (-1032, -72) or (-1024, -64)
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+            const int b = 2 * lj + part;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t o[4];
+                nibbles_to_h(word(d0.q[part], q) ^ 0x88888888u, neg, o);
+                *reinterpret_cast<uint4*>(bt + bt_unit<FMT>(b, q, ln)) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+        if constexpr (FMT == Q4_K) {
+            uint32_t sc0, m0, sc1, m1;
+            q4k_scales(d0.meta, lj, sc0, m0, sc1, m1);
+            const float dd = half_lo(d0.meta.x), dmin = half_hi(d0.meta.x);
+            scl[scl_index<FMT>(2 * lj, ln)] = make_float2(dd * (float)sc0, dmin * (float)m0);
+            scl[scl_index<FMT>(2 * lj + 1, ln)] = make_float2(dd * (float)sc1, dmin * (float)m1);
+        } else {
+            scl[scl_index<FMT>(2 * lj, ln)] = make_float2(half_lo(d0.meta.x), 0.f);
+            scl[scl_index<FMT>(2 * lj + 1, ln)] = make_float2(half_hi(d0.meta.x), 0.f);
+        }
+    } else if constexpr (FMT == Q8_0) {
+        const int b = lj;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t o[4];
+            bytes_to_h(word(d0.q[q >> 1], 2 * (q & 1)), o[0], o[1]);
+            bytes_to_h(word(d0.q[q >> 1], 2 * (q & 1) + 1), o[2], o[3]);
+            *reinterpret_cast<uint4*>(bt + bt_unit<FMT>(b, q, ln)) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        scl[scl_index<FMT>(b, ln)] = make_float2(half_lo(d0.meta.x), 0.f);
+    } else {  // Q6_K: four 16-weight scale groups per chunk
+        const float dd = half_lo(d0.meta.y);
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+            const int g = 4 * lj + gg;
+            const uint32_t L0 = word(d0.q[gg >> 1], (gg & 1) * 2) ^ 0x88888888u;
+            const uint32_t L1 = word(d0.q[gg >> 1], (gg & 1) * 2 + 1) ^ 0x88888888u;
+            const uint32_t H = word(d0.q[2], gg);
+            uint32_t o[4], o2[4];
+            q6_to_h(L0, H & 0x33333333u, o);
+            q6_to_h(L1, (H >> 2) & 0x33333333u, o2);
+            *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 0, ln)) = make_uint2(o[0], o[1]);
+            *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 1, ln)) = make_uint2(o[2], o[3]);
+            *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 2, ln)) = make_uint2(o2[0], o2[1]);
+            *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 3, ln)) = make_uint2(o2[2], o2[3]);
+            scl[scl_index<FMT>(g, ln)] = make_float2(dd * (float)(int8_t)((d0.meta.x >> (8 * gg)) & 0xffu), 0.f);
+        }
+    }
+}
+
+template <int FMT, int NT, bool XF32, int W>
+__global__ void __launch_bounds__(64 * W) matvec_mfma(MvParams p, int M, uint32_t x_bytes) {
     using TR = MfmaTraits<FMT>;
-    using L = MfmaLds<FMT, NT, XF32>;
+    using L = MfmaLds<FMT, NT, XF32, W>;
     constexpr int SUBK = TR::SUBK, NB = TR::NB, NTA = L::NTA, UB = L::UB;
-    constexpr int XI = 16 * NT * (SUBK / 8) / (64 * kMfmaWaves);  // activation items per thread
+    constexpr int XI = 16 * NT * (SUBK / 8) / (64 * W);  // activation items per thread
     constexpr int XW = XF32 ? 2 : 1;                                // 16-byte loads per item
     extern __shared__ uint4 smem[];
     uint8_t* lds = reinterpret_cast<uint8_t*>(smem);
@@ -132,7 +190,7 @@ __global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x
     uint8_t* const bt = lds + 2 * L::XBUF + wave * L::WAVE;
     float2* const scl = reinterpret_cast<float2*>(bt + L::BTILE);
 
-    const int64_t row0 = ((int64_t)blockIdx.x * kMfmaWaves + wave) * 16;
+    const int64_t row0 = ((int64_t)blockIdx.x * W + wave) * 16;
     const int nch = p.P.nch;
     const int steps = (nch + 3) / 4;
     const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
@@ -153,7 +211,7 @@ __global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x
     auto load_x = [&](int t, uint4 (&v)[XI][XW]) {
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
-            const int item = (int)threadIdx.x + 256 * i;
+            const int item = (int)threadIdx.x + 64 * W * i;
             const int mm = ((item >> 4) / K8) * 16 + (item & 15), k = t * SUBK + 8 * ((item >> 4) % K8);
             const bool ok = mm < M && k < p.K;
             const uint32_t off = (uint32_t)(((int64_t)mm * p.ldx + k) * (XF32 ? 4 : 2));
@@ -167,7 +225,7 @@ __global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x
     auto store_x = [&](const uint4 (&v)[XI][XW], uint8_t* xb) {
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
-            const int item = (int)threadIdx.x + 256 * i;
+            const int item = (int)threadIdx.x + 64 * W * i;
             const int m = item & 15, k8 = (item >> 4) % K8, tm = (item >> 4) / K8;
             uint4 parts[2];  // [0] = fp16 values (or the high parts), [1] = low parts
             if constexpr (XF32) {
@@ -202,59 +260,7 @@ __global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x
             }
         }
     };
-    // Decodes this lane's chunk(s) into the wave's B tile and scale table.
-    auto store_b = [&](const ChunkData<FMT>& d0) {
-        if constexpr (FMT == Q4_0 || FMT == Q4_K) {
-            const uint32_t neg = FMT == Q4_0 ? 0xD480E408u : 0xD400E400u;  // (-1032, -72) or (-1024, -64)
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-                const int b = 2 * lj + part;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    uint32_t o[4];
-                    nibbles_to_h(word(d0.q[part], q) ^ 0x88888888u, neg, o);
-                    *reinterpret_cast<uint4*>(bt + bt_unit<FMT>(b, q, ln)) = make_uint4(o[0], o[1], o[2], o[3]);
-                }
-            }
-            if constexpr (FMT == Q4_K) {
-                uint32_t sc0, m0, sc1, m1;
-                q4k_scales(d0.meta, lj, sc0, m0, sc1, m1);
-                const float dd = half_lo(d0.meta.x), dmin = half_hi(d0.meta.x);
-                scl[scl_index<FMT>(2 * lj, ln)] = make_float2(dd * (float)sc0, dmin * (float)m0);
-                scl[scl_index<FMT>(2 * lj + 1, ln)] = make_float2(dd * (float)sc1, dmin * (float)m1);
-            } else {
-                scl[scl_index<FMT>(2 * lj, ln)] = make_float2(half_lo(d0.meta.x), 0.f);
-                scl[scl_index<FMT>(2 * lj + 1, ln)] = make_float2(half_hi(d0.meta.x), 0.f);
-            }
-        } else if constexpr (FMT == Q8_0) {
-            const int b = lj;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                uint32_t o[4];
-                bytes_to_h(word(d0.q[q >> 1], 2 * (q & 1)), o[0], o[1]);
-                bytes_to_h(word(d0.q[q >> 1], 2 * (q & 1) + 1), o[2], o[3]);
-                *reinterpret_cast<uint4*>(bt + bt_unit<FMT>(b, q, ln)) = make_uint4(o[0], o[1], o[2], o[3]);
-            }
-            scl[scl_index<FMT>(b, ln)] = make_float2(half_lo(d0.meta.x), 0.f);
-        } else {  // Q6_K: four 16-weight scale groups per chunk
-            const float dd = half_lo(d0.meta.y);
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) {
-                const int g = 4 * lj + gg;
-                const uint32_t L0 = word(d0.q[gg >> 1], (gg & 1) * 2) ^ 0x88888888u;
-                const uint32_t L1 = word(d0.q[gg >> 1], (gg & 1) * 2 + 1) ^ 0x88888888u;
-                const uint32_t H = word(d0.q[2], gg);
-                uint32_t o[4], o2[4];
-                q6_to_h(L0, H & 0x33333333u, o);
-                q6_to_h(L1, (H >> 2) & 0x33333333u, o2);
-                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 0, ln)) = make_uint2(o[0], o[1]);
-                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 1, ln)) = make_uint2(o[2], o[3]);
-                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 2, ln)) = make_uint2(o2[0], o2[1]);
-                *reinterpret_cast<uint2*>(bt + bt_unit<FMT>(g, 3, ln)) = make_uint2(o2[2], o2[3]);
-                scl[scl_index<FMT>(g, ln)] = make_float2(dd * (float)(int8_t)((d0.meta.x >> (8 * gg)) & 0xffu), 0.f);
-            }
-        }
-    };
+    auto store_b = [&](const ChunkData<FMT>& d0) { decode_to_tile<FMT>(d0, ln, lj, bt, scl); };
 
     f4_t acc[NT];
 #pragma unroll
@@ -356,62 +362,273 @@ __global__ void __launch_bounds__(256) matvec_mfma(MvParams p, int M, uint32_t x
     }
 }
 
-size_t mfma_lds_bytes(int fmt, int xtype, int M) {
+// Split-K form for M <= 16 rows of fp16 activations. A workgroup of
+// kSplitK waves owns one 16-row stripe and its waves take interleaved
+// sub-steps of K, so a matrix of N rows runs N/16 x kSplitK independent waves
+// with no barrier inside the loop. Each lane loads its own matrix-core A
+// fragments (eight or four activation values per block) straight from the
+// cache hierarchy; the weights go through the wave's LDS tile as above. The
+// waves' 16x16 partial sums are added in wave order at the end.
+constexpr int kSplitK = 4;
+
+template <int FMT>
+struct SkLds {
+    using T = MfmaTraits<FMT>;
+    static constexpr int UB = T::KB == 32 ? 16 : 8;
+    static constexpr int BTILE = T::NB * 4 * kUnitPad * UB + 128;
+    static constexpr int SCALES = T::NB * 16 * 8 + 128;
+    static constexpr int WAVE = BTILE + SCALES;
+    static constexpr int RED = kSplitK * 64 * 16;  // partial sums, one f4 per lane and wave
+    static constexpr int TOTAL = kSplitK * WAVE + RED;
+};
+
+template <int FMT>
+__global__ void __launch_bounds__(64 * kSplitK) matvec_mfma_sk(MvParams p, int M, uint32_t x_bytes) {
+    using TR = MfmaTraits<FMT>;
+    using L = SkLds<FMT>;
+    constexpr int SUBK = TR::SUBK, NB = TR::NB, KB = TR::KB;
+    constexpr int DW = kWeightDepth;
+    extern __shared__ uint4 smem[];
+    uint8_t* lds = reinterpret_cast<uint8_t*>(smem);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint8_t* const bt = lds + wave * L::WAVE;
+    float2* const scl = reinterpret_cast<float2*>(bt + L::BTILE);
+    f4_t* const red = reinterpret_cast<f4_t*>(lds + kSplitK * L::WAVE);
+
+    const int64_t row0 = (int64_t)blockIdx.x * 16;
+    const int nch = p.P.nch;
+    const int steps = (nch + 3) / 4;
+    const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), (short)0, (int)x_bytes, 0x00020000);
+    const int ln = lane >> 2, lj = lane & 3;   // loader: row, chunk of the sub-step
+    const int mn = lane & 15, mq = lane >> 4;  // matrix core: row n / activation row m, k-slice
+    const int64_t lrow = row0 + ln;
+    const bool lrow_ok = lrow < p.rows;
+    const uint32_t xkeep = mn < M ? 0xFFFFFFFFu : 0u;
+
+    auto load_w = [&](int t, ChunkData<FMT>& d) {
+        const int c = t * 4 + lj;
+        load_chunk_rs<FMT>(rs, p.P, (uint32_t)lrow, c, lrow_ok && c < nch, d);
+    };
+    // A fragment of block b of sub-step t: activation row mn, values KB/4
+    // starting at k = t * SUBK + KB * b + (KB / 4) * mq.
+    using XF = typename std::conditional<KB == 32, h8_t, h4_t>::type;
+    auto load_x = [&](int t, XF (&a)[NB]) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int k = t * SUBK + KB * b + (KB / 4) * mq;
+            const uint32_t off = oob_unless((uint32_t)(((int64_t)mn * p.ldx + k) * 2), xkeep & (k < p.K ? 0xFFFFFFFFu : 0u));
+            if constexpr (KB == 32) {
+                a[b] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+            } else {
+                typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+                a[b] = __builtin_bit_cast(h4_t, __builtin_amdgcn_raw_buffer_load_b64(xrs, off, 0, 0));
+            }
+        }
+    };
+
+    f4_t acc = {0.f, 0.f, 0.f, 0.f};
+    auto multiply = [&](const XF (&a)[NB]) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float2 s = scl[scl_index<FMT>(b, mn)];
+            const f4_t z = {0.f, 0.f, 0.f, 0.f};
+            f4_t D, D2;
+            if constexpr (KB == 32) {
+                const h8_t B = *reinterpret_cast<const h8_t*>(bt + bt_unit<FMT>(b, mq, mn));
+                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[b], B, z, 0, 0, 0);
+                if constexpr (FMT == Q4_K) {
+                    const h8_t one = {1, 1, 1, 1, 1, 1, 1, 1};
+                    D2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[b], one, z, 0, 0, 0);
+                }
+            } else {
+                const h4_t B = *reinterpret_cast<const h4_t*>(bt + bt_unit<FMT>(b, mq, mn));
+                D = __builtin_amdgcn_mfma_f32_16x16x16f16(a[b], B, z, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = fmaf(s.x, D[j], acc[j]);
+                if constexpr (FMT == Q4_K) v = fmaf(-s.y, D2[j], v);
+                acc[j] = v;
+            }
+        }
+    };
+
+    // this wave's sub-steps: wave, wave + kSplitK, ...; every wave runs the
+    // same number of rounds, the sub-steps past K load nothing and add zero
+    const int per_wave = (steps + kSplitK - 1) / kSplitK;
+    const int rounds = (per_wave + DW - 1) / DW;
+    auto sub = [&](int i) { return wave + kSplitK * i; };
+    ChunkData<FMT> w[DW];
+    XF xr[2][NB];
+    load_x(sub(0), xr[0]);
+    load_x(sub(1), xr[1]);
+#pragma unroll
+    for (int i = 0; i < DW; ++i) load_w(sub(i), w[i]);
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+        for (int u = 0; u < DW; ++u) {
+            const int i = r * DW + u;
+            decode_to_tile<FMT>(w[u], ln, lj, bt, scl);
+            asm volatile("" ::: "memory");  // the tile is read back under other types
+            multiply(xr[u & 1]);
+            asm volatile("" ::: "memory");  // and rewritten by the next sub-step
+            load_w(sub(i + DW), w[u]);
+            load_x(sub(i + 2), xr[u & 1]);
+            // keep each sub-step's work together: without a barrier in the
+            // loop the scheduler would otherwise interleave sub-steps and run
+            // out of registers
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        f4_t t = red[lane];
+#pragma unroll
+        for (int v = 1; v < kSplitK; ++v) {
+            const f4_t o = red[v * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) t[j] += o[j];
+        }
+        const int64_t row = row0 + mn;
+        if (row < p.rows)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = 4 * mq + j;
+                if (m < M) p.y[(int64_t)m * p.ldy + row] = t[j];
+            }
+    }
+}
+
+template <int FMT>
+static hipError_t launch_mfma_sk(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
+                                 hipEvent_t ev1) {
+    const size_t lds = SkLds<FMT>::TOTAL;
+    auto kernel = matvec_mfma_sk<FMT>;
+    const int grid = (int)((p.rows + 15) / 16);
+    if (ev0 || ev1)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kSplitK), (uint32_t)lds, stream, ev0, ev1, 0u, p, M, x_bytes);
+    else
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kSplitK), lds, stream, p, M, x_bytes);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static size_t lds_of(bool f32, bool two, int W) {
+    if (W == 1 && (f32 || two)) W = 2;  // as launch_mfma_w
+#define RQ_LDS(NT, XF) (W == 1 ? MfmaLds<FMT, NT, XF, 1>::TOTAL : W == 2 ? MfmaLds<FMT, NT, XF, 2>::TOTAL : MfmaLds<FMT, NT, XF, 4>::TOTAL)
+    return two ? (f32 ? RQ_LDS(2, true) : RQ_LDS(2, false)) : (f32 ? RQ_LDS(1, true) : RQ_LDS(1, false));
+#undef RQ_LDS
+}
+
+// Waves (16-row stripes) per workgroup: four when there are rows enough to
+// give every CU a few workgroups, fewer for short matrices. RQMV_MFMA_WAVES
+// overrides it for tuning.
+static int mfma_waves(int64_t rows, int cus) {
+    const int64_t stripes = (rows + 15) / 16;
+    const char* env = getenv("RQMV_MFMA_WAVES");
+    if (env && *env) {
+        const int w = atoi(env);
+        if (w == 1 || w == 2 || w == 4) return w;
+    }
+    if (stripes >= (int64_t)6 * cus) return 4;
+    if (stripes >= (int64_t)3 * cus) return 2;
+    return 1;
+}
+
+size_t mfma_lds_bytes(int fmt, int xtype, int M, int64_t rows, int cus) {
     const bool f32 = xtype == X_F32, two = M > 16;
+    if (!two && !f32) {
+        const size_t sk = fmt == Q4_0 ? SkLds<Q4_0>::TOTAL : fmt == Q4_K ? SkLds<Q4_K>::TOTAL
+                        : fmt == Q8_0 ? SkLds<Q8_0>::TOTAL : fmt == Q6_K ? SkLds<Q6_K>::TOTAL : 0;
+        if (sk) return sk;  // (the larger of the two forms is below the LDS limit either way)
+    }
+    const int W = mfma_waves(rows, cus);
     switch (fmt) {
-        case Q4_0: return two ? (f32 ? MfmaLds<Q4_0, 2, true>::TOTAL : MfmaLds<Q4_0, 2, false>::TOTAL)
-                              : (f32 ? MfmaLds<Q4_0, 1, true>::TOTAL : MfmaLds<Q4_0, 1, false>::TOTAL);
-        case Q4_K: return two ? (f32 ? MfmaLds<Q4_K, 2, true>::TOTAL : MfmaLds<Q4_K, 2, false>::TOTAL)
-                              : (f32 ? MfmaLds<Q4_K, 1, true>::TOTAL : MfmaLds<Q4_K, 1, false>::TOTAL);
-        case Q8_0: return two ? (f32 ? MfmaLds<Q8_0, 2, true>::TOTAL : MfmaLds<Q8_0, 2, false>::TOTAL)
-                              : (f32 ? MfmaLds<Q8_0, 1, true>::TOTAL : MfmaLds<Q8_0, 1, false>::TOTAL);
-        case Q6_K: return two ? (f32 ? MfmaLds<Q6_K, 2, true>::TOTAL : MfmaLds<Q6_K, 2, false>::TOTAL)
-                              : (f32 ? MfmaLds<Q6_K, 1, true>::TOTAL : MfmaLds<Q6_K, 1, false>::TOTAL);
+        case Q4_0: return lds_of<Q4_0>(f32, two, W);
+        case Q4_K: return lds_of<Q4_K>(f32, two, W);
+        case Q8_0: return lds_of<Q8_0>(f32, two, W);
+        case Q6_K: return lds_of<Q6_K>(f32, two, W);
         default: return 0;
     }
 }
 
-template <int FMT, int NT, bool XF32>
+template <int FMT, int NT, bool XF32, int W>
 static hipError_t launch_mfma_one(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
                                   hipEvent_t ev1) {
-    const size_t lds = MfmaLds<FMT, NT, XF32>::TOTAL;
-    auto kernel = matvec_mfma<FMT, NT, XF32>;
+    const size_t lds = MfmaLds<FMT, NT, XF32, W>::TOTAL;
+    auto kernel = matvec_mfma<FMT, NT, XF32, W>;
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
     const int64_t stripes = (p.rows + 15) / 16;
-    const int grid = (int)((stripes + kMfmaWaves - 1) / kMfmaWaves);
+    const int grid = (int)((stripes + W - 1) / W);
     if (ev0 || ev1)
-        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), (uint32_t)lds, stream, ev0, ev1, 0u, p, M, x_bytes);
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * W), (uint32_t)lds, stream, ev0, ev1, 0u, p, M, x_bytes);
     else
-        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p, M, x_bytes);
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * W), lds, stream, p, M, x_bytes);
     return hipGetLastError();
 }
 
-template <int FMT>
-static hipError_t launch_mfma_fmt(int xtype, const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream,
-                                  hipEvent_t ev0, hipEvent_t ev1) {
-    if (M > 16) {
-        if (xtype == X_F32) return launch_mfma_one<FMT, 2, true>(p, M, x_bytes, stream, ev0, ev1);
-        return launch_mfma_one<FMT, 2, false>(p, M, x_bytes, stream, ev0, ev1);
-    }
-    if (xtype == X_F32) return launch_mfma_one<FMT, 1, true>(p, M, x_bytes, stream, ev0, ev1);
-    return launch_mfma_one<FMT, 1, false>(p, M, x_bytes, stream, ev0, ev1);
+// A single-wave workgroup stages all activations itself; it is kept to one
+// 16-row tile of fp16 activations, where that fits in registers.
+template <int NT, bool XF32>
+constexpr int min_waves() {
+    return NT == 1 && !XF32 ? 1 : 2;
 }
 
-hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, hipStream_t stream, hipEvent_t ev0,
-                              hipEvent_t ev1) {
+template <int FMT, int NT, bool XF32>
+static hipError_t launch_mfma_w(int W, const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
+                                hipEvent_t ev1) {
+    if (W == 4) return launch_mfma_one<FMT, NT, XF32, 4>(p, M, x_bytes, stream, ev0, ev1);
+    if constexpr (min_waves<NT, XF32>() == 1)
+        if (W == 1) return launch_mfma_one<FMT, NT, XF32, 1>(p, M, x_bytes, stream, ev0, ev1);
+    return launch_mfma_one<FMT, NT, XF32, 2>(p, M, x_bytes, stream, ev0, ev1);
+}
+
+template <int FMT>
+static hipError_t launch_mfma_fmt(int xtype, int W, const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream,
+                                  hipEvent_t ev0, hipEvent_t ev1) {
+    if (M > 16) {
+        if (xtype == X_F32) return launch_mfma_w<FMT, 2, true>(W, p, M, x_bytes, stream, ev0, ev1);
+        return launch_mfma_w<FMT, 2, false>(W, p, M, x_bytes, stream, ev0, ev1);
+    }
+    if (xtype == X_F32) return launch_mfma_w<FMT, 1, true>(W, p, M, x_bytes, stream, ev0, ev1);
+    return launch_mfma_w<FMT, 1, false>(W, p, M, x_bytes, stream, ev0, ev1);
+}
+
+hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, int cus, hipStream_t stream,
+                              hipEvent_t ev0, hipEvent_t ev1) {
     if (M < 1 || M > 32) return hipErrorInvalidValue;
     const size_t esize = xtype == X_F32 ? 4 : 2;
     const int64_t x_bytes = ((int64_t)(M - 1) * p.ldx + p.K) * (int64_t)esize;
     if (x_bytes >= (int64_t)kOobOffset) return hipErrorInvalidValue;
+    // Split-K for short and medium matrices (each wave re-reads its
+    // activations from the caches, which pays off while the stripes are too
+    // few to fill the GPU); the shared-staging form for tall ones.
+    // RQMV_MFMA_SK=0/1 forces either.
+    const char* sk_env = getenv("RQMV_MFMA_SK");
+    const bool sk = sk_env && *sk_env ? *sk_env != '0' : (p.rows + 15) / 16 <= (int64_t)4 * cus;
+    if (M <= 16 && xtype == X_F16 && sk) {
+        switch (fmt) {
+            case Q4_0: return launch_mfma_sk<Q4_0>(p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+            case Q4_K: return launch_mfma_sk<Q4_K>(p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+            case Q8_0: return launch_mfma_sk<Q8_0>(p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+            case Q6_K: return launch_mfma_sk<Q6_K>(p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    const int W = mfma_waves(p.rows, cus);
     switch (fmt) {
-        case Q4_0: return launch_mfma_fmt<Q4_0>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
-        case Q4_K: return launch_mfma_fmt<Q4_K>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
-        case Q8_0: return launch_mfma_fmt<Q8_0>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
-        case Q6_K: return launch_mfma_fmt<Q6_K>(xtype, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q4_0: return launch_mfma_fmt<Q4_0>(xtype, W, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q4_K: return launch_mfma_fmt<Q4_K>(xtype, W, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q8_0: return launch_mfma_fmt<Q8_0>(xtype, W, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
+        case Q6_K: return launch_mfma_fmt<Q6_K>(xtype, W, p, M, (uint32_t)x_bytes, stream, ev0, ev1);
         default: return hipErrorInvalidValue;
     }
 }

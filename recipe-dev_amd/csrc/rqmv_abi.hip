@@ -140,17 +140,19 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     p.ldx = ldx;
     p.ldy = ldy;
     int done = 0;
-    // Two or more activation rows of a quantized weight go to the matrix
-    // cores, up to 32 rows per launch.
-    const int mfma_min = env_int("RQMV_MFMA_MIN", 2);
+    // Three or more activation rows of a quantized weight go to the matrix
+    // cores, up to 32 rows per launch (at two the vector kernels are as fast).
+    const int mfma_min = env_int("RQMV_MFMA_MIN", 3);
     if (w->fmt != rq::F16 && m >= mfma_min) {
         while (done < m) {
             const int mb = m - done > 32 ? 32 : m - done;
-            if (rq::mfma_lds_bytes(w->fmt, xtype, mb) > info.lds_limit) return fail(RQMV_EINVAL, "LDS too small");
+            if (rq::mfma_lds_bytes(w->fmt, xtype, mb, rows, info.cus) > info.lds_limit)
+                return fail(RQMV_EINVAL, "LDS too small");
             p.x = static_cast<const char*>(x) + (size_t)done * (size_t)ldx * esize;
             p.y = y + (int64_t)done * ldy;
             const bool first = done == 0, last = done + mb >= m;
-            hipError_t e = rq::launch_matvec_mfma(w->fmt, xtype, mb, p, stream, first ? ev0 : nullptr, last ? ev1 : nullptr);
+            hipError_t e = rq::launch_matvec_mfma(w->fmt, xtype, mb, p, info.cus, stream, first ? ev0 : nullptr,
+                                                  last ? ev1 : nullptr);
             if (e != hipSuccess) return hip_fail(e, "matvec launch");
             done += mb;
         }

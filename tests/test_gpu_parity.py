@@ -140,6 +140,30 @@ def test_matvec_parity_matrix_core_sizes(gpu, fmt, xdt, m):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("form", ["split-k", "staged-1", "staged-2", "staged-4"])
+def test_matrix_core_forms(gpu, fmt, form, monkeypatch):
+    """Both matrix-core kernels, the split-K one and the staged one at every
+    workgroup size (RQMV_MFMA_SK, RQMV_MFMA_WAVES), with partial row tiles,
+    fp16 and fp32 activations, one and two 16-row tiles."""
+    if form == "split-k":
+        monkeypatch.setenv("RQMV_MFMA_SK", "1")
+        waves = "4"
+    else:
+        monkeypatch.setenv("RQMV_MFMA_SK", "0")
+        waves = form.split("-")[1]
+    monkeypatch.setenv("RQMV_MFMA_WAVES", waves)
+    rows, cols = (83, 768) if fmt in ("q4_k", "q6_k") else (83, 800)
+    w = _weights(fmt, rows, cols, seed=int(waves) + 7)
+    W = gpu.Weight(fmt, rows, cols, w)
+    for xdt in ("f16", "f32"):
+        for m in (5, 16, 27):
+            xh, dt, x32 = _x(m, cols, xdt, seed=m + 3)
+            y = _run_matvec(gpu, W, xh, dt, rows)
+            ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+            assert rel_l2(y, ref) <= 2e-4, (fmt, waves, xdt, m)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 def test_small_m_vector_path(gpu, fmt, monkeypatch):
     """RQMV_MFMA_MIN moves small M back to the vector kernels; both paths agree with the oracle."""
     monkeypatch.setenv("RQMV_MFMA_MIN", "99")
