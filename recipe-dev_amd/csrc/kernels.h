@@ -20,6 +20,11 @@ struct MvParams {
     float* y;
     int64_t ldy;
     int G;  // lanes that share one row (power of two, 8..64)
+    // F16 weights only: rows at or past `split` come from P2 (row - split), so
+    // that two weights of one width run as one launch (an MoE router and its
+    // shared-expert gate). split >= rows: P alone.
+    Planes P2;
+    int64_t split;
 };
 
 struct LaunchShape {

@@ -71,7 +71,14 @@ __device__ __forceinline__ void load_rows(const MvParams& p, const StepWalk& w, 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t row = row0 + r < p.rows ? row0 + r : p.rows - 1;
-        load_chunk<FMT>(p.P, row, c, d[r]);
+        if constexpr (FMT == F16) {
+            const bool second = row >= p.split;
+            Planes P = p.P;
+            P.base = second ? p.P2.base : p.P.base;
+            load_chunk<FMT>(P, second ? row - p.split : row, c, d[r]);
+        } else {
+            load_chunk<FMT>(p.P, row, c, d[r]);
+        }
     }
 }
 

@@ -31,13 +31,13 @@ struct MoeWorkspace {
 size_t moe_workspace_bytes(const MoeDims& d);
 MoeWorkspace moe_workspace(void* base, const MoeDims& d);
 
-// Top-k routing on one wave (amd-nv-cpu.ll:4489-4652 topk_forward_wave_body semantics).
-hipError_t launch_moe_topk(const MoeDims& d, MoeWorkspace ws, float* route_dense, hipStream_t stream);
-
-// h[slot][f] = silu(gate_slot[f] . x) * (up_slot[f] . x) for every routed slot and the shared expert.
+// Routes the position (ws.ids, ws.weights and route_dense when not null,
+// topk_forward_wave_body semantics, amd-nv-cpu.ll:4489-4652) and computes
+// h[slot][f] = silu(gate_slot[f] . x) * (up_slot[f] . x) for every routed slot
+// and the shared expert.
 hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
-                          const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws, int cus,
-                          hipStream_t stream);
+                          const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws,
+                          float* route_dense, int cus, hipStream_t stream);
 
 // y[n] = sum_slot w_slot * (down_slot[n] . h_slot), routed slots in ascending expert id, then the shared expert.
 hipError_t launch_moe_down(int fmt, const MoeDims& d, const MoeBank& down, const MoeBank& down_sh, MoeWorkspace ws,

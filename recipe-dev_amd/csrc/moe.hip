@@ -6,10 +6,11 @@
 // are topk_forward_wave_body (amd-nv-cpu.ll:4489-4652) and packed_lanes_body
 // modes 1/2 (amd-nv-cpu.ll:2897-2986, 3041-3086).
 //
-// Here the router runs as an F16 matvec, then:
-//   moe_topk  one wave: repeated wave argmax (the lower expert on a tie), the
-//             routing weights, slots in ascending expert id;
-//   moe_glu   one lane group per (slot, hidden row): the gate and up rows of the
+// Here the router and the shared expert's gate run as one F16 matvec, then:
+//   moe_glu   every wave first routes the position (a radix select of the k
+//             best scores, the lower expert on a tie; the routing weights;
+//             slots in ascending expert id), then one lane group per (slot,
+//             hidden row) reads the gate and up rows of the
 //             slot's expert are read together against x staged in LDS, and
 //             silu(gate) * up is written per slot (routed slots, then shared);
 //   moe_down  one lane group per output row: its lanes walk the chunks of every
@@ -43,138 +44,195 @@ MoeWorkspace moe_workspace(void* base, const MoeDims& d) {
 
 __device__ __forceinline__ float sigmoidf_dev(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-// (value, index) argmax across the wave; a higher value wins, the lower index on a tie.
+// (value, index) pair of the better expert: the higher score, the lower id on a tie.
+__device__ __forceinline__ void better_of(float& v, int& i, float pv, int pi) {
+    const bool take = pv > v || (pv == v && pi < i);
+    v = take ? pv : v;
+    i = take ? pi : i;
+}
+
+// One argmax step against the lane DPP control CTRL names (rows in ROW_MASK);
+// a lane without a source keeps its own pair.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+    const int vb = __builtin_bit_cast(int, v);
+    const float pv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(vb, vb, CTRL, ROW_MASK, 0xf, false));
+    const int pi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false);
+    better_of(v, i, pv, pi);
+}
+
+// The best (value, index) of the wave, in every lane: pairs within quads,
+// half rows and rows, then rows 0-1 into row 1, rows 2-3 into row 3 and row 1
+// into row 3 (the DPP pattern of a wave scan), read back from lane 63.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off);
-        const int oi = __shfl_xor(i, off);
-        const bool take = (oi >= 0) && (i < 0 || ov > v || (ov == v && oi < i));
-        if (take) {
-            v = ov;
-            i = oi;
-        }
-    }
+    argmax_dpp<0xB1, 0xF>(v, i);   // quad_perm [1,0,3,2]
+    argmax_dpp<0x4E, 0xF>(v, i);   // quad_perm [2,3,0,1]
+    argmax_dpp<0x141, 0xF>(v, i);  // row_half_mirror
+    argmax_dpp<0x140, 0xF>(v, i);  // row_mirror
+    argmax_dpp<0x142, 0xA>(v, i);  // row_bcast:15
+    argmax_dpp<0x143, 0xC>(v, i);  // row_bcast:31
+    v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    i = __builtin_amdgcn_readlane(i, 63);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+// Sum over the wave in a fixed DPP order, in every lane.
+__device__ __forceinline__ float wave_sum_fixed(float v) {
+    v = group_sum(v, 64);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+// Top-k routing (topk_forward_body semantics, amd-nv-cpu.ll:4486-4716) on one
+// wave. The router scores sit in registers (expert lane + 64 j in v[j]) as
+// order-preserving 32-bit keys; a radix select over the 32 key bits (one
+// ballot and population count per register per bit) finds the k-th largest
+// key T; the experts above T are kept, and of those equal to T the lowest ids,
+// so a tie goes to the lower expert. Slots are the kept experts in ascending
+// id, counted from the ballots. The picked ids go to the wave's `slot_ids`
+// (LDS); with `publish` the wave also writes the routing (ids, weights, the
+// shared expert's weight, the dense routing plane) to the workspace. Sums run
+// in a fixed order, so the weights are deterministic.
+constexpr int kTopkMaxExperts = 2048;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Experts per lane: E <= 64 * kTopkSlots.
-constexpr int kTopkSlots = 32;
+// Lanes below this one whose bit is set in `mask`.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
 
-__global__ void __launch_bounds__(64) moe_topk_kernel(MoeDims d, MoeWorkspace ws, float* route_dense) {
-    __shared__ int pick_id[64];
-    __shared__ float pick_val[64];
-    const int lane = threadIdx.x;
-    const int E = d.experts;
-    uint32_t taken = 0;  // bit i: expert lane + 64 i already picked
-    for (int p = 0; p < d.top; ++p) {
-        float bv = 0.f;
-        int bi = -1;
-        for (int i = 0; i < kTopkSlots; ++i) {
-            const int e = lane + 64 * i;
-            if (e >= E) break;
-            if (taken & (1u << i)) continue;
-            const float v = ws.logits[e];
-            if (bi < 0 || v > bv) {  // ascending e: keeps the lower expert on a tie
-                bv = v;
-                bi = e;
-            }
-        }
-        wave_argmax(bv, bi);
-        if (bi >= 0 && (bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == 0) {
-            pick_id[p] = bi;
-            pick_val[p] = bv;
-        }
-    }
-    __syncthreads();
+template <int S>
+__device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace& ws, float* route_dense, bool publish,
+                                           int* slot_ids) {
+    const int lane = threadIdx.x & 63;
+    const int E = d.experts, k = d.top;
     const bool sigmoid = d.scoring != 0, renorm = d.renormalize != 0;
+    float v[S];
+    uint32_t key[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = ws.logits[e < E ? e : E - 1];
+        key[j] = e < E ? order_key(v[j]) : 0u;  // an absent expert ranks below every score
+    }
+    const float shared_logit = ws.logits[E];  // read early; used only with a gated shared expert
+    // T = the largest key with at least k keys >= T
+    uint32_t T = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = T | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < S; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+        if (cnt >= k) T = cand;
+    }
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < S; ++j) above += __popcll(__ballot(key[j] > T));
+    // keep every key above T and the (k - above) lowest-id keys equal to T;
+    // slot = kept experts of lower id
+    int need = k - above, kept_before = 0;
+    bool kept[S];
+    int slot[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const uint64_t eq = __ballot(key[j] == T);
+        const bool take_eq = key[j] == T && lanes_below(eq) < need;
+        kept[j] = key[j] > T || take_eq;
+        const int taken_eq = __popcll(eq) < need ? __popcll(eq) : need;
+        need -= taken_eq;
+        const uint64_t km = __ballot(kept[j]);
+        slot[j] = kept_before + lanes_below(km);
+        kept_before += __popcll(km);
+    }
     // Maximum and total over the kept experts (renormalized) or over all.
-    float maximum, total;
-    if (renorm) {
-        maximum = pick_val[0];
-        float t = 0.f;
-        for (int p = lane; p < d.top; p += 64) t += sigmoid ? sigmoidf_dev(pick_val[p]) : expf(pick_val[p] - maximum);
-        total = wave_sum(t);
-    } else {
-        float mx = -INFINITY;
-        for (int e = lane; e < E; e += 64) mx = fmaxf(mx, ws.logits[e]);
-        maximum = wave_max(mx);
-        float t = 0.f;
-        for (int e = lane; e < E; e += 64) t += sigmoid ? sigmoidf_dev(ws.logits[e]) : expf(ws.logits[e] - maximum);
-        total = wave_sum(t);
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+        if ((renorm ? kept[j] : lane + 64 * j < E)) m = fmaxf(m, v[j]);
+    float mx = m;
+    {
+        int ii = 0;
+        wave_argmax(mx, ii);
     }
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+        if ((renorm ? kept[j] : lane + 64 * j < E)) t += sigmoid ? sigmoidf_dev(v[j]) : expf(v[j] - mx);
+    const float total = wave_sum_fixed(t);
     const float denom = (renorm || !sigmoid) ? total : 1.0f;
-    if (route_dense)
-        for (int e = lane; e < E; e += 64) route_dense[e] = 0.f;
-    __syncthreads();
-    for (int p = lane; p < d.top; p += 64) {
-        const int id = pick_id[p];
-        int slot = 0;  // rank of this expert among the picked ids
-        for (int q = 0; q < d.top; ++q) slot += pick_id[q] < id;
-        const float raw = sigmoid ? sigmoidf_dev(pick_val[p]) : expf(pick_val[p] - maximum);
-        const float w = raw / denom * d.scale;
-        ws.ids[slot] = id;
-        ws.weights[slot] = w;
-        if (route_dense) route_dense[id] = w;
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+        if (kept[j]) slot_ids[slot[j]] = lane + 64 * j;
+    if (publish) {
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int e = lane + 64 * j;
+            if (e >= E) continue;
+            const float raw = sigmoid ? sigmoidf_dev(v[j]) : expf(v[j] - mx);
+            const float w = raw / denom * d.scale;
+            if (kept[j]) {
+                ws.ids[slot[j]] = e;
+                ws.weights[slot[j]] = w;
+            }
+            if (route_dense) route_dense[e] = kept[j] ? w : 0.f;
+        }
+        // The shared expert's weight: its gate's Sigmoid activation, 0.5 (tanh(v/2) + 1)
+        // (recipe.rs:22662-22668), or 1 when it has no gate.
+        if (lane == 0 && d.hidden_shared > 0)
+            ws.weights[k] = d.shared_gated ? 0.5f * (tanhf(0.5f * shared_logit) + 1.0f) : 1.0f;
     }
-    // The shared expert's weight: its gate's Sigmoid activation, 0.5 (tanh(v/2) + 1)
-    // (recipe.rs:22662-22668), or 1 when it has no gate.
-    if (lane == 0 && d.hidden_shared > 0)
-        ws.weights[d.top] = d.shared_gated ? 0.5f * (tanhf(0.5f * ws.logits[E]) + 1.0f) : 1.0f;
 }
 
-template <int FMT, bool XF32>
+template <int FMT, bool XF32, int S>
 __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
-                                                       MoeBank up_sh, const void* x, MoeWorkspace ws, int G) {
+                                                       MoeBank up_sh, const void* x, MoeWorkspace ws, float* route_dense,
+                                                       int G) {
     constexpr int XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
+    __shared__ int slot_ids_all[4][64];
     const int nch = gate.P.nch;
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
-    stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, xd, reinterpret_cast<float*>(xb));
-    __syncthreads();
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
     const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
     const int routed = d.top * d.hidden;
     const int total_rows = routed + d.hidden_shared;
     const int rows_per_wave = 64 / G;
     const int tiles = (total_rows + rows_per_wave - 1) / rows_per_wave;
-    for (int tile = blockIdx.x * wpb + wave; tile < tiles; tile += gridDim.x * wpb) {
-        const int r = tile * rows_per_wave + sub;
-        if (r >= total_rows) continue;  // whole lane group idles; reductions stay inside the group
-        Planes pg, pu;
-        int64_t rg, ru;
+    // Every wave routes the position itself (a few microseconds of one wave,
+    // instead of a launch and a round trip through memory); the first wave of
+    // the first workgroup also writes the routing out for the down kernel.
+    int* const slot_ids = slot_ids_all[wave];
+    route_wave<S>(d, ws, route_dense, blockIdx.x == 0 && wave == 0, slot_ids);
+    // Row r of the gate/up stack: hidden row f of routed slot s, or of the shared expert.
+    auto fetch = [&](int r, int c, ChunkData<FMT>& dg, ChunkData<FMT>& du) {
+        r = r < total_rows ? r : total_rows - 1;
+        c = c < nch ? c : nch - 1;
         if (r < routed) {
             const int s = r / d.hidden, f = r % d.hidden;
-            const int64_t e = ws.ids[s];
-            pg = gate.P;
-            pu = up.P;
-            rg = e * gate.rows + f;
-            ru = e * up.rows + f;
+            const int64_t e = slot_ids[s];
+            load_chunk<FMT>(gate.P, e * gate.rows + f, c, dg);
+            load_chunk<FMT>(up.P, e * up.rows + f, c, du);
         } else {
-            const int f = r - routed;
-            pg = gate_sh.P;
-            pu = up_sh.P;
-            rg = f;
-            ru = f;
+            load_chunk<FMT>(gate_sh.P, r - routed, c, dg);
+            load_chunk<FMT>(up_sh.P, r - routed, c, du);
         }
+    };
+    int tile = blockIdx.x * wpb + wave;
+    // the first chunk's weights are requested before the activations are staged
+    ChunkData<FMT> dg, du;
+    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, dg, du);
+    stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, xd, reinterpret_cast<float*>(xb));
+    __syncthreads();
+    bool fetched = true;
+    for (; tile < tiles; tile += gridDim.x * wpb) {
+        const int r = tile * rows_per_wave + sub;
         float ag = 0.f, au = 0.f;
         for (int c = g; c < nch; c += G) {
-            ChunkData<FMT> dg, du;
-            load_chunk<FMT>(pg, rg, c, dg);
-            load_chunk<FMT>(pu, ru, c, du);
+            if (!fetched) fetch(r, c, dg, du);
+            fetched = false;
             uint4 xv[1][XP];
             uint4 bv[1][2];
 #pragma unroll
@@ -184,9 +242,10 @@ __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, M
             dot_int<FMT, 1>(dg, c, xv, bv, &ag);
             dot_int<FMT, 1>(du, c, xv, bv, &au);
         }
+        fetched = false;
         ag = group_sum(ag, G);
         au = group_sum(au, G);
-        if (g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
+        if (r < total_rows && g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
     }
 }
 
@@ -201,30 +260,40 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, 
     const int routed_ch = d.top * cps;
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
-    stage_all<FMT, true>(nch, K, ws.h, 0, 1, xd, reinterpret_cast<float*>(xb));
-    __syncthreads();
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
     const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
     const int rows_per_wave = 64 / G;
     const int tiles = (d.d_model + rows_per_wave - 1) / rows_per_wave;
-    for (int tile = blockIdx.x * wpb + wave; tile < tiles; tile += gridDim.x * wpb) {
+    // Chunk c of output row n: chunk lc of slot s's expert down row, or of the shared expert's.
+    auto fetch = [&](int n, int c, ChunkData<FMT>& cd, float& w, int& lc) {
+        n = n < d.d_model ? n : d.d_model - 1;
+        c = c < nch ? c : nch - 1;
+        if (c < routed_ch) {
+            const int s = c / cps;
+            lc = c - s * cps;
+            load_chunk<FMT>(down.P, (int64_t)ws.ids[s] * down.rows + n, lc, cd);
+            w = ws.weights[s];
+        } else {
+            lc = c - routed_ch;
+            load_chunk<FMT>(down_sh.P, n, lc, cd);
+            w = ws.weights[d.top];
+        }
+    };
+    int tile = blockIdx.x * wpb + wave;
+    // the first chunk's weights are requested before the slot activations are staged
+    ChunkData<FMT> cd;
+    float w;
+    int lc;
+    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd, w, lc);
+    stage_all<FMT, true>(nch, K, ws.h, 0, 1, xd, reinterpret_cast<float*>(xb));
+    __syncthreads();
+    bool fetched = true;
+    for (; tile < tiles; tile += gridDim.x * wpb) {
         const int n = tile * rows_per_wave + sub;
-        if (n >= d.d_model) continue;
         float acc = 0.f;
         for (int c = g; c < nch; c += G) {
-            ChunkData<FMT> cd;
-            float w;
-            int lc;
-            if (c < routed_ch) {
-                const int s = c / cps;
-                lc = c - s * cps;
-                load_chunk<FMT>(down.P, (int64_t)ws.ids[s] * down.rows + n, lc, cd);
-                w = ws.weights[s];
-            } else {
-                lc = c - routed_ch;
-                load_chunk<FMT>(down_sh.P, n, lc, cd);
-                w = ws.weights[d.top];
-            }
+            if (!fetched) fetch(n, c, cd, w, lc);
+            fetched = false;
             uint4 xv[1][XP];
             uint4 bv[1][2];
 #pragma unroll
@@ -235,15 +304,10 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, 
             dot_int<FMT, 1>(cd, lc, xv, bv, &part);
             acc = fmaf(w, part, acc);
         }
+        fetched = false;
         acc = group_sum(acc, G);
-        if (g == G - 1) y[n] = acc;
+        if (n < d.d_model && g == G - 1) y[n] = acc;
     }
-}
-
-hipError_t launch_moe_topk(const MoeDims& d, MoeWorkspace ws, float* route_dense, hipStream_t stream) {
-    if (d.experts > 64 * kTopkSlots || d.top > 64 || d.top < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(64), 0, stream, d, ws, route_dense);
-    return hipGetLastError();
 }
 
 static int lanes_for(int64_t nch) {
@@ -252,9 +316,10 @@ static int lanes_for(int64_t nch) {
     return G;
 }
 
-template <int FMT>
-static hipError_t glu_fmt(int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
-                          const MoeBank& up_sh, const void* x, MoeWorkspace ws, int cus, hipStream_t stream) {
+template <int FMT, bool XF32, int S>
+static hipError_t glu_launch(const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
+                             const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense, int cus,
+                             hipStream_t stream) {
     const int nch = gate.P.nch;
     const int G = lanes_for(nch);
     const int total_rows = d.top * d.hidden + d.hidden_shared;
@@ -262,29 +327,48 @@ static hipError_t glu_fmt(int xtype, const MoeDims& d, const MoeBank& gate, cons
     int grid = (total_rows + rows_per_block - 1) / rows_per_block;
     if (grid > cus * 8) grid = cus * 8;
     const size_t lds = stage_bytes_int(FMT, 1, nch);
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(xtype == 0 ? reinterpret_cast<const void*>(&moe_glu_kernel<FMT, true>)
-                                                       : reinterpret_cast<const void*>(&moe_glu_kernel<FMT, false>),
+    auto kernel = moe_glu_kernel<FMT, XF32, S>;
+    if (lds > 60000) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    if (xtype == 0)
-        hipLaunchKernelGGL((moe_glu_kernel<FMT, true>), dim3(grid), dim3(256), lds, stream, d, gate, up, gate_sh, up_sh,
-                           x, ws, G);
-    else
-        hipLaunchKernelGGL((moe_glu_kernel<FMT, false>), dim3(grid), dim3(256), lds, stream, d, gate, up, gate_sh,
-                           up_sh, x, ws, G);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, stream, d, gate, up, gate_sh, up_sh, x, ws, route_dense, G);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
-                          const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws, int cus,
+template <int FMT, bool XF32>
+static hipError_t glu_slots(const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
+                            const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense, int cus,
+                            hipStream_t stream) {
+    const int slots = (d.experts + 63) / 64;
+#define RQ_GLU(S) glu_launch<FMT, XF32, S>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream)
+    if (slots <= 1) return RQ_GLU(1);
+    if (slots <= 2) return RQ_GLU(2);
+    if (slots <= 4) return RQ_GLU(4);
+    if (slots <= 8) return RQ_GLU(8);
+    if (slots <= 16) return RQ_GLU(16);
+    return RQ_GLU(32);
+#undef RQ_GLU
+}
+
+template <int FMT>
+static hipError_t glu_fmt(int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
+                          const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense, int cus,
                           hipStream_t stream) {
+    if (d.experts > kTopkMaxExperts || d.top > 64 || d.top < 1) return hipErrorInvalidValue;
+    if (xtype == 0) return glu_slots<FMT, true>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+    return glu_slots<FMT, false>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+}
+
+hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
+                          const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws,
+                          float* route_dense, int cus, hipStream_t stream) {
     switch (fmt) {
-        case Q4_0: return glu_fmt<Q4_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, cus, stream);
-        case Q8_0: return glu_fmt<Q8_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, cus, stream);
-        case Q4_K: return glu_fmt<Q4_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, cus, stream);
-        case Q6_K: return glu_fmt<Q6_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, cus, stream);
+        case Q4_0: return glu_fmt<Q4_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+        case Q8_0: return glu_fmt<Q8_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+        case Q4_K: return glu_fmt<Q4_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+        case Q6_K: return glu_fmt<Q6_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
         default: return hipErrorInvalidValue;
     }
 }

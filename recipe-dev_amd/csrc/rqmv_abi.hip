@@ -125,7 +125,7 @@ int check_launch(const rqmv_weight* w, DeviceInfo* info) {
 // at a time in blocks the VALU kernels take (8, 4, 2, 1) and LDS can hold.
 int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const void* x, int xtype, int m, int64_t ldx,
                 float* y, int64_t ldy, hipStream_t stream, const DeviceInfo& info, hipEvent_t ev0 = nullptr,
-                hipEvent_t ev1 = nullptr) {
+                hipEvent_t ev1 = nullptr, const rqmv_weight* extra_row = nullptr) {
     if (!x || !y) return fail(RQMV_EINVAL, "x or y is NULL");
     if (xtype != RQMV_DTYPE_F16 && xtype != RQMV_DTYPE_F32) return fail(RQMV_EINVAL, "x_dtype must be F16 or F32");
     if (m <= 0) return fail(RQMV_EINVAL, "m must be positive");
@@ -135,6 +135,14 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
         return fail(RQMV_EINVAL, "x rows must start 16-byte aligned (x and ldx * element size)");
     rq::MvParams p;
     p.P = planes_of(w, first_row);
+    p.P2 = p.P;
+    p.split = rows;
+    if (extra_row) {  // one more output row from a second F16 weight of the same width
+        if (w->fmt != rq::F16 || extra_row->fmt != rq::F16 || extra_row->cols != w->cols || m != 1)
+            return fail(RQMV_EINVAL, "an extra row needs two F16 weights of one width and one activation row");
+        p.P2 = planes_of(extra_row, 0);
+        rows += 1;
+    }
     p.rows = rows;
     p.K = (int)w->cols;
     p.ldx = ldx;
@@ -382,18 +390,16 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
         if (w && w->device != params->router->device) return fail(RQMV_ESTATE, "moe weights live on different devices");
     hipStream_t s = static_cast<hipStream_t>(stream);
     rq::MoeWorkspace ws = rq::moe_workspace(workspace, d);
-    rc = matvec_rows(params->router, 0, d.experts, x_dev, x_dtype, 1, d.d_model, ws.logits, d.experts, s, info);
+    // router logits and the shared expert's gate logit: one F16 launch over
+    // both weights (experts + 1 rows)
+    rc = matvec_rows(params->router, 0, d.experts, x_dev, x_dtype, 1, d.d_model, ws.logits, d.experts, s, info,
+                     nullptr, nullptr, params->shared_gate_inp);
     if (rc != RQMV_OK) return rc;
-    if (params->shared_gate_inp) {
-        rc = matvec_rows(params->shared_gate_inp, 0, 1, x_dev, x_dtype, 1, d.d_model, ws.logits + d.experts, 1, s, info);
-        if (rc != RQMV_OK) return rc;
-    }
-    hipError_t e = rq::launch_moe_topk(d, ws, route_dev, s);
-    if (e != hipSuccess) return hip_fail(e, "moe top-k launch");
     const int fmt = params->gate_exps->fmt;
-    e = rq::launch_moe_glu(fmt, x_dtype, d, bank_of(params->gate_exps), bank_of(params->up_exps),
-                           bank_of(params->gate_shexp), bank_of(params->up_shexp), x_dev, ws, info.cus, s);
-    if (e != hipSuccess) return hip_fail(e, "moe gate/up launch");
+    hipError_t e = rq::launch_moe_glu(fmt, x_dtype, d, bank_of(params->gate_exps), bank_of(params->up_exps),
+                                      bank_of(params->gate_shexp), bank_of(params->up_shexp), x_dev, ws, route_dev,
+                                      info.cus, s);
+    if (e != hipSuccess) return hip_fail(e, "moe routing and gate/up launch");
     e = rq::launch_moe_down(fmt, d, bank_of(params->down_exps), bank_of(params->down_shexp), ws, y_dev, info.cus, s);
     if (e != hipSuccess) return hip_fail(e, "moe down launch");
     return RQMV_OK;
