@@ -201,12 +201,133 @@ def moe_bench(args):
     graph.close()
 
 
+def decode_bench(args):
+    """Single-token decode of a random-init 32-layer decoder: d 4096, 32 query
+    and 8 kv heads of 128, NeoX rotary (base 500000), SiLU-GLU of 14336,
+    RMSNorm eps 1e-5, every projection Q4_K (fused QKV and gate|up), the
+    128256-token head Q8_0, an fp16 KV cache prefilled N(0, 1) to 4096
+    positions. A step is one token: embedding row, 32 layers, final norm,
+    head, argmax, position advance, replayed from one captured HIP graph with
+    the token and position in device memory (greedy decoding). Every layer
+    holds its own weight bytes (about 5 GB streamed per token), so nothing is
+    served from the Infinity Cache."""
+    import rqmv
+    from rqmv import synth
+    from rqmv.decode import DecodeModel, DecoderShape
+
+    shape = DecoderShape()
+    ctx = 4096
+    max_ctx = ctx + args.warmup + args.steps + 8
+    rqmv.init(0)
+    log(f"bench: decode_c5 layers={shape.layers} d={shape.d} ctx={ctx} steps={args.steps} warmup={args.warmup}")
+    t0 = time.perf_counter()
+    D = synth.DecoderSynth(shape)
+    model = DecodeModel(shape, max_ctx, D.embed(), D.out_norm(), D.head())
+    layer0 = None
+    for i in range(shape.layers):
+        t = D.layer(i)
+        model.set_layer(i, t)
+        model.set_cache(i, *D.cache(i, ctx))
+        if i == 0:
+            layer0 = t
+    rqmv.synchronize()
+    log(f"bench: model built in {time.perf_counter() - t0:.1f} s")
+    stream = rqmv.Stream()
+    model.set_position(1, ctx)
+    model.enqueue_step(stream)  # one eager step first
+    stream.synchronize()
+    logits = model.read_logits()
+    tok = model.read_token()
+    ok = bool(np.isfinite(logits).all()) and tok == int(np.argmax(logits)) and model.read_position() == ctx + 1
+    log(f"bench: eager step token {tok} finite={bool(np.isfinite(logits).all())} consistent={ok}")
+    if not ok and not args.no_check:
+        log("bench: decode step check failed")
+        sys.exit(1)
+    graph = model.capture(stream)
+    for _ in range(args.warmup):
+        graph.launch(stream)
+    stream.synchronize()
+    pos0 = model.read_position()
+    e0, e1 = rqmv.Event(), rqmv.Event()
+    e0.record(stream)
+    for _ in range(args.steps):
+        graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    total_ms = e0.elapsed_ms(e1)
+    ms_per_step = total_ms / args.steps
+    tok_s = 1000.0 / ms_per_step
+    assert model.read_position() == pos0 + args.steps
+    # bytes one token streams: every projection and the head as stored, the
+    # KV cache up to the position (keys and values, fp16), embedding row,
+    # norm scales, activations in and out of each projection
+    s = shape
+    mean_len = pos0 + (args.steps + 1) / 2.0
+    kv_bytes = s.layers * 2 * s.kv_heads * mean_len * s.head_dim * 2
+    small = s.d * 4 + (2 * s.layers + 1) * s.d * 4
+    bytes_per_token = model.weight_bytes() + kv_bytes + small
+    achieved = bytes_per_token * tok_s / 1e9
+    log(f"bench: {args.steps} steps {total_ms:.2f} ms -> {ms_per_step * 1e3:.1f} us/token, {tok_s:.1f} tok/s, "
+        f"{achieved:.0f} GB/s over {bytes_per_token / 1e9:.3f} GB/token")
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "single-token decode, random-init 32-layer decoder: d 4096, 32/8 heads of 128, "
+                               "NeoX rotary base 500000, SiLU-GLU 14336, RMSNorm 1e-5, Q4_K projections, "
+                               "Q8_0 head 128256, fp16 KV cache prefilled to 4096",
+                   "bytes_per_token": int(bytes_per_token), "positions": [pos0, pos0 + args.steps - 1],
+                   "launches_per_token": 4 + 10 * s.layers + 1, "activations": "f32", "kv_cache": "f16",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "note": "whole token (every launch of the step) from graph replays"},
+    }
+    if not args.no_cpu:
+        import oracle
+
+        cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+        # recipe's CPU float path on layer 0's four projections, timed per layer
+        # and scaled to 32 layers, plus the head, plus f64 attention over one
+        # layer's cache scaled to 32 layers
+        xs = {"qkv": s.d, "o": s.d, "gate_up": s.d, "down": s.ffn}
+        rows = {"qkv": s.qkv_rows, "o": s.d, "gate_up": 2 * s.ffn, "down": s.d}
+        rng = np.random.default_rng(0)
+        t0 = time.perf_counter()
+        runs = 0
+        while time.perf_counter() - t0 < args.cpu_seconds * 0.6:
+            for k in ("qkv", "o", "gate_up", "down"):
+                oracle.matvec_recipe_f32(s.proj_fmt, getattr(layer0, k), rows[k], xs[k],
+                                         rng.standard_normal(xs[k]).astype(np.float32), threads=cores)
+            runs += 1
+        layer_s = (time.perf_counter() - t0) / runs
+        head = D.head()
+        t0 = time.perf_counter()
+        oracle.matvec_recipe_f32(s.head_fmt, head, s.vocab, s.d, rng.standard_normal(s.d).astype(np.float32),
+                                 threads=cores)
+        head_s = time.perf_counter() - t0
+        from oracle import decode as oref
+        kc, vc = D.cache(0, ctx)
+        q = rng.standard_normal((s.q_heads, s.head_dim))
+        t0 = time.perf_counter()
+        oref.attention(q, kc.view(np.float16).astype(np.float32), vc.view(np.float16).astype(np.float32), ctx)
+        attn_s = time.perf_counter() - t0
+        token_s = s.layers * (layer_s + attn_s) + head_s
+        out["cpu_baseline"] = {
+            "value": round(1.0 / token_s, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"layer-0 projections x{runs} ({layer_s * 1e3:.0f} ms/layer, recipe fp32 float path), head "
+                      f"once ({head_s * 1e3:.0f} ms), attention over 4096 positions once ({attn_s * 1e3:.0f} ms, "
+                      f"numpy), scaled to 32 layers; {cores} threads"}
+    print(json.dumps(out), flush=True)
+    graph.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="q4_k_up", choices=sorted(WORKLOADS) + ["moe_c4"])
+    ap.add_argument("--workload", default="q4_k_up", choices=sorted(WORKLOADS) + ["moe_c4", "decode_c5"])
     ap.add_argument("--m", type=int, default=1, help="activation rows")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -226,6 +347,9 @@ def main():
 
     if args.workload == "moe_c4":
         moe_bench(args)
+        return
+    if args.workload == "decode_c5":
+        decode_bench(args)
         return
 
     import rqmv

@@ -139,6 +139,46 @@ int rqmv_moe_workspace_size(const rqmv_moe_params* params, size_t* bytes);
 int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,
              void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode-step helpers. They have no counterpart at the matrix-vector
+ * boundary: they run the rest of a decoder layer on the device between the
+ * projections, for the end-to-end single-token decode, with the semantics of
+ * recipe's attention block and feed-forward (lower_attention,
+ * recipe.rs:23056-23150; silu(gate) * up, 23279-23286, 22662-22668). All
+ * pointers are device pointers; `pos` points to a device int32 holding the
+ * token's position (so that a captured step replays at the next position
+ * after rqmv_advance). Activations are fp32; the KV cache is fp16, laid out
+ * [kv head][position][head_dim] with max_ctx positions per head. */
+
+/* x += delta (delta may be NULL); out = x / sqrt(mean(x^2) + eps) * weight. */
+int rqmv_add_rmsnorm(float* x, const float* delta, const float* weight, int n, float eps, float* out, void* stream);
+
+/* NeoX rotary on the q and k heads of qkv ([q | k | v] heads of head_dim, in
+ * place; pair i turns by pos * base^(-2i/head_dim)), then the rotated keys and
+ * the values are stored in the caches at pos (nothing is stored when pos is
+ * outside 0..max_ctx-1). */
+int rqmv_rope_kv(float* qkv, const int* pos, int q_heads, int kv_heads, int head_dim, double base, void* k_cache,
+                 void* v_cache, int max_ctx, void* stream);
+
+/* Grouped-query attention of one query (q_heads x head_dim) over positions
+ * 0..min(pos, max_ctx - 1) of the cache: softmax(q k / sqrt(head_dim)) v per
+ * query head. head_dim is a multiple of 64 up to 256; at most 8 query heads
+ * share a kv head. */
+int rqmv_attention_workspace_size(int q_heads, int head_dim, int max_ctx, size_t* bytes);
+int rqmv_attention(const float* q, const void* k_cache, const void* v_cache, const int* pos, int q_heads, int kv_heads,
+                   int head_dim, int max_ctx, void* workspace, size_t workspace_bytes, float* out, void* stream);
+
+/* out[i] = silu(gate_up[i]) * gate_up[n + i]. */
+int rqmv_silu_mul(const float* gate_up, int n, float* out, void* stream);
+
+/* *out = the index of the largest value (the lowest index on a tie). */
+int rqmv_argmax(const float* values, int n, int* out, void* stream);
+
+/* out = table[token mod rows] (rows x n fp32): the next token's embedding. */
+int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, void* stream);
+
+/* *pos += 1 on the device (the last launch of a captured decode step). */
+int rqmv_advance(int* pos, void* stream);
+
 /* Host-only loader functions (no device needed): the repacked layout's size
  * and the repack / unpack themselves, for inspection and testing. */
 int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* bytes);

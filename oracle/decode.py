@@ -1,0 +1,131 @@
+"""f64 restatement of one single-token decode step of a llama-style decoder.
+
+TEST INFRASTRUCTURE ONLY: the checker of the device decode step (tests/ and
+smoke()); the product never imports it.
+
+Semantics (recipe's attention block and feed-forward, one position at a time):
+- RMSNorm: x / sqrt(mean(x^2) + eps) * scale (lower_normalize,
+  recipe.rs:23190-23210; emit_normalize_stats, recipe.rs:6836-6870).
+- Fused QKV projection laid out [q heads | k heads | v heads]; rotary on
+  queries and keys; scores q.k / sqrt(head_dim); softmax over positions
+  0..pos; weighted sum of values; output projection (lower_attention,
+  recipe.rs:23056-23150).
+- NeoX rotary without yarn (rope_pair, amd-nv-cpu.ll:3719-3780): pair i of a
+  head is (x_i, x_{i+half}), angle = pos * exp(-(2i/dims) * log(base)),
+  lower = a cos - b sin, upper = b cos + a sin.
+- SiLU-GLU: silu(gate) * up with silu(v) = v * sigmoid(v)
+  (recipe.rs:23279-23286, 22662-22668).
+- The KV cache stores fp16: the appended key (after rotation) and value are
+  rounded to fp16 (round to nearest even), as the device cache holds them.
+Projection weights are dequantized with the oracle's bit-exact decoders and
+every product, sum and transcendental is taken in float64.
+
+Pins: each piece reduces to a closed form checked in tests/test_oracle_decode.py
+(RMSNorm of a constant vector, rotation by angle 0 and by pi/2 per pair, the
+norm preserved by the rotation, attention over one position returning that
+position's value and over identical keys returning the mean of the values,
+silu(0) = 0 and silu(v) -> v for large v, the fused projections equal to the
+separate ones).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import dequant_rows
+
+
+def rmsnorm(x: np.ndarray, scale: np.ndarray, eps: float) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float64)
+    return x / np.sqrt(np.mean(x * x) + eps) * np.asarray(scale, dtype=np.float64)
+
+
+def rope_neox(heads: np.ndarray, pos: int, base: float) -> np.ndarray:
+    """Rotate each row (a head of even width) by the NeoX rotary at `pos`."""
+    h = np.array(heads, dtype=np.float64, copy=True)
+    dims = h.shape[-1]
+    half = dims // 2
+    i = np.arange(half, dtype=np.float64)
+    angle = float(pos) * np.exp(-(2.0 * i / dims) * np.log(base))
+    c, s = np.cos(angle), np.sin(angle)
+    a, b = h[..., :half].copy(), h[..., half:].copy()
+    h[..., :half] = a * c - b * s
+    h[..., half:] = b * c + a * s
+    return h
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, length: int) -> np.ndarray:
+    """q [nq, hd]; k, v [nkv, >= length, hd]; query head h reads kv head h // (nq / nkv)."""
+    nq, hd = q.shape
+    nkv = k.shape[0]
+    group = nq // nkv
+    out = np.empty((nq, hd), dtype=np.float64)
+    for h in range(nq):
+        kh = h // group
+        s = (k[kh, :length].astype(np.float64) @ q[h].astype(np.float64)) / np.sqrt(hd)
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ v[kh, :length].astype(np.float64)
+    return out
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.asarray(gate, dtype=np.float64)
+    return g * (0.5 * (np.tanh(0.5 * g) + 1.0)) * np.asarray(up, dtype=np.float64)
+
+
+def _fp16_round(values: np.ndarray) -> np.ndarray:
+    return np.asarray(values, dtype=np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+class DecoderReference:
+    """The decoder's weights dequantized once; `step` advances one token.
+
+    `shape` has layers, d, q_heads, kv_heads, head_dim, ffn, vocab, rope_base,
+    eps, proj_fmt, head_fmt. Caches are float64 arrays [kv_heads, max_ctx,
+    head_dim] holding fp16 values."""
+
+    def __init__(self, shape, embed, out_norm, head, layers, caches, max_ctx: int):
+        s = self.shape = shape
+        self.embed = np.asarray(embed, dtype=np.float64)
+        self.out_norm = np.asarray(out_norm, dtype=np.float64)
+        self.head = dequant_rows(s.head_fmt, head, s.vocab, s.d).reshape(s.vocab, s.d).astype(np.float64)
+        qkv_rows = (s.q_heads + 2 * s.kv_heads) * s.head_dim
+        self.layers = []
+        for t in layers:
+            self.layers.append({
+                "attn_norm": np.asarray(t.attn_norm, dtype=np.float64),
+                "qkv": dequant_rows(s.proj_fmt, t.qkv, qkv_rows, s.d).reshape(qkv_rows, s.d).astype(np.float64),
+                "o": dequant_rows(s.proj_fmt, t.o, s.d, s.d).reshape(s.d, s.d).astype(np.float64),
+                "ffn_norm": np.asarray(t.ffn_norm, dtype=np.float64),
+                "gate_up": dequant_rows(s.proj_fmt, t.gate_up, 2 * s.ffn, s.d).reshape(2 * s.ffn, s.d)
+                .astype(np.float64),
+                "down": dequant_rows(s.proj_fmt, t.down, s.d, s.ffn).reshape(s.d, s.ffn).astype(np.float64),
+            })
+        self.k, self.v = [], []
+        for kc, vc in caches:
+            n = kc.shape[1]
+            kf = np.zeros((s.kv_heads, max_ctx, s.head_dim))
+            vf = np.zeros((s.kv_heads, max_ctx, s.head_dim))
+            kf[:, :n] = np.asarray(kc, dtype=np.uint16).view(np.float16).astype(np.float64)
+            vf[:, :n] = np.asarray(vc, dtype=np.uint16).view(np.float16).astype(np.float64)
+            self.k.append(kf)
+            self.v.append(vf)
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        """Logits of the token at `pos` (its key and value join the caches)."""
+        s = self.shape
+        hd, nq, nkv = s.head_dim, s.q_heads, s.kv_heads
+        x = self.embed[token % s.vocab].copy()
+        for i, L in enumerate(self.layers):
+            xn = rmsnorm(x, L["attn_norm"], s.eps)
+            qkv = L["qkv"] @ xn
+            q = rope_neox(qkv[:nq * hd].reshape(nq, hd), pos, s.rope_base)
+            k = rope_neox(qkv[nq * hd:(nq + nkv) * hd].reshape(nkv, hd), pos, s.rope_base)
+            v = qkv[(nq + nkv) * hd:].reshape(nkv, hd)
+            self.k[i][:, pos] = _fp16_round(k)
+            self.v[i][:, pos] = _fp16_round(v)
+            a = attention(q, self.k[i], self.v[i], pos + 1).reshape(-1)
+            x = x + L["o"] @ a
+            xn = rmsnorm(x, L["ffn_norm"], s.eps)
+            gu = L["gate_up"] @ xn
+            x = x + L["down"] @ silu_mul(gu[:s.ffn], gu[s.ffn:])
+        return self.head @ rmsnorm(x, self.out_norm, s.eps)

@@ -7,6 +7,7 @@
 
 #include "../../include/rqmv.h"
 #include "kernels.h"
+#include "decode.h"
 #include "moe.h"
 #include "repack.h"
 
@@ -403,6 +404,66 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
     e = rq::launch_moe_down(fmt, d, bank_of(params->down_exps), bank_of(params->down_shexp), ws, y_dev, info.cus, s);
     if (e != hipSuccess) return hip_fail(e, "moe down launch");
     return RQMV_OK;
+}
+
+int rqmv_add_rmsnorm(float* x, const float* delta, const float* weight, int n, float eps, float* out, void* stream) {
+    if (!x || !weight || !out || n <= 0) return fail(RQMV_EINVAL, "add_rmsnorm: bad arguments");
+    hipError_t e = rq::launch_add_rmsnorm(x, delta, weight, n, eps, out, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "add_rmsnorm launch");
+}
+
+int rqmv_rope_kv(float* qkv, const int* pos, int q_heads, int kv_heads, int head_dim, double base, void* k_cache,
+                 void* v_cache, int max_ctx, void* stream) {
+    if (!qkv || !pos || !k_cache || !v_cache || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 ||
+        max_ctx <= 0 || !(base > 1.0))
+        return fail(RQMV_EINVAL, "rope_kv: bad arguments");
+    hipError_t e = rq::launch_rope_kv(qkv, pos, q_heads, kv_heads, head_dim, base, static_cast<__half*>(k_cache),
+                                      static_cast<__half*>(v_cache), max_ctx, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "rope_kv launch");
+}
+
+int rqmv_attention_workspace_size(int q_heads, int head_dim, int max_ctx, size_t* bytes) {
+    if (q_heads <= 0 || head_dim <= 0 || max_ctx <= 0 || !bytes) return fail(RQMV_EINVAL, "attention: bad arguments");
+    *bytes = rq::attention_workspace_bytes(q_heads, head_dim, max_ctx);
+    return RQMV_OK;
+}
+
+int rqmv_attention(const float* q, const void* k_cache, const void* v_cache, const int* pos, int q_heads, int kv_heads,
+                   int head_dim, int max_ctx, void* workspace, size_t workspace_bytes, float* out, void* stream) {
+    if (!q || !k_cache || !v_cache || !pos || !workspace || !out || q_heads <= 0 || kv_heads <= 0 || max_ctx <= 0)
+        return fail(RQMV_EINVAL, "attention: bad arguments");
+    if (q_heads % kv_heads || q_heads / kv_heads > 8 || head_dim % 64 || head_dim > 256)
+        return fail(RQMV_EINVAL, "attention: q_heads must be 1..8 x kv_heads and head_dim a multiple of 64 up to 256");
+    if (workspace_bytes < rq::attention_workspace_bytes(q_heads, head_dim, max_ctx))
+        return fail(RQMV_EINVAL, "attention: workspace too small");
+    hipError_t e = rq::launch_attention(q, static_cast<const __half*>(k_cache), static_cast<const __half*>(v_cache), pos,
+                                        q_heads, kv_heads, head_dim, max_ctx, workspace, out,
+                                        static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "attention launch");
+}
+
+int rqmv_silu_mul(const float* gate_up, int n, float* out, void* stream) {
+    if (!gate_up || !out || n <= 0) return fail(RQMV_EINVAL, "silu_mul: bad arguments");
+    hipError_t e = rq::launch_silu_mul(gate_up, n, out, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "silu_mul launch");
+}
+
+int rqmv_argmax(const float* values, int n, int* out, void* stream) {
+    if (!values || !out || n <= 0) return fail(RQMV_EINVAL, "argmax: bad arguments");
+    hipError_t e = rq::launch_argmax(values, n, out, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "argmax launch");
+}
+
+int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, void* stream) {
+    if (!table || !token || !out || rows <= 0 || n <= 0) return fail(RQMV_EINVAL, "embed_row: bad arguments");
+    hipError_t e = rq::launch_embed_row(table, rows, n, token, out, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "embed_row launch");
+}
+
+int rqmv_advance(int* pos, void* stream) {
+    if (!pos) return fail(RQMV_EINVAL, "advance: NULL position");
+    hipError_t e = rq::launch_advance(pos, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "advance launch");
 }
 
 int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* bytes) {

@@ -56,6 +56,16 @@ class _Lib:
         L.rqmv_expert_matvec.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p]
         L.rqmv_moe_workspace_size.argtypes = [c_void_p, POINTER(c_size_t)]
         L.rqmv_moe.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        L.rqmv_add_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]
+        L.rqmv_rope_kv.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, ctypes.c_double, c_void_p, c_void_p, c_int,
+                                   c_void_p]
+        L.rqmv_attention_workspace_size.argtypes = [c_int, c_int, c_int, POINTER(c_size_t)]
+        L.rqmv_attention.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
+                                     c_size_t, c_void_p, c_void_p]
+        L.rqmv_silu_mul.argtypes = [c_void_p, c_int, c_void_p, c_void_p]
+        L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p]
+        L.rqmv_advance.argtypes = [c_void_p, c_void_p]
+        L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
         L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t)]
         L.rqmv_repack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
         L.rqmv_unpack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
@@ -388,3 +398,52 @@ def unpack_host(fmt, rows: int, cols: int, packed: np.ndarray, nbytes: int) -> n
     pk = _as_bytes(packed)
     _check(lib().lib.rqmv_unpack_host(_fmt(fmt), rows, cols, pk.ctypes.data, out.ctypes.data), "rqmv_unpack_host")
     return out
+
+
+# ------------------------------------------------- decode-step helpers ----
+# Thin wrappers of the decode-step entry points (device buffers in and out).
+
+def _sh(stream):
+    return stream.handle if stream else None
+
+
+def add_rmsnorm(x: DeviceBuffer, delta: DeviceBuffer | None, weight: DeviceBuffer, n: int, eps: float,
+                out: DeviceBuffer, stream: Stream | None = None, delta_offset: int = 0):
+    _check(lib().lib.rqmv_add_rmsnorm(x.ptr, (delta.ptr + delta_offset) if delta else None, weight.ptr, n, eps,
+                                      out.ptr, _sh(stream)), "rqmv_add_rmsnorm")
+
+
+def rope_kv(qkv: DeviceBuffer, pos: DeviceBuffer, q_heads: int, kv_heads: int, head_dim: int, base: float,
+            k_cache: DeviceBuffer, v_cache: DeviceBuffer, max_ctx: int, stream: Stream | None = None):
+    _check(lib().lib.rqmv_rope_kv(qkv.ptr, pos.ptr, q_heads, kv_heads, head_dim, base, k_cache.ptr, v_cache.ptr,
+                                  max_ctx, _sh(stream)), "rqmv_rope_kv")
+
+
+def attention_workspace_size(q_heads: int, head_dim: int, max_ctx: int) -> int:
+    n = c_size_t()
+    _check(lib().lib.rqmv_attention_workspace_size(q_heads, head_dim, max_ctx, byref(n)), "rqmv_attention_workspace_size")
+    return n.value
+
+
+def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, pos: DeviceBuffer, q_heads: int,
+              kv_heads: int, head_dim: int, max_ctx: int, workspace: DeviceBuffer, out: DeviceBuffer,
+              stream: Stream | None = None):
+    _check(lib().lib.rqmv_attention(q.ptr, k_cache.ptr, v_cache.ptr, pos.ptr, q_heads, kv_heads, head_dim, max_ctx,
+                                    workspace.ptr, workspace.nbytes, out.ptr, _sh(stream)), "rqmv_attention")
+
+
+def silu_mul(gate_up: DeviceBuffer, n: int, out: DeviceBuffer, stream: Stream | None = None):
+    _check(lib().lib.rqmv_silu_mul(gate_up.ptr, n, out.ptr, _sh(stream)), "rqmv_silu_mul")
+
+
+def argmax(values: DeviceBuffer, n: int, out: DeviceBuffer, stream: Stream | None = None):
+    _check(lib().lib.rqmv_argmax(values.ptr, n, out.ptr, _sh(stream)), "rqmv_argmax")
+
+
+def advance(pos: DeviceBuffer, stream: Stream | None = None):
+    _check(lib().lib.rqmv_advance(pos.ptr, _sh(stream)), "rqmv_advance")
+
+
+def embed_row(table: DeviceBuffer, rows: int, n: int, token: DeviceBuffer, out: DeviceBuffer,
+              stream: Stream | None = None):
+    _check(lib().lib.rqmv_embed_row(table.ptr, rows, n, token.ptr, out.ptr, _sh(stream)), "rqmv_embed_row")

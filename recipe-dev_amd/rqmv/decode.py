@@ -1,0 +1,181 @@
+"""Single-token decode of a llama-style decoder on the device.
+
+One step runs, for a token held in device memory at a position held in device
+memory (so that a captured step replays at the next position):
+
+    x = embed[token]
+    per layer:  xn = rmsnorm(x) * attn_norm            (x += previous FFN output first)
+                qkv = W_qkv xn                          (one fused projection, [q | k | v] heads)
+                rotate q, k (NeoX); append k, v (fp16) to the layer's cache at pos
+                a = attention(q, cache[0..pos])         (grouped-query, 1/sqrt(head_dim))
+                o = W_o a
+                xn = rmsnorm(x += o) * ffn_norm
+                gu = W_gate|up xn                       (one fused projection, [gate | up] rows)
+                h = silu(gate) * up
+                f = W_down h
+    xn = rmsnorm(x += f) * out_norm;  logits = W_head xn;  token = argmax(logits);  pos += 1
+
+This is recipe's attention block and SiLU-GLU feed-forward (lower_attention,
+recipe.rs:23056-23150; lower_normalize, recipe.rs:23190-23210; silu(gate) * up,
+recipe.rs:23279-23286, 22662-22668) run one position at a time. Every
+projection is a quantized matrix-vector product of librqmv; the norms, rotary,
+attention, SiLU-GLU, argmax and embedding gather are librqmv's decode helpers.
+The residual stream and every activation are fp32; the KV cache is fp16.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import (DTYPE_F32, DeviceBuffer, Graph, Stream, Weight, add_rmsnorm, advance, argmax, attention,
+               attention_workspace_size, embed_row, rope_kv, silu_mul)
+
+
+@dataclass(frozen=True)
+class DecoderShape:
+    layers: int = 32
+    d: int = 4096
+    q_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 14336
+    vocab: int = 128256
+    rope_base: float = 500000.0
+    eps: float = 1e-5
+    proj_fmt: str = "q4_k"
+    head_fmt: str = "q8_0"
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.q_heads + 2 * self.kv_heads) * self.head_dim
+
+    def validate(self):
+        if self.d % 256 or self.ffn % 256:
+            raise ValueError("d and ffn must be multiples of 256 (one K-quant superblock)")
+        if self.q_heads * self.head_dim != self.d:
+            raise ValueError("q_heads * head_dim must equal d")
+        if self.q_heads % self.kv_heads or self.q_heads // self.kv_heads > 8:
+            raise ValueError("q_heads must be a multiple of kv_heads, at most 8 per kv head")
+        if self.head_dim % 64 or self.head_dim > 256:
+            raise ValueError("head_dim must be a multiple of 64 up to 256")
+
+
+@dataclass
+class LayerTensors:
+    """One layer's tensors as the file stores them: fp32 norm scales and GGUF
+    blocks of the fused projections (rows of W_q, W_k, W_v stacked; rows of
+    W_gate then W_up stacked)."""
+    attn_norm: np.ndarray
+    qkv: np.ndarray
+    o: np.ndarray
+    ffn_norm: np.ndarray
+    gate_up: np.ndarray
+    down: np.ndarray
+
+
+class DecodeModel:
+    """The device state of one decoder: weights, caches and step buffers."""
+
+    def __init__(self, shape: DecoderShape, max_ctx: int, embed: np.ndarray, out_norm: np.ndarray,
+                 head: np.ndarray):
+        shape.validate()
+        self.shape, self.max_ctx = shape, int(max_ctx)
+        s = shape
+        embed = np.ascontiguousarray(embed, dtype=np.float32)
+        if embed.shape != (s.vocab, s.d):
+            raise ValueError(f"embedding table must be {(s.vocab, s.d)}, got {embed.shape}")
+        self.embed = DeviceBuffer.from_array(embed)
+        self.out_norm = DeviceBuffer.from_array(np.ascontiguousarray(out_norm, dtype=np.float32))
+        self.head = Weight(s.head_fmt, s.vocab, s.d, head)
+        self.layers: list[dict | None] = [None] * s.layers
+        cache_bytes = s.kv_heads * self.max_ctx * s.head_dim * 2
+        self.k_cache = [DeviceBuffer(cache_bytes) for _ in range(s.layers)]
+        self.v_cache = [DeviceBuffer(cache_bytes) for _ in range(s.layers)]
+        f32 = 4
+        self.x = DeviceBuffer(s.d * f32)
+        self.xn = DeviceBuffer(s.d * f32)
+        self.qkv = DeviceBuffer(s.qkv_rows * f32)
+        self.attn = DeviceBuffer(s.d * f32)
+        self.o = DeviceBuffer(s.d * f32)
+        self.gu = DeviceBuffer(2 * s.ffn * f32)
+        self.h = DeviceBuffer(s.ffn * f32)
+        self.f = DeviceBuffer(s.d * f32)
+        self.logits = DeviceBuffer(s.vocab * f32)
+        self.token = DeviceBuffer(4)
+        self.pos = DeviceBuffer(4)
+        self.workspace = DeviceBuffer(attention_workspace_size(s.q_heads, s.head_dim, self.max_ctx))
+
+    # ---------------------------------------------------------------- setup
+    def set_layer(self, index: int, t: LayerTensors):
+        s = self.shape
+        self.layers[index] = {
+            "attn_norm": DeviceBuffer.from_array(np.ascontiguousarray(t.attn_norm, dtype=np.float32)),
+            "qkv": Weight(s.proj_fmt, s.qkv_rows, s.d, t.qkv),
+            "o": Weight(s.proj_fmt, s.d, s.d, t.o),
+            "ffn_norm": DeviceBuffer.from_array(np.ascontiguousarray(t.ffn_norm, dtype=np.float32)),
+            "gate_up": Weight(s.proj_fmt, 2 * s.ffn, s.d, t.gate_up),
+            "down": Weight(s.proj_fmt, s.d, s.ffn, t.down),
+        }
+
+    def set_cache(self, index: int, k: np.ndarray, v: np.ndarray):
+        """Prefill layer `index`'s cache: k, v are fp16 bits [kv_heads, n, head_dim]
+        for positions 0..n-1."""
+        s = self.shape
+        for buf, src in ((self.k_cache[index], k), (self.v_cache[index], v)):
+            src = np.asarray(src, dtype=np.uint16)
+            n = src.shape[1]
+            if src.shape != (s.kv_heads, n, s.head_dim) or n > self.max_ctx:
+                raise ValueError(f"cache prefill must be [kv_heads, n <= max_ctx, head_dim], got {src.shape}")
+            full = np.zeros((s.kv_heads, self.max_ctx, s.head_dim), dtype=np.uint16)
+            full[:, :n] = src
+            buf.upload(full)
+
+    def set_position(self, token: int, pos: int):
+        self.token.upload(np.array([token], dtype=np.int32))
+        self.pos.upload(np.array([pos], dtype=np.int32))
+
+    # ----------------------------------------------------------------- step
+    def enqueue_step(self, stream: Stream | None = None):
+        """Enqueue one decode step on `stream` (capturable: no allocation, no
+        host synchronisation)."""
+        s = self.shape
+        if any(layer is None for layer in self.layers):
+            raise RuntimeError("every layer must be set before a step")
+        embed_row(self.embed, s.vocab, s.d, self.token, self.x, stream)
+        for i, L in enumerate(self.layers):
+            add_rmsnorm(self.x, self.f if i else None, L["attn_norm"], s.d, s.eps, self.xn, stream)
+            L["qkv"].matvec(self.xn, DTYPE_F32, 1, s.d, self.qkv, s.qkv_rows, stream)
+            rope_kv(self.qkv, self.pos, s.q_heads, s.kv_heads, s.head_dim, s.rope_base, self.k_cache[i],
+                    self.v_cache[i], self.max_ctx, stream)
+            attention(self.qkv, self.k_cache[i], self.v_cache[i], self.pos, s.q_heads, s.kv_heads, s.head_dim,
+                      self.max_ctx, self.workspace, self.attn, stream)
+            L["o"].matvec(self.attn, DTYPE_F32, 1, s.d, self.o, s.d, stream)
+            add_rmsnorm(self.x, self.o, L["ffn_norm"], s.d, s.eps, self.xn, stream)
+            L["gate_up"].matvec(self.xn, DTYPE_F32, 1, s.d, self.gu, 2 * s.ffn, stream)
+            silu_mul(self.gu, s.ffn, self.h, stream)
+            L["down"].matvec(self.h, DTYPE_F32, 1, s.ffn, self.f, s.d, stream)
+        add_rmsnorm(self.x, self.f, self.out_norm, s.d, s.eps, self.xn, stream)
+        self.head.matvec(self.xn, DTYPE_F32, 1, s.d, self.logits, s.vocab, stream)
+        argmax(self.logits, s.vocab, self.token, stream)
+        advance(self.pos, stream)
+
+    def capture(self, stream: Stream) -> Graph:
+        """A HIP graph of one step; each launch decodes the next token."""
+        return Graph(stream, lambda: self.enqueue_step(stream))
+
+    def read_logits(self) -> np.ndarray:
+        return self.logits.download(np.float32, self.shape.vocab)
+
+    def read_token(self) -> int:
+        return int(self.token.download(np.int32, 1)[0])
+
+    def read_position(self) -> int:
+        return int(self.pos.download(np.int32, 1)[0])
+
+    def weight_bytes(self) -> int:
+        """GGUF bytes of every projection and the head (what one step streams)."""
+        total = self.head.gguf_nbytes
+        for L in self.layers:
+            total += sum(L[k].gguf_nbytes for k in ("qkv", "o", "gate_up", "down"))
+        return total

@@ -171,3 +171,109 @@ def activations_f16(count: int, seed: int = DEFAULT_SEED, tag: str = "x") -> np.
 
 def activations_f32(count: int, seed: int = DEFAULT_SEED, tag: str = "x") -> np.ndarray:
     return normal(seed, tag + ".f32", count).astype(np.float32)
+
+
+# ------------------------------------------------------------- decoder ----
+# A random-init decoder for the single-token decode step. Projection weights
+# of one layer are drawn with the generators above; every layer then holds
+# those blocks with a layer-specific byte pattern XORed over the code and
+# sub-scale bytes (the fp16 block scales are kept), which keeps each field's
+# distribution uniform over its range while giving every layer its own bytes
+# (so no layer's weights can be served from another's cache lines). KV-cache
+# prefill is N(0, 1) in fp16, one layer drawn and the others given per-layer
+# random signs. A large output head is drawn for its first eighth of rows and
+# the other eighths are keyed variants of it, like the layers. The embedding
+# table (fp32, not a quantized tensor; one row is read per token) is N(0, 1)
+# from numpy's PCG64 under the seed for its first 8192 rows, repeated over the
+# vocabulary with a random sign per row.
+
+_SCALE_BYTES = {"q4_0": (0, 2), "q8_0": (0, 2), "q4_k": (0, 4), "q6_k": (208, 210)}
+
+
+def _payload_mask(fmt: str) -> np.ndarray:
+    """Per block byte: True for the code and sub-scale bytes a layer key may flip."""
+    bb = BLOCK[fmt][1]
+    keep = np.ones(bb, dtype=bool)
+    lo, hi = _SCALE_BYTES[fmt]
+    keep[lo:hi] = False
+    return keep
+
+
+def layer_variant(fmt: str, blocks: np.ndarray, seed: int, tag: str) -> np.ndarray:
+    """`blocks` with the layer key `tag` XORed over every block's payload bytes."""
+    bb = BLOCK[fmt][1]
+    key = random_bytes(seed, tag + ".key", bb)
+    key[~_payload_mask(fmt)] = 0
+    return (blocks.reshape(-1, bb) ^ key[None, :]).reshape(-1)
+
+
+def fp16_normal(count: int, seed: int, tag: str) -> np.ndarray:
+    return fp16_bits(normal(seed, tag, count).astype(np.float32))
+
+
+class DecoderSynth:
+    """Seeded tensors of a random-init decoder of the given shape (an object
+    with layers, d, q_heads, kv_heads, head_dim, ffn, vocab, proj_fmt,
+    head_fmt). `norm_std` = 0 gives identity RMSNorm scales (recipe's
+    initial value, recipe.rs:23206-23208); tests draw them N(1, norm_std^2)."""
+
+    def __init__(self, shape, seed: int = DEFAULT_SEED, norm_std: float = 0.0):
+        self.shape, self.seed, self.norm_std = shape, seed, norm_std
+        s = shape
+        qkv_rows = (s.q_heads + 2 * s.kv_heads) * s.head_dim
+        f = s.proj_fmt
+        self._base = {
+            "qkv": (qkv_rows, s.d, weights(f, qkv_rows, s.d, seed, "dec.qkv")),
+            "o": (s.d, s.d, weights(f, s.d, s.d, seed, "dec.o")),
+            "gate_up": (2 * s.ffn, s.d, weights(f, 2 * s.ffn, s.d, seed, "dec.gate_up")),
+            "down": (s.d, s.ffn, weights(f, s.d, s.ffn, seed, "dec.down")),
+        }
+        self._kv_base = None
+
+    def _norm(self, tag: str) -> np.ndarray:
+        n = self.shape.d
+        if self.norm_std == 0.0:
+            return np.ones(n, dtype=np.float32)
+        return (1.0 + self.norm_std * normal(self.seed, tag, n)).astype(np.float32)
+
+    def layer(self, index: int):
+        from .decode import LayerTensors
+        f = self.shape.proj_fmt
+        w = {k: layer_variant(f, b, self.seed, f"dec.l{index}.{k}") for k, (_, _, b) in self._base.items()}
+        return LayerTensors(attn_norm=self._norm(f"dec.l{index}.attn_norm"), qkv=w["qkv"], o=w["o"],
+                            ffn_norm=self._norm(f"dec.l{index}.ffn_norm"), gate_up=w["gate_up"], down=w["down"])
+
+    def cache(self, index: int, ctx: int):
+        """fp16 bits [kv_heads, ctx, head_dim] of keys and values for layer `index`."""
+        s = self.shape
+        n = s.kv_heads * ctx * s.head_dim
+        if self._kv_base is None or self._kv_base[0].size != n:
+            self._kv_base = (fp16_normal(n, self.seed, "dec.kcache"), fp16_normal(n, self.seed, "dec.vcache"))
+        out = []
+        for j, base in enumerate(self._kv_base):
+            signs = random_bytes(self.seed, f"dec.l{index}.signs{j}", 2 * n).view(np.uint16) & np.uint16(0x8000)
+            out.append((base ^ signs).reshape(s.kv_heads, ctx, s.head_dim))
+        return out[0], out[1]
+
+    def out_norm(self) -> np.ndarray:
+        return self._norm("dec.out_norm")
+
+    def head(self) -> np.ndarray:
+        s = self.shape
+        if s.vocab < 16384 or s.vocab % 8:
+            return weights(s.head_fmt, s.vocab, s.d, self.seed, "dec.head")
+        base = weights(s.head_fmt, s.vocab // 8, s.d, self.seed, "dec.head")
+        parts = [base] + [layer_variant(s.head_fmt, base, self.seed, f"dec.head{c}") for c in range(1, 8)]
+        return np.concatenate(parts)
+
+    def embed(self) -> np.ndarray:
+        s = self.shape
+        rng = np.random.Generator(np.random.PCG64(self.seed))
+        base = rng.standard_normal((min(s.vocab, 8192), s.d), dtype=np.float32)
+        if s.vocab <= base.shape[0]:
+            return base
+        reps = -(-s.vocab // base.shape[0])
+        table = np.tile(base, (reps, 1))[: s.vocab]
+        signs = np.where(rng.integers(0, 2, s.vocab) == 1, np.float32(-1.0), np.float32(1.0))
+        table *= signs[:, None]
+        return table

@@ -1,0 +1,219 @@
+"""GPU parity of the decode-step helpers and of a whole decode step against the
+oracle's f64 decode reference (oracle/decode.py), through the C ABI.
+
+Bars: residual adds bit-exact (one fp32 add, as numpy does it); the helpers
+within rel 1e-5 (norm, rotary, attention, SiLU-GLU); cache appends within one
+fp16 rounding of the reference; logits of a whole step within rel-L2 1e-3 of
+the f64 reference (the projections' own bar), steps replayed from a captured
+HIP graph included; argmax bit-exact with ties to the lowest index.
+"""
+import numpy as np
+import pytest
+
+from oracle import decode as ref
+from rqmv import synth
+from rqmv.decode import DecodeModel, DecoderShape
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(11)
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _i32(gpu, v):
+    return gpu.DeviceBuffer.from_array(np.array([v], dtype=np.int32))
+
+
+@pytest.mark.parametrize("n", [1, 100, 4096, 5120])
+def test_add_rmsnorm(gpu, n):
+    x = RNG.standard_normal(n).astype(np.float32) * 40
+    delta = RNG.standard_normal(n).astype(np.float32)
+    w = (1 + 0.1 * RNG.standard_normal(n)).astype(np.float32)
+    X, D, W, O = (gpu.DeviceBuffer.from_array(a) for a in (x, delta, w, np.zeros(n, np.float32)))
+    gpu.add_rmsnorm(X, D, W, n, 1e-5, O)
+    gpu.synchronize()
+    xs = x + delta
+    assert np.array_equal(X.download(np.float32), xs)
+    assert rel_err(O.download(np.float32), ref.rmsnorm(xs, w, 1e-5)) < 1e-5
+    gpu.add_rmsnorm(X, None, W, n, 1e-5, O)  # no delta: x unchanged
+    gpu.synchronize()
+    assert np.array_equal(X.download(np.float32), xs)
+
+
+@pytest.mark.parametrize("nq,nkv,hd", [(4, 2, 64), (32, 8, 128), (8, 8, 256)])
+@pytest.mark.parametrize("pos", [0, 7, 4095])
+def test_rope_kv(gpu, nq, nkv, hd, pos):
+    max_ctx = 4100
+    qkv = RNG.standard_normal((nq + 2 * nkv) * hd).astype(np.float32)
+    Q = gpu.DeviceBuffer.from_array(qkv)
+    cache_bytes = nkv * max_ctx * hd * 2
+    K, V = gpu.DeviceBuffer(cache_bytes), gpu.DeviceBuffer(cache_bytes)
+    K.fill_zero()
+    V.fill_zero()
+    gpu.rope_kv(Q, _i32(gpu, pos), nq, nkv, hd, 500000.0, K, V, max_ctx)
+    gpu.synchronize()
+    got = Q.download(np.float32)
+    q_ref = ref.rope_neox(qkv[:nq * hd].reshape(nq, hd), pos, 500000.0).reshape(-1)
+    k_ref = ref.rope_neox(qkv[nq * hd:(nq + nkv) * hd].reshape(nkv, hd), pos, 500000.0)
+    assert rel_err(got[:nq * hd], q_ref) < 1e-5
+    assert rel_err(got[nq * hd:(nq + nkv) * hd], k_ref.reshape(-1)) < 1e-5
+    assert np.array_equal(got[(nq + nkv) * hd:], qkv[(nq + nkv) * hd:])  # values untouched
+    kc = K.download(np.uint16).reshape(nkv, max_ctx, hd).view(np.float16)
+    vc = V.download(np.uint16).reshape(nkv, max_ctx, hd).view(np.float16)
+    # the cache holds fp16 of the fp32 results: within one fp16 rounding of the f64 reference
+    k16 = k_ref.astype(np.float16).astype(np.float64)
+    assert np.all(np.abs(kc[:, pos].astype(np.float64) - k16) <= np.abs(k16) * 2 ** -10 + 2 ** -24)
+    assert np.array_equal(vc[:, pos], qkv[(nq + nkv) * hd:].reshape(nkv, hd).astype(np.float16))
+    others = np.ones(max_ctx, bool)
+    others[pos] = False
+    assert not np.any(kc.view(np.uint16)[:, others]) and not np.any(vc.view(np.uint16)[:, others])
+
+
+def test_rope_kv_position_outside_cache_writes_nothing(gpu):
+    nq, nkv, hd, max_ctx = 4, 2, 64, 16
+    qkv = RNG.standard_normal((nq + 2 * nkv) * hd).astype(np.float32)
+    Q = gpu.DeviceBuffer.from_array(qkv)
+    K, V = gpu.DeviceBuffer(nkv * max_ctx * hd * 2), gpu.DeviceBuffer(nkv * max_ctx * hd * 2)
+    K.fill_zero()
+    V.fill_zero()
+    gpu.rope_kv(Q, _i32(gpu, max_ctx), nq, nkv, hd, 1e4, K, V, max_ctx)
+    gpu.synchronize()
+    assert not np.any(K.download(np.uint16)) and not np.any(V.download(np.uint16))
+
+
+@pytest.mark.parametrize("nq,nkv,hd", [(4, 2, 64), (32, 8, 128), (8, 1, 128), (4, 4, 256)])
+@pytest.mark.parametrize("length", [1, 127, 128, 129, 300])
+def test_attention(gpu, nq, nkv, hd, length):
+    max_ctx = 384
+    q = RNG.standard_normal((nq, hd)).astype(np.float32)
+    kc = RNG.standard_normal((nkv, max_ctx, hd)).astype(np.float16)
+    vc = RNG.standard_normal((nkv, max_ctx, hd)).astype(np.float16)
+    Q = gpu.DeviceBuffer.from_array(q)
+    K = gpu.DeviceBuffer.from_array(kc.view(np.uint16))
+    V = gpu.DeviceBuffer.from_array(vc.view(np.uint16))
+    ws = gpu.DeviceBuffer(gpu.attention_workspace_size(nq, hd, max_ctx))
+    O = gpu.DeviceBuffer(nq * hd * 4)
+    gpu.attention(Q, K, V, _i32(gpu, length - 1), nq, nkv, hd, max_ctx, ws, O)
+    gpu.synchronize()
+    want = ref.attention(q, kc.astype(np.float64), vc.astype(np.float64), length)
+    assert rel_err(O.download(np.float32), want.reshape(-1)) < 1e-5
+
+
+def test_attention_long_context(gpu):
+    nq, nkv, hd, max_ctx = 32, 8, 128, 4160
+    q = (RNG.standard_normal((nq, hd)) * 0.2).astype(np.float32)
+    kc = RNG.standard_normal((nkv, max_ctx, hd)).astype(np.float16)
+    vc = RNG.standard_normal((nkv, max_ctx, hd)).astype(np.float16)
+    Q = gpu.DeviceBuffer.from_array(q)
+    K = gpu.DeviceBuffer.from_array(kc.view(np.uint16))
+    V = gpu.DeviceBuffer.from_array(vc.view(np.uint16))
+    ws = gpu.DeviceBuffer(gpu.attention_workspace_size(nq, hd, max_ctx))
+    O = gpu.DeviceBuffer(nq * hd * 4)
+    for length in (4096, 4097, max_ctx):
+        gpu.attention(Q, K, V, _i32(gpu, length - 1), nq, nkv, hd, max_ctx, ws, O)
+        gpu.synchronize()
+        want = ref.attention(q, kc.astype(np.float64), vc.astype(np.float64), length)
+        assert rel_err(O.download(np.float32), want.reshape(-1)) < 1e-5, length
+
+
+@pytest.mark.parametrize("n", [1, 300, 14336])
+def test_silu_mul(gpu, n):
+    gu = (RNG.standard_normal(2 * n) * 6).astype(np.float32)
+    G, O = gpu.DeviceBuffer.from_array(gu), gpu.DeviceBuffer(4 * n)
+    gpu.silu_mul(G, n, O)
+    gpu.synchronize()
+    got = O.download(np.float32).astype(np.float64)
+    want = ref.silu_mul(gu[:n], gu[n:])
+    # recipe's sigmoid is 0.5 (tanh(v / 2) + 1) in fp32 (recipe.rs:22662-22668):
+    # near v -> -inf the sum cancels, so each element carries an absolute error
+    # of a few fp32 ulps of 1 times |g u| besides its relative rounding
+    g, u = gu[:n].astype(np.float64), gu[n:].astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2.0 ** -22 * np.abs(g * u) + 1e-6 * np.abs(want))
+    if n >= 300:
+        assert rel_err(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1025, 128256])
+def test_argmax_lowest_index_on_ties(gpu, n):
+    v = RNG.standard_normal(n).astype(np.float32)
+    if n > 10:
+        v[n // 3] = v[n - 2] = v.max() + 1.0  # a tie: the lower index wins
+        v[5] = -np.inf
+    V, O = gpu.DeviceBuffer.from_array(v), gpu.DeviceBuffer(4)
+    gpu.argmax(V, n, O)
+    gpu.synchronize()
+    assert int(O.download(np.int32, 1)[0]) == int(np.argmax(v))
+
+
+def test_embed_row(gpu):
+    rows, n = 50, 4096
+    table = RNG.standard_normal((rows, n)).astype(np.float32)
+    T, O = gpu.DeviceBuffer.from_array(table), gpu.DeviceBuffer(4 * n)
+    for tok in (0, 49, 123):
+        gpu.embed_row(T, rows, n, _i32(gpu, tok), O)
+        gpu.synchronize()
+        assert np.array_equal(O.download(np.float32), table[tok % rows])
+
+
+# ------------------------------------------------------ whole decode step ----
+
+def _small_decoder(gpu, shape, ctx, max_ctx, seed):
+    D = synth.DecoderSynth(shape, seed=seed, norm_std=0.1)
+    layers = [D.layer(i) for i in range(shape.layers)]
+    caches = [D.cache(i, ctx) for i in range(shape.layers)]
+    embed = D.embed()
+    model = DecodeModel(shape, max_ctx, embed, D.out_norm(), D.head())
+    for i in range(shape.layers):
+        model.set_layer(i, layers[i])
+        model.set_cache(i, *caches[i])
+    R = ref.DecoderReference(shape, embed, D.out_norm(), D.head(), layers, caches, max_ctx)
+    return model, R
+
+
+@pytest.mark.parametrize("proj_fmt,head_fmt", [("q4_k", "q8_0"), ("q6_k", "q4_0")])
+def test_decode_steps_match_reference(gpu, proj_fmt, head_fmt):
+    shape = DecoderShape(layers=2, d=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=512,
+                         proj_fmt=proj_fmt, head_fmt=head_fmt)
+    ctx, max_ctx = 16, 24
+    model, R = _small_decoder(gpu, shape, ctx, max_ctx, seed=21)
+    stream = gpu.Stream()
+    token, pos = 7, ctx
+    model.set_position(token, pos)
+    # one eager step, then steps replayed from a captured graph (teacher-forced:
+    # the reference decodes the token the device chose)
+    model.enqueue_step(stream)
+    stream.synchronize()
+    steps = [(token, pos, model.read_logits(), model.read_token())]
+    graph = model.capture(stream)
+    for _ in range(3):
+        token, pos = steps[-1][3], steps[-1][1] + 1
+        graph.launch(stream)
+        stream.synchronize()
+        steps.append((token, pos, model.read_logits(), model.read_token()))
+    assert model.read_position() == ctx + 4
+    for token, pos, logits, chosen in steps:
+        want = R.step(token, pos)
+        assert rel_err(logits, want) < 1e-3, (token, pos, rel_err(logits, want))
+        assert chosen == int(np.argmax(logits))
+    graph.close()
+    stream.close()
+
+
+def test_decode_real_head_shapes(gpu):
+    """One step at the full decoder's attention and projection widths (two
+    layers, smaller vocab), against the f64 reference."""
+    shape = DecoderShape(layers=2, d=4096, q_heads=32, kv_heads=8, head_dim=128, ffn=14336, vocab=2048)
+    ctx, max_ctx = 300, 320
+    model, R = _small_decoder(gpu, shape, ctx, max_ctx, seed=5)
+    model.set_position(3, ctx)
+    model.enqueue_step()
+    gpu.synchronize()
+    logits = model.read_logits()
+    want = R.step(3, ctx)
+    assert rel_err(logits, want) < 1e-3
+    assert model.read_token() == int(np.argmax(logits))
