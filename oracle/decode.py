@@ -13,19 +13,21 @@ Semantics (recipe's attention block and feed-forward, one position at a time):
 - NeoX rotary without yarn (rope_pair, amd-nv-cpu.ll:3719-3780): pair i of a
   head is (x_i, x_{i+half}), angle = pos * exp(-(2i/dims) * log(base)),
   lower = a cos - b sin, upper = b cos + a sin.
-- SiLU-GLU: silu(gate) * up with silu(v) = v * sigmoid(v)
-  (recipe.rs:23279-23286, 22662-22668).
+- SiLU-GLU: silu(gate) * up with silu(v) = v * sigmoid(v) and the sigmoid
+  taken as 0.5 (tanh(v / 2) + 1) (recipe.rs:23279-23286, 22662-22668).
 - The KV cache stores fp16: the appended key (after rotation) and value are
   rounded to fp16 (round to nearest even), as the device cache holds them.
 Projection weights are dequantized with the oracle's bit-exact decoders and
 every product, sum and transcendental is taken in float64.
 
-Pins: each piece reduces to a closed form checked in tests/test_oracle_decode.py
-(RMSNorm of a constant vector, rotation by angle 0 and by pi/2 per pair, the
-norm preserved by the rotation, attention over one position returning that
-position's value and over identical keys returning the mean of the values,
-silu(0) = 0 and silu(v) -> v for large v, the fused projections equal to the
-separate ones).
+Pins (tests/test_oracle_decode.py): RMSNorm of a constant vector and its
+scale invariance; the rotary equal to multiplying each pair, as a complex
+number, by exp(i pos base^(-2i/dims)), the identity at pos 0, and scores that
+depend on the relative position only; attention over one position returning
+its value, over identical keys returning the mean of the values, and equal to
+scipy's softmax with the query-to-kv-head grouping; SiLU-GLU against scipy's
+logistic function; a decoder whose output and down projections are zero
+reducing to the head applied to the normalised embedding.
 """
 from __future__ import annotations
 
