@@ -277,7 +277,7 @@ def decode_bench(args):
                                "NeoX rotary base 500000, SiLU-GLU 14336, RMSNorm 1e-5, Q4_K projections, "
                                "Q8_0 head 128256, fp16 KV cache prefilled to 4096",
                    "bytes_per_token": int(bytes_per_token), "positions": [pos0, pos0 + args.steps - 1],
-                   "launches_per_token": 4 + 10 * s.layers + 1, "activations": "f32", "kv_cache": "f16",
+                   "launches_per_token": 1 + 10 * s.layers + 5, "activations": "f32", "kv_cache": "f16",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,

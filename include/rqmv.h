@@ -161,17 +161,22 @@ int rqmv_rope_kv(float* qkv, const int* pos, int q_heads, int kv_heads, int head
 
 /* Grouped-query attention of one query (q_heads x head_dim) over positions
  * 0..min(pos, max_ctx - 1) of the cache: softmax(q k / sqrt(head_dim)) v per
- * query head. head_dim is a multiple of 64 up to 256; at most 8 query heads
- * share a kv head. */
-int rqmv_attention_workspace_size(int q_heads, int head_dim, int max_ctx, size_t* bytes);
+ * query head. head_dim is 64, 128 or 256; at most 8 query heads share a kv
+ * head; max_ctx is at most 65536; q, the caches, the workspace and out are
+ * 16-byte aligned. Two launches (per-chunk partial results in the workspace,
+ * then their merge); calls sharing a workspace must not overlap. */
+int rqmv_attention_workspace_size(int q_heads, int kv_heads, int head_dim, int max_ctx, size_t* bytes);
 int rqmv_attention(const float* q, const void* k_cache, const void* v_cache, const int* pos, int q_heads, int kv_heads,
                    int head_dim, int max_ctx, void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /* out[i] = silu(gate_up[i]) * gate_up[n + i]. */
 int rqmv_silu_mul(const float* gate_up, int n, float* out, void* stream);
 
-/* *out = the index of the largest value (the lowest index on a tie). */
-int rqmv_argmax(const float* values, int n, int* out, void* stream);
+/* *out = the index of the largest value (the lowest index on a tie; NaNs
+ * are skipped). Two launches (per-slice bests in the workspace, then their
+ * reduction); calls sharing a workspace must not overlap. */
+int rqmv_argmax_workspace_size(size_t* bytes);
+int rqmv_argmax(const float* values, int n, int* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* out = table[token mod rows] (rows x n fp32): the next token's embedding. */
 int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, void* stream);

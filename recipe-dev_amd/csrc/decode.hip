@@ -83,81 +83,127 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(float* qkv, const int* pos
 
 // ---------------------------------------------------------- attention ----
 
-// One workgroup per (kv head, chunk of kAttnChunk positions). Pass 1: the
-// scores of every query head of the group against every position of the chunk
-// (eight lanes per position, head_dim / 8 values each, summed over the eight
-// lanes), scaled by 1/sqrt(head_dim), into LDS. Pass 2: per query head the
-// chunk's maximum m, the weights e_t = exp(s_t - m) and their sum l. Pass 3:
-// o[d] = sum_t e_t v_t[d]. The chunk's (m, l, o) go to the workspace and
-// attn_combine_kernel merges the chunks.
+// Split over positions (flash decoding), in two launches. attention_kernel:
+// one workgroup of kAttnThreads per (kv head, chunk of kAttnChunk positions);
+// a chunk is read once for every query head of its group. Lanes take one
+// 16-byte piece (eight values) of a position's key and value: HD / 8 lanes per
+// position, the whole chunk's keys and values loaded into registers before
+// any arithmetic. Pass 1: each query head's score against each position (an
+// eight-value dot per lane, summed over the position's lanes), times
+// 1/sqrt(HD), into LDS. Pass 2: per query head (one wave each) the chunk's
+// maximum m, weights e = exp(s - m) and their sum l. Pass 3: o = sum e v, per
+// lane over its positions, summed over the lanes that hold the same values.
+// The chunk's (m, l, o) go to the workspace. attn_combine_kernel: one
+// workgroup per query head merges the live chunks, out = sum_c o_c
+// e^(m_c - M) / sum_c l_c e^(m_c - M), chunks in order. (A single launch
+// whose last workgroup merges costs more: publishing the partial results
+// across the XCDs' L2 caches takes an L2 write-back per workgroup.)
 constexpr int kAttnChunk = 128;
-constexpr int kAttnMaxGroup = 8;     // query heads per kv head
-constexpr int kAttnMaxHead = 256;    // head_dim
+constexpr int kAttnThreads = 512;
+constexpr int kAttnMaxGroup = 8;      // query heads per kv head
+constexpr int kAttnMaxChunks = 512;   // max_ctx up to 65536
 
-__device__ __forceinline__ float sum8(float v) {
+template <int LPP>
+__device__ __forceinline__ float sum_lanes(float v) {
+    // sum over aligned groups of LPP lanes (8, 16 or 32); every lane of a group gets the sum
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
-    return v;  // every lane of the aligned group of eight holds the sum
+    if constexpr (LPP >= 16)
+        v += __builtin_bit_cast(float,
+                                __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
+    if constexpr (LPP >= 32) v += __shfl_xor(v, 16);
+    return v;
 }
 
-__global__ void __launch_bounds__(256) attn_partial_kernel(const float* q, const __half* kc, const __half* vc,
-                                                           const int* pos_dev, int nq, int nkv, int hd, int max_ctx,
-                                                           float scale, float* part_ml, float* part_o) {
-    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
-    __shared__ float ml[kAttnMaxGroup][2];
-    __shared__ float sq[kAttnMaxGroup * kAttnMaxHead];
+struct AttnWork {
+    float* ml;  // [nq][nchunks][2]
+    float* o;   // [nq][nchunks][hd]
+};
+
+__host__ __device__ inline AttnWork attn_work(void* ws, int nq, int hd, int nchunks) {
+    AttnWork w;
+    w.ml = static_cast<float*>(ws);
+    w.o = w.ml + (size_t)nq * nchunks * 2;
+    return w;
+}
+
+template <int HD, int MAXG>
+__global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q, const __half* kc, const __half* vc,
+                                                                 const int* pos_dev, int nkv, int group, int max_ctx,
+                                                                 float scale, AttnWork ws, int nchunks) {
+    constexpr int LPP = HD / 8;                    // lanes per position
+    constexpr int PPS = kAttnThreads / LPP;        // positions per sweep
+    constexpr int NS = kAttnChunk / PPS;           // sweeps per chunk
+    constexpr int WAVES = kAttnThreads / 64;
+    __shared__ float sc[MAXG][kAttnChunk];
+    __shared__ float ml[MAXG][2];
+    __shared__ float red[WAVES][MAXG * HD];
     const int kh = blockIdx.x, chunk = blockIdx.y;
-    const int len = min(*pos_dev + 1, max_ctx);  // positions past the cache are not read
+    const int len = min(*pos_dev + 1, max_ctx);
     const int t0 = chunk * kAttnChunk;
-    const int group = nq / nkv;
-    const int t = threadIdx.x;
-    const int per = hd / 8;  // values per lane in pass 1 (a multiple of 8)
-    const __half* kbase = kc + (size_t)kh * max_ctx * hd;
-    const __half* vbase = vc + (size_t)kh * max_ctx * hd;
-    for (int i = t; i < group * hd; i += blockDim.x) sq[i] = q[(size_t)kh * group * hd + i];
-    __syncthreads();
-    // pass 1: eight lanes per position, 32 positions per sweep of 256 threads
-    const int sub = t & 7, slot = t >> 3;
-    for (int p0 = 0; p0 < kAttnChunk; p0 += 32) {
-        const int tp = t0 + p0 + slot;
-        float dots[kAttnMaxGroup];
+    if (t0 >= len) return;  // a chunk past the position: nothing to read (the whole workgroup leaves)
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int b = t % LPP, slot = t / LPP;
+    const int nq = nkv * group;
+
+    // keys and values of this lane's positions; positions past the end read the last live one (weight 0)
+    uint4 kr[NS], vr[NS];
+    const size_t head_base = (size_t)kh * max_ctx;
 #pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g) dots[g] = 0.f;
-        if (tp < len) {
-            const uint4* krow = reinterpret_cast<const uint4*>(kbase + (size_t)tp * hd + sub * per);
-            for (int e8 = 0; e8 < per / 8; ++e8) {
-                const uint4 raw = krow[e8];
-                const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+    for (int j = 0; j < NS; ++j) {
+        const int p = min(t0 + slot + j * PPS, len - 1);
+        kr[j] = *reinterpret_cast<const uint4*>(kc + (head_base + p) * HD + b * 8);
+    }
 #pragma unroll
-                for (int h2 = 0; h2 < 4; ++h2) {
-                    const int e = e8 * 8 + 2 * h2;
-                    const float k0 = half_lo(w4[h2]), k1 = half_hi(w4[h2]);
+    for (int j = 0; j < NS; ++j) {
+        const int p = min(t0 + slot + j * PPS, len - 1);
+        vr[j] = *reinterpret_cast<const uint4*>(vc + (head_base + p) * HD + b * 8);
+    }
+    float qr[MAXG][8];
 #pragma unroll
-                    for (int g = 0; g < kAttnMaxGroup; ++g)
-                        if (g < group) {
-                            const float* qg = sq + g * hd + sub * per + e;
-                            dots[g] = fmaf(qg[1], k1, fmaf(qg[0], k0, dots[g]));
-                        }
-                }
-            }
+    for (int g = 0; g < MAXG; ++g) {
+        if (g < group) {
+            const float4* qs = reinterpret_cast<const float4*>(q + ((size_t)(kh * group + g) * HD + b * 8));
+            const float4 a = qs[0], c = qs[1];
+            qr[g][0] = a.x, qr[g][1] = a.y, qr[g][2] = a.z, qr[g][3] = a.w;
+            qr[g][4] = c.x, qr[g][5] = c.y, qr[g][6] = c.z, qr[g][7] = c.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qr[g][e] = 0.f;
         }
+    }
+
+    // pass 1: scores
 #pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g) {
-            const float s = sum8(dots[g]);
-            if (g < group && sub == 0) sc[g][p0 + slot] = tp < len ? s * scale : -INFINITY;
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+        float kv[8];
+#pragma unroll
+        for (int h2 = 0; h2 < 4; ++h2) {
+            kv[2 * h2] = half_lo(w4[h2]);
+            kv[2 * h2 + 1] = half_hi(w4[h2]);
+        }
+        const int pl = slot + j * PPS;
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kv[e], d);
+            d = sum_lanes<LPP>(d);
+            if (g < group && b == 0) sc[g][pl] = t0 + pl < len ? d * scale : -INFINITY;
         }
     }
     __syncthreads();
-    // pass 2: one wave per query head of the group (up to four at a time)
-    const int lane = t & 63, wave = t >> 6;
-    for (int g = wave; g < group; g += 4) {
+
+    // pass 2: per query head, the chunk's maximum, weights and their sum
+    for (int g = wave; g < group; g += WAVES) {
         float m = -INFINITY;
         for (int i = lane; i < kAttnChunk; i += 64) m = fmaxf(m, sc[g][i]);
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
         float l = 0.f;
         for (int i = lane; i < kAttnChunk; i += 64) {
-            const float e = sc[g][i] == -INFINITY ? 0.f : expf(sc[g][i] - m);
+            const float e = sc[g][i] == -INFINITY ? 0.f : __expf(sc[g][i] - m);
             sc[g][i] = e;
             l += e;
         }
@@ -168,46 +214,111 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* q, const
         }
     }
     __syncthreads();
-    // pass 3: thread d (and d + 256, ...) accumulates o[g][d] for every head of the group
-    const int n_out = hd;
-    for (int d = t; d < n_out; d += blockDim.x) {
-        float o[kAttnMaxGroup];
+
+    // pass 3: o = sum_p e_p v_p over this lane's positions, then over the lanes
+    // holding the same eight values (across the wave, then across waves)
+    float o[MAXG][8];
 #pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g) o[g] = 0.f;
-        const int tn = len - t0 < kAttnChunk ? len - t0 : kAttnChunk;
-        for (int i = 0; i < tn; ++i) {
-            const float vv = __half2float(vbase[(size_t)(t0 + i) * hd + d]);
+    for (int g = 0; g < MAXG; ++g)
 #pragma unroll
-            for (int g = 0; g < kAttnMaxGroup; ++g)
-                if (g < group) o[g] = fmaf(sc[g][i], vv, o[g]);
+        for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+        float vv[8];
+#pragma unroll
+        for (int h2 = 0; h2 < 4; ++h2) {
+            vv[2 * h2] = half_lo(w4[h2]);
+            vv[2 * h2 + 1] = half_hi(w4[h2]);
         }
-        const int nchunks = gridDim.y;
+        const int pl = slot + j * PPS;
 #pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g)
-            if (g < group) part_o[((size_t)(kh * group + g) * nchunks + chunk) * hd + d] = o[g];
+        for (int g = 0; g < MAXG; ++g) {
+            const float wgt = g < group ? sc[g][pl] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] = fmaf(wgt, vv[e], o[g][e]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            for (int off = LPP; off < 64; off <<= 1) o[g][e] += __shfl_xor(o[g][e], off);
+    if (lane < LPP) {
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[wave][g * HD + b * 8 + e] = o[g][e];
+    }
+    __syncthreads();
+    for (int i = t; i < group * HD; i += kAttnThreads) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) acc += red[w][i];
+        const int g = i / HD, d = i % HD;
+        ws.o[((size_t)(kh * group + g) * nchunks + chunk) * HD + d] = acc;
     }
     if (t < group) {
-        const int nchunks = gridDim.y;
-        part_ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 0] = ml[t][0];
-        part_ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 1] = ml[t][1];
+        ws.ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 0] = ml[t][0];
+        ws.ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 1] = ml[t][1];
     }
 }
 
-// out[h][d] = sum_c o_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, chunks in order.
-__global__ void __launch_bounds__(256) attn_combine_kernel(const float* part_ml, const float* part_o, const int* pos_dev,
-                                                           int nq, int hd, int max_ctx, int nchunks_alloc, float* out) {
-    const int h = blockIdx.x;
+// out[h] = sum_c w_c o_c with w_c = e^(m_c - M) / sum_c l_c e^(m_c - M) over
+// the live chunks of query head h. Each thread takes one 16-byte column of the
+// head and every cl_n-th chunk (its loads independent of each other); the
+// chunk lanes are then summed in order through LDS.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const int* pos_dev, int max_ctx, int nchunks,
+                                                           float* out) {
+    constexpr int COLS4 = HD / 4;
+    constexpr int CLN = 256 / COLS4;
+    __shared__ float wts[kAttnMaxChunks];
+    __shared__ float part[2][4];
+    __shared__ float4 cred[256];
+    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int len = min(*pos_dev + 1, max_ctx);
-    const int nchunks = (len + kAttnChunk - 1) / kAttnChunk;
-    const float* ml = part_ml + (size_t)h * nchunks_alloc * 2;
+    const int live = (len + kAttnChunk - 1) / kAttnChunk;
+    const float* hml = ws.ml + (size_t)h * nchunks * 2;
+    // M and L over the chunks: each wave a strided share, then across the four waves
     float M = -INFINITY;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, ml[2 * c]);
+    for (int c = t; c < live; c += 256) M = fmaxf(M, hml[2 * c]);
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) part[0][wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
     float L = 0.f;
-    for (int c = 0; c < nchunks; ++c) L += ml[2 * c + 1] * expf(ml[2 * c] - M);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float o = 0.f;
-        for (int c = 0; c < nchunks; ++c) o = fmaf(part_o[((size_t)h * nchunks_alloc + c) * hd + d], expf(ml[2 * c] - M), o);
-        out[(size_t)h * hd + d] = o / L;
+    for (int c = t; c < live; c += 256) {
+        const float e = __expf(hml[2 * c] - M);
+        wts[c] = e;
+        L += hml[2 * c + 1] * e;
+    }
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+    if (lane == 0) part[1][wave] = L;
+    __syncthreads();
+    const float inv = 1.0f / ((part[1][0] + part[1][1]) + (part[1][2] + part[1][3]));
+    const int col = t % COLS4, cl = t / COLS4;
+    const float* po = ws.o + (size_t)h * nchunks * HD + col * 4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+    for (int c = cl; c < live; c += CLN) {
+        const float4 v = *reinterpret_cast<const float4*>(po + (size_t)c * HD);
+        const float w = wts[c];
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
+    }
+    cred[t] = acc;
+    __syncthreads();
+    if (t < COLS4) {
+        float4 o4 = cred[t];
+        for (int k = 1; k < CLN; ++k) {
+            const float4 v = cred[k * COLS4 + t];
+            o4.x += v.x, o4.y += v.y, o4.z += v.z, o4.w += v.w;
+        }
+        o4.x *= inv, o4.y *= inv, o4.z *= inv, o4.w *= inv;
+        *reinterpret_cast<float4*>(out + (size_t)h * HD + t * 4) = o4;
     }
 }
 
@@ -224,33 +335,68 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const float* gu, int n, f
 
 // ------------------------------------------------------------- argmax ----
 
-// The index of the largest value (the lowest index on a tie); one workgroup.
-__global__ void __launch_bounds__(1024) argmax_kernel(const float* v, int n, int* out) {
-    __shared__ float bv[1024];
-    __shared__ int bi[1024];
+// The index of the largest value (the lowest index on a tie; NaNs are
+// skipped), in two launches: kArgmaxBlocks workgroups each take a contiguous
+// slice and leave their best (value, index) in the workspace, then one
+// workgroup reduces those.
+constexpr int kArgmaxBlocks = 128;
+constexpr int kArgmaxThreads = 256;
+
+__device__ __forceinline__ bool beats(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void block_best(float& best, int& idx) {
+    __shared__ float bv[kArgmaxThreads];
+    __shared__ int bi[kArgmaxThreads];
     const int t = threadIdx.x;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = t; i < n; i += blockDim.x)
-        if (v[i] > best) {  // ascending i: keeps the lowest index on a tie
-            best = v[i];
-            idx = i;
-        }
     bv[t] = best;
     bi[t] = idx;
     __syncthreads();
-    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-        if (t < s) {
-            const float ov = bv[t + s];
-            const int oi = bi[t + s];
-            if (ov > bv[t] || (ov == bv[t] && oi < bi[t])) {
-                bv[t] = ov;
-                bi[t] = oi;
-            }
+    for (int s = kArgmaxThreads / 2; s > 0; s >>= 1) {
+        if (t < s && beats(bv[t + s], bi[t + s], bv[t], bi[t])) {
+            bv[t] = bv[t + s];
+            bi[t] = bi[t + s];
         }
         __syncthreads();
     }
-    if (t == 0) *out = bi[0];
+    best = bv[0];
+    idx = bi[0];
+}
+
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_part_kernel(const float* v, int n, float* part_v,
+                                                                     int* part_i) {
+    const int t = threadIdx.x;
+    const int per = (n + gridDim.x - 1) / gridDim.x;
+    const int lo = blockIdx.x * per, hi = min(n, lo + per);
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = lo + t; i < hi; i += kArgmaxThreads) {
+        const float x = v[i];
+        if (beats(x, i, best, idx)) {
+            best = x;
+            idx = i;
+        }
+    }
+    block_best(best, idx);
+    if (t == 0) {
+        part_v[blockIdx.x] = best;
+        part_i[blockIdx.x] = idx;
+    }
+}
+
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_final_kernel(const float* part_v, const int* part_i, int parts,
+                                                                      int* out) {
+    const int t = threadIdx.x;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int b = t; b < parts; b += kArgmaxThreads)
+        if (beats(part_v[b], part_i[b], best, idx)) {
+            best = part_v[b];
+            idx = part_i[b];
+        }
+    block_best(best, idx);
+    if (t == 0) *out = idx == 0x7fffffff ? 0 : idx;
 }
 
 // out = table[token mod rows] (the next token's embedding row).
@@ -284,25 +430,48 @@ hipError_t launch_rope_kv(float* qkv, const int* pos, int nq, int nkv, int hd, d
 
 size_t attention_workspace_bytes(int nq, int hd, int max_ctx) {
     const size_t nchunks = (size_t)(max_ctx + kAttnChunk - 1) / kAttnChunk;
-    return nq * nchunks * 2 * sizeof(float) + nq * nchunks * (size_t)hd * sizeof(float);
+    return (nq * nchunks * 2 + nq * nchunks * (size_t)hd) * sizeof(float);
+}
+
+template <int HD, int MAXG>
+static void launch_attention_t(const float* q, const __half* kc, const __half* vc, const int* pos, int nkv, int group,
+                               int max_ctx, AttnWork ws, int nchunks, float* out, hipStream_t stream) {
+    const float scale = 1.0f / sqrtf((float)HD);
+    hipLaunchKernelGGL((attention_kernel<HD, MAXG>), dim3(nkv, nchunks), dim3(kAttnThreads), 0, stream, q, kc, vc, pos,
+                       nkv, group, max_ctx, scale, ws, nchunks);
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(nkv * group), dim3(256), 0, stream, ws, pos, max_ctx, nchunks,
+                       out);
+}
+
+template <int HD>
+static void launch_attention_hd(const float* q, const __half* kc, const __half* vc, const int* pos, int nkv, int group,
+                                int max_ctx, AttnWork ws, int nchunks, float* out, hipStream_t stream) {
+    if (group <= 1)
+        launch_attention_t<HD, 1>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+    else if (group <= 2)
+        launch_attention_t<HD, 2>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+    else if (group <= 4)
+        launch_attention_t<HD, 4>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+    else
+        launch_attention_t<HD, 8>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
 }
 
 hipError_t launch_attention(const float* q, const __half* kc, const __half* vc, const int* pos, int nq, int nkv,
                             int hd, int max_ctx, void* workspace, float* out, hipStream_t stream) {
-    if (nkv < 1 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || hd % 64 != 0 || hd > kAttnMaxHead)
+    if (nkv < 1 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || (hd != 64 && hd != 128 && hd != 256) ||
+        max_ctx > kAttnMaxChunks * kAttnChunk)
         return hipErrorInvalidValue;
     const int nchunks = (max_ctx + kAttnChunk - 1) / kAttnChunk;
-    float* part_ml = static_cast<float*>(workspace);
-    float* part_o = part_ml + (size_t)nq * nchunks * 2;
-    const float scale = 1.0f / sqrtf((float)hd);
-    // every chunk of the allocation runs; chunks past the position write -inf
-    // maxima and zero sums that the combine ignores (it reads only the live ones)
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(nkv, nchunks), dim3(256), 0, stream, q, kc, vc, pos, nq, nkv, hd,
-                       max_ctx, scale, part_ml, part_o);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(nq), dim3(256), 0, stream, part_ml, part_o, pos, nq, hd, max_ctx, nchunks,
-                       out);
+    const int group = nq / nkv;
+    const AttnWork ws = attn_work(workspace, nq, hd, nchunks);
+    // every chunk of the allocation is launched (the grid stays fixed while the
+    // position advances under a captured graph); chunks past the position leave at once
+    if (hd == 64)
+        launch_attention_hd<64>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+    else if (hd == 128)
+        launch_attention_hd<128>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+    else
+        launch_attention_hd<256>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
     return hipGetLastError();
 }
 
@@ -313,8 +482,14 @@ hipError_t launch_silu_mul(const float* gu, int n, float* out, hipStream_t strea
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* v, int n, int* out, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, stream, v, n, out);
+size_t argmax_workspace_bytes() { return kArgmaxBlocks * (sizeof(float) + sizeof(int)); }
+
+hipError_t launch_argmax(const float* v, int n, int* out, void* workspace, hipStream_t stream) {
+    float* part_v = static_cast<float*>(workspace);
+    int* part_i = reinterpret_cast<int*>(part_v + kArgmaxBlocks);
+    const int blocks = n < kArgmaxBlocks * kArgmaxThreads ? (n + kArgmaxThreads - 1) / kArgmaxThreads : kArgmaxBlocks;
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(blocks), dim3(kArgmaxThreads), 0, stream, v, n, part_v, part_i);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, stream, part_v, part_i, blocks, out);
     return hipGetLastError();
 }
 

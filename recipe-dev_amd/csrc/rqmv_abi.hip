@@ -422,8 +422,9 @@ int rqmv_rope_kv(float* qkv, const int* pos, int q_heads, int kv_heads, int head
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "rope_kv launch");
 }
 
-int rqmv_attention_workspace_size(int q_heads, int head_dim, int max_ctx, size_t* bytes) {
-    if (q_heads <= 0 || head_dim <= 0 || max_ctx <= 0 || !bytes) return fail(RQMV_EINVAL, "attention: bad arguments");
+int rqmv_attention_workspace_size(int q_heads, int kv_heads, int head_dim, int max_ctx, size_t* bytes) {
+    if (q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || max_ctx <= 0 || !bytes)
+        return fail(RQMV_EINVAL, "attention: bad arguments");
     *bytes = rq::attention_workspace_bytes(q_heads, head_dim, max_ctx);
     return RQMV_OK;
 }
@@ -432,8 +433,12 @@ int rqmv_attention(const float* q, const void* k_cache, const void* v_cache, con
                    int head_dim, int max_ctx, void* workspace, size_t workspace_bytes, float* out, void* stream) {
     if (!q || !k_cache || !v_cache || !pos || !workspace || !out || q_heads <= 0 || kv_heads <= 0 || max_ctx <= 0)
         return fail(RQMV_EINVAL, "attention: bad arguments");
-    if (q_heads % kv_heads || q_heads / kv_heads > 8 || head_dim % 64 || head_dim > 256)
-        return fail(RQMV_EINVAL, "attention: q_heads must be 1..8 x kv_heads and head_dim a multiple of 64 up to 256");
+    if (q_heads % kv_heads || q_heads / kv_heads > 8 || (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+        max_ctx > 65536)
+        return fail(RQMV_EINVAL,
+                    "attention: q_heads must be 1..8 x kv_heads, head_dim 64, 128 or 256, max_ctx at most 65536");
+    if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out | (uintptr_t)workspace) & 15)
+        return fail(RQMV_EINVAL, "attention: q, caches, workspace and out must be 16-byte aligned");
     if (workspace_bytes < rq::attention_workspace_bytes(q_heads, head_dim, max_ctx))
         return fail(RQMV_EINVAL, "attention: workspace too small");
     hipError_t e = rq::launch_attention(q, static_cast<const __half*>(k_cache), static_cast<const __half*>(v_cache), pos,
@@ -448,9 +453,16 @@ int rqmv_silu_mul(const float* gate_up, int n, float* out, void* stream) {
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "silu_mul launch");
 }
 
-int rqmv_argmax(const float* values, int n, int* out, void* stream) {
-    if (!values || !out || n <= 0) return fail(RQMV_EINVAL, "argmax: bad arguments");
-    hipError_t e = rq::launch_argmax(values, n, out, static_cast<hipStream_t>(stream));
+int rqmv_argmax_workspace_size(size_t* bytes) {
+    if (!bytes) return fail(RQMV_EINVAL, "argmax: NULL size");
+    *bytes = rq::argmax_workspace_bytes();
+    return RQMV_OK;
+}
+
+int rqmv_argmax(const float* values, int n, int* out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!values || !out || !workspace || n <= 0) return fail(RQMV_EINVAL, "argmax: bad arguments");
+    if (workspace_bytes < rq::argmax_workspace_bytes()) return fail(RQMV_EINVAL, "argmax: workspace too small");
+    hipError_t e = rq::launch_argmax(values, n, out, workspace, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "argmax launch");
 }
 

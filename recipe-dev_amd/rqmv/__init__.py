@@ -59,11 +59,12 @@ class _Lib:
         L.rqmv_add_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]
         L.rqmv_rope_kv.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, ctypes.c_double, c_void_p, c_void_p, c_int,
                                    c_void_p]
-        L.rqmv_attention_workspace_size.argtypes = [c_int, c_int, c_int, POINTER(c_size_t)]
+        L.rqmv_attention_workspace_size.argtypes = [c_int, c_int, c_int, c_int, POINTER(c_size_t)]
         L.rqmv_attention.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
                                      c_size_t, c_void_p, c_void_p]
         L.rqmv_silu_mul.argtypes = [c_void_p, c_int, c_void_p, c_void_p]
-        L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p]
+        L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_void_p]
+        L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
         L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
         L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t)]
@@ -419,10 +420,21 @@ def rope_kv(qkv: DeviceBuffer, pos: DeviceBuffer, q_heads: int, kv_heads: int, h
                                   max_ctx, _sh(stream)), "rqmv_rope_kv")
 
 
-def attention_workspace_size(q_heads: int, head_dim: int, max_ctx: int) -> int:
+def attention_workspace_size(q_heads: int, kv_heads: int, head_dim: int, max_ctx: int) -> int:
     n = c_size_t()
-    _check(lib().lib.rqmv_attention_workspace_size(q_heads, head_dim, max_ctx, byref(n)), "rqmv_attention_workspace_size")
+    _check(lib().lib.rqmv_attention_workspace_size(q_heads, kv_heads, head_dim, max_ctx, byref(n)),
+           "rqmv_attention_workspace_size")
     return n.value
+
+
+def attention_workspace(q_heads: int, kv_heads: int, head_dim: int, max_ctx: int) -> DeviceBuffer:
+    return DeviceBuffer(attention_workspace_size(q_heads, kv_heads, head_dim, max_ctx))
+
+
+def argmax_workspace() -> DeviceBuffer:
+    n = c_size_t()
+    _check(lib().lib.rqmv_argmax_workspace_size(byref(n)), "rqmv_argmax_workspace_size")
+    return DeviceBuffer(n.value)
 
 
 def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, pos: DeviceBuffer, q_heads: int,
@@ -436,8 +448,8 @@ def silu_mul(gate_up: DeviceBuffer, n: int, out: DeviceBuffer, stream: Stream | 
     _check(lib().lib.rqmv_silu_mul(gate_up.ptr, n, out.ptr, _sh(stream)), "rqmv_silu_mul")
 
 
-def argmax(values: DeviceBuffer, n: int, out: DeviceBuffer, stream: Stream | None = None):
-    _check(lib().lib.rqmv_argmax(values.ptr, n, out.ptr, _sh(stream)), "rqmv_argmax")
+def argmax(values: DeviceBuffer, n: int, out: DeviceBuffer, workspace: DeviceBuffer, stream: Stream | None = None):
+    _check(lib().lib.rqmv_argmax(values.ptr, n, out.ptr, workspace.ptr, workspace.nbytes, _sh(stream)), "rqmv_argmax")
 
 
 def advance(pos: DeviceBuffer, stream: Stream | None = None):

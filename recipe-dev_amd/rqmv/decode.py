@@ -28,8 +28,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (DTYPE_F32, DeviceBuffer, Graph, Stream, Weight, add_rmsnorm, advance, argmax, attention,
-               attention_workspace_size, embed_row, rope_kv, silu_mul)
+from . import (DTYPE_F32, DeviceBuffer, Graph, Stream, Weight, add_rmsnorm, advance, argmax, argmax_workspace,
+               attention, attention_workspace, embed_row, rope_kv, silu_mul)
 
 
 @dataclass(frozen=True)
@@ -57,8 +57,8 @@ class DecoderShape:
             raise ValueError("q_heads * head_dim must equal d")
         if self.q_heads % self.kv_heads or self.q_heads // self.kv_heads > 8:
             raise ValueError("q_heads must be a multiple of kv_heads, at most 8 per kv head")
-        if self.head_dim % 64 or self.head_dim > 256:
-            raise ValueError("head_dim must be a multiple of 64 up to 256")
+        if self.head_dim not in (64, 128, 256):
+            raise ValueError("head_dim must be 64, 128 or 256")
 
 
 @dataclass
@@ -104,7 +104,8 @@ class DecodeModel:
         self.logits = DeviceBuffer(s.vocab * f32)
         self.token = DeviceBuffer(4)
         self.pos = DeviceBuffer(4)
-        self.workspace = DeviceBuffer(attention_workspace_size(s.q_heads, s.head_dim, self.max_ctx))
+        self.workspace = attention_workspace(s.q_heads, s.kv_heads, s.head_dim, self.max_ctx)
+        self.argmax_ws = argmax_workspace()
 
     # ---------------------------------------------------------------- setup
     def set_layer(self, index: int, t: LayerTensors):
@@ -157,7 +158,7 @@ class DecodeModel:
             L["down"].matvec(self.h, DTYPE_F32, 1, s.ffn, self.f, s.d, stream)
         add_rmsnorm(self.x, self.f, self.out_norm, s.d, s.eps, self.xn, stream)
         self.head.matvec(self.xn, DTYPE_F32, 1, s.d, self.logits, s.vocab, stream)
-        argmax(self.logits, s.vocab, self.token, stream)
+        argmax(self.logits, s.vocab, self.token, self.argmax_ws, stream)
         advance(self.pos, stream)
 
     def capture(self, stream: Stream) -> Graph:

@@ -96,7 +96,7 @@ def test_attention(gpu, nq, nkv, hd, length):
     Q = gpu.DeviceBuffer.from_array(q)
     K = gpu.DeviceBuffer.from_array(kc.view(np.uint16))
     V = gpu.DeviceBuffer.from_array(vc.view(np.uint16))
-    ws = gpu.DeviceBuffer(gpu.attention_workspace_size(nq, hd, max_ctx))
+    ws = gpu.attention_workspace(nq, nkv, hd, max_ctx)
     O = gpu.DeviceBuffer(nq * hd * 4)
     gpu.attention(Q, K, V, _i32(gpu, length - 1), nq, nkv, hd, max_ctx, ws, O)
     gpu.synchronize()
@@ -112,7 +112,7 @@ def test_attention_long_context(gpu):
     Q = gpu.DeviceBuffer.from_array(q)
     K = gpu.DeviceBuffer.from_array(kc.view(np.uint16))
     V = gpu.DeviceBuffer.from_array(vc.view(np.uint16))
-    ws = gpu.DeviceBuffer(gpu.attention_workspace_size(nq, hd, max_ctx))
+    ws = gpu.attention_workspace(nq, nkv, hd, max_ctx)
     O = gpu.DeviceBuffer(nq * hd * 4)
     for length in (4096, 4097, max_ctx):
         gpu.attention(Q, K, V, _i32(gpu, length - 1), nq, nkv, hd, max_ctx, ws, O)
@@ -145,9 +145,11 @@ def test_argmax_lowest_index_on_ties(gpu, n):
         v[n // 3] = v[n - 2] = v.max() + 1.0  # a tie: the lower index wins
         v[5] = -np.inf
     V, O = gpu.DeviceBuffer.from_array(v), gpu.DeviceBuffer(4)
-    gpu.argmax(V, n, O)
-    gpu.synchronize()
-    assert int(O.download(np.int32, 1)[0]) == int(np.argmax(v))
+    ws = gpu.argmax_workspace()
+    for _ in range(2):  # a second call over the same workspace
+        gpu.argmax(V, n, O, ws)
+        gpu.synchronize()
+        assert int(O.download(np.int32, 1)[0]) == int(np.argmax(v))
 
 
 def test_embed_row(gpu):
