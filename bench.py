@@ -277,7 +277,7 @@ def decode_bench(args):
                                "NeoX rotary base 500000, SiLU-GLU 14336, RMSNorm 1e-5, Q4_K projections, "
                                "Q8_0 head 128256, fp16 KV cache prefilled to 4096",
                    "bytes_per_token": int(bytes_per_token), "positions": [pos0, pos0 + args.steps - 1],
-                   "launches_per_token": 1 + 10 * s.layers + 5, "activations": "f32", "kv_cache": "f16",
+                   "launches_per_token": 1 + 6 * s.layers + 4, "activations": "f32", "kv_cache": "f16",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
@@ -290,13 +290,13 @@ def decode_bench(args):
         # recipe's CPU float path on layer 0's four projections, timed per layer
         # and scaled to 32 layers, plus the head, plus f64 attention over one
         # layer's cache scaled to 32 layers
-        xs = {"qkv": s.d, "o": s.d, "gate_up": s.d, "down": s.ffn}
-        rows = {"qkv": s.qkv_rows, "o": s.d, "gate_up": 2 * s.ffn, "down": s.d}
+        xs = {"qkv": s.d, "o": s.d, "gate": s.d, "up": s.d, "down": s.ffn}
+        rows = {"qkv": s.qkv_rows, "o": s.d, "gate": s.ffn, "up": s.ffn, "down": s.d}
         rng = np.random.default_rng(0)
         t0 = time.perf_counter()
         runs = 0
         while time.perf_counter() - t0 < args.cpu_seconds * 0.6:
-            for k in ("qkv", "o", "gate_up", "down"):
+            for k in ("qkv", "o", "gate", "up", "down"):
                 oracle.matvec_recipe_f32(s.proj_fmt, getattr(layer0, k), rows[k], xs[k],
                                          rng.standard_normal(xs[k]).astype(np.float32), threads=cores)
             runs += 1

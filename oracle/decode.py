@@ -98,8 +98,8 @@ class DecoderReference:
                 "qkv": dequant_rows(s.proj_fmt, t.qkv, qkv_rows, s.d).reshape(qkv_rows, s.d).astype(np.float64),
                 "o": dequant_rows(s.proj_fmt, t.o, s.d, s.d).reshape(s.d, s.d).astype(np.float64),
                 "ffn_norm": np.asarray(t.ffn_norm, dtype=np.float64),
-                "gate_up": dequant_rows(s.proj_fmt, t.gate_up, 2 * s.ffn, s.d).reshape(2 * s.ffn, s.d)
-                .astype(np.float64),
+                "gate": dequant_rows(s.proj_fmt, t.gate, s.ffn, s.d).reshape(s.ffn, s.d).astype(np.float64),
+                "up": dequant_rows(s.proj_fmt, t.up, s.ffn, s.d).reshape(s.ffn, s.d).astype(np.float64),
                 "down": dequant_rows(s.proj_fmt, t.down, s.d, s.ffn).reshape(s.d, s.ffn).astype(np.float64),
             })
         self.k, self.v = [], []
@@ -128,6 +128,5 @@ class DecoderReference:
             a = attention(q, self.k[i], self.v[i], pos + 1).reshape(-1)
             x = x + L["o"] @ a
             xn = rmsnorm(x, L["ffn_norm"], s.eps)
-            gu = L["gate_up"] @ xn
-            x = x + L["down"] @ silu_mul(gu[:s.ffn], gu[s.ffn:])
+            x = x + L["down"] @ silu_mul(L["gate"] @ xn, L["up"] @ xn)
         return self.head @ rmsnorm(x, self.out_norm, s.eps)

@@ -83,25 +83,40 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(float* qkv, const int* pos
 
 // ---------------------------------------------------------- attention ----
 
-// Split over positions (flash decoding), in two launches. attention_kernel:
-// one workgroup of kAttnThreads per (kv head, chunk of kAttnChunk positions);
-// a chunk is read once for every query head of its group. Lanes take one
-// 16-byte piece (eight values) of a position's key and value: HD / 8 lanes per
-// position, the whole chunk's keys and values loaded into registers before
-// any arithmetic. Pass 1: each query head's score against each position (an
-// eight-value dot per lane, summed over the position's lanes), times
-// 1/sqrt(HD), into LDS. Pass 2: per query head (one wave each) the chunk's
-// maximum m, weights e = exp(s - m) and their sum l. Pass 3: o = sum e v, per
-// lane over its positions, summed over the lanes that hold the same values.
-// The chunk's (m, l, o) go to the workspace. attn_combine_kernel: one
-// workgroup per query head merges the live chunks, out = sum_c o_c
-// e^(m_c - M) / sum_c l_c e^(m_c - M), chunks in order. (A single launch
-// whose last workgroup merges costs more: publishing the partial results
-// across the XCDs' L2 caches takes an L2 write-back per workgroup.)
-constexpr int kAttnChunk = 128;
-constexpr int kAttnThreads = 512;
+// Split over positions (flash decoding), in two launches.
+//
+// attention_kernel: one workgroup of kAttnThreads per (kv head, chunk of
+// kAttnChunk positions); a chunk is read once for every query head of its
+// group. Lanes take one 16-byte piece (eight values) of a position's key and
+// value: HD / 8 lanes per position, the whole chunk's keys and values loaded
+// into registers before any arithmetic (addresses clamped into the cache;
+// positions past the end are masked by selection, never by multiplying, so
+// stale cache contents cannot leak in). Pass 1: each query head's score
+// against each position (an eight-value dot per lane, summed over the
+// position's lanes), times 1/sqrt(HD), into LDS. Pass 2: per query head the
+// chunk's maximum m, weights e = exp(s - m) and their sum l. Pass 3: o = sum e
+// v, per lane over its positions, summed over the lanes that hold the same
+// values. The chunk's (m, l, o) go to the workspace.
+//
+// ROPE (the decode step's fused form): q and the new key come unrotated in
+// qkv ([q heads | k heads | v heads]) and are turned here with a cos/sin table
+// (rope_table_kernel); the chunk holding the position takes the new key and
+// value (rounded to fp16, as the cache holds them) instead of the cache's
+// entry and stores them into the cache.
+//
+// attn_combine_kernel: one workgroup per query head merges the live chunks,
+// out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), chunks in order. Its
+// loads do not depend on the position (every allocated chunk's partials are
+// read and the dead ones dropped by selection), so they all go out at once.
+//
+// (A single launch whose last workgroup merges costs more: publishing the
+// partial results across the XCDs' L2 caches takes an L2 write-back per
+// workgroup.)
+constexpr int kAttnChunk = 64;
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kAttnMaxGroup = 8;      // query heads per kv head
-constexpr int kAttnMaxChunks = 512;   // max_ctx up to 65536
+constexpr int kAttnMaxChunks = 1024;  // max_ctx up to 65536
 
 template <int LPP>
 __device__ __forceinline__ float sum_lanes(float v) {
@@ -128,62 +143,120 @@ __host__ __device__ inline AttnWork attn_work(void* ws, int nq, int hd, int nchu
     return w;
 }
 
-template <int HD, int MAXG>
-__global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q, const __half* kc, const __half* vc,
-                                                                 const int* pos_dev, int nkv, int group, int max_ctx,
-                                                                 float scale, AttnWork ws, int nchunks) {
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p), c = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = c.x, v[5] = c.y, v[6] = c.z, v[7] = c.w;
+}
+
+__device__ __forceinline__ void unpack8(const uint4& r, float (&v)[8]) {
+    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int h2 = 0; h2 < 4; ++h2) {
+        v[2 * h2] = half_lo(w4[h2]);
+        v[2 * h2 + 1] = half_hi(w4[h2]);
+    }
+}
+
+__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int h2 = 0; h2 < 4; ++h2)
+        w[h2] = (uint32_t)__half_as_ushort(__float2half(v[2 * h2])) |
+                ((uint32_t)__half_as_ushort(__float2half(v[2 * h2 + 1])) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// NeoX rotation of the eight values x (dims 8b..8b+7 of a head) given their
+// partners xp (dims 8b +- HD/2) and the position's (cos, sin) row.
+template <int HD>
+__device__ __forceinline__ void rotate8(float (&x)[8], const float (&xp)[8], const float2* cs_row, int b) {
+    constexpr int HALF = HD / 2;
+    const bool upper = 8 * b >= HALF;
+    const int i0 = 8 * b - (upper ? HALF : 0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float2 cs = cs_row[i0 + e];
+        // lower half: x_i c - x_{i+half} s; upper half: x_{i+half} c + x_i s
+        x[e] = upper ? x[e] * cs.x + xp[e] * cs.y : x[e] * cs.x - xp[e] * cs.y;
+    }
+}
+
+template <int HD, int MAXG, bool ROPE>
+__global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q, const float* kv_new, __half* kc,
+                                                                 __half* vc, const float2* rope, const int* pos_dev,
+                                                                 int nkv, int group, int max_ctx, float scale,
+                                                                 AttnWork ws, int nchunks) {
     constexpr int LPP = HD / 8;                    // lanes per position
     constexpr int PPS = kAttnThreads / LPP;        // positions per sweep
     constexpr int NS = kAttnChunk / PPS;           // sweeps per chunk
-    constexpr int WAVES = kAttnThreads / 64;
+    constexpr int HALF = HD / 2;
     __shared__ float sc[MAXG][kAttnChunk];
     __shared__ float ml[MAXG][2];
-    __shared__ float red[WAVES][MAXG * HD];
+    __shared__ float red[kAttnWaves][MAXG * HD];
     const int kh = blockIdx.x, chunk = blockIdx.y;
-    const int len = min(*pos_dev + 1, max_ctx);
+    const int pos = *pos_dev;
+    const int len = min(pos + 1, max_ctx);  // positions past the cache are not read
     const int t0 = chunk * kAttnChunk;
     if (t0 >= len) return;  // a chunk past the position: nothing to read (the whole workgroup leaves)
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int b = t % LPP, slot = t / LPP;
-    const int nq = nkv * group;
+    const int pb = (b + LPP / 2) % LPP;  // the lane piece holding the rotation partners
+    const float2* cs_row = rope + (size_t)min(pos, max_ctx - 1) * HALF;  // the table has max_ctx rows
 
-    // keys and values of this lane's positions; positions past the end read the last live one (weight 0)
+    // keys and values of this lane's positions (clamped into the cache; masked below)
     uint4 kr[NS], vr[NS];
     const size_t head_base = (size_t)kh * max_ctx;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const int p = min(t0 + slot + j * PPS, len - 1);
+        const int p = min(t0 + slot + j * PPS, max_ctx - 1);
         kr[j] = *reinterpret_cast<const uint4*>(kc + (head_base + p) * HD + b * 8);
     }
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const int p = min(t0 + slot + j * PPS, len - 1);
+        const int p = min(t0 + slot + j * PPS, max_ctx - 1);
         vr[j] = *reinterpret_cast<const uint4*>(vc + (head_base + p) * HD + b * 8);
     }
     float qr[MAXG][8];
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
         if (g < group) {
-            const float4* qs = reinterpret_cast<const float4*>(q + ((size_t)(kh * group + g) * HD + b * 8));
-            const float4 a = qs[0], c = qs[1];
-            qr[g][0] = a.x, qr[g][1] = a.y, qr[g][2] = a.z, qr[g][3] = a.w;
-            qr[g][4] = c.x, qr[g][5] = c.y, qr[g][6] = c.z, qr[g][7] = c.w;
+            load8(q + (size_t)(kh * group + g) * HD + b * 8, qr[g]);
+            if constexpr (ROPE) {
+                float qp[8];
+                load8(q + (size_t)(kh * group + g) * HD + pb * 8, qp);
+                rotate8<HD>(qr[g], qp, cs_row, b);
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) qr[g][e] = 0.f;
+        }
+    }
+    if constexpr (ROPE) {
+        // the new position's key and value replace the cache entry in the chunk that holds it
+        const int jn = pos - t0 - slot;
+        if (pos < max_ctx && jn >= 0 && jn < kAttnChunk && jn % PPS == 0) {
+            float kn[8], kp[8], vn[8];
+            load8(kv_new + (size_t)kh * HD + b * 8, kn);
+            load8(kv_new + (size_t)kh * HD + pb * 8, kp);
+            load8(kv_new + (size_t)(nkv + kh) * HD + b * 8, vn);
+            rotate8<HD>(kn, kp, cs_row, b);
+            const uint4 k16 = pack8(kn), v16 = pack8(vn);
+            *reinterpret_cast<uint4*>(kc + (head_base + pos) * HD + b * 8) = k16;
+            *reinterpret_cast<uint4*>(vc + (head_base + pos) * HD + b * 8) = v16;
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+                if (j == jn / PPS) {
+                    kr[j] = k16;
+                    vr[j] = v16;
+                }
         }
     }
 
     // pass 1: scores
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
         float kv[8];
-#pragma unroll
-        for (int h2 = 0; h2 < 4; ++h2) {
-            kv[2 * h2] = half_lo(w4[h2]);
-            kv[2 * h2 + 1] = half_hi(w4[h2]);
-        }
+        unpack8(kr[j], kv);
         const int pl = slot + j * PPS;
 #pragma unroll
         for (int g = 0; g < MAXG; ++g) {
@@ -196,17 +269,14 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     }
     __syncthreads();
 
-    // pass 2: per query head, the chunk's maximum, weights and their sum
-    for (int g = wave; g < group; g += WAVES) {
-        float m = -INFINITY;
-        for (int i = lane; i < kAttnChunk; i += 64) m = fmaxf(m, sc[g][i]);
+    // pass 2: per query head, the chunk's maximum, weights and their sum (one position per lane)
+    for (int g = wave; g < group; g += kAttnWaves) {
+        const float s = sc[g][lane];
+        float m = s;
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        float l = 0.f;
-        for (int i = lane; i < kAttnChunk; i += 64) {
-            const float e = sc[g][i] == -INFINITY ? 0.f : __expf(sc[g][i] - m);
-            sc[g][i] = e;
-            l += e;
-        }
+        const float e = s == -INFINITY ? 0.f : __expf(s - m);
+        sc[g][lane] = e;
+        float l = e;
         for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
         if (lane == 0) {
             ml[g][0] = m;
@@ -224,14 +294,12 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
         for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
         float vv[8];
-#pragma unroll
-        for (int h2 = 0; h2 < 4; ++h2) {
-            vv[2 * h2] = half_lo(w4[h2]);
-            vv[2 * h2 + 1] = half_hi(w4[h2]);
-        }
+        unpack8(vr[j], vv);
         const int pl = slot + j * PPS;
+        const bool live = t0 + pl < len;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vv[e] = live ? vv[e] : 0.f;
 #pragma unroll
         for (int g = 0; g < MAXG; ++g) {
             const float wgt = g < group ? sc[g][pl] : 0.f;
@@ -254,7 +322,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     for (int i = t; i < group * HD; i += kAttnThreads) {
         float acc = 0.f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) acc += red[w][i];
+        for (int w = 0; w < kAttnWaves; ++w) acc += red[w][i];
         const int g = i / HD, d = i % HD;
         ws.o[((size_t)(kh * group + g) * nchunks + chunk) * HD + d] = acc;
     }
@@ -266,42 +334,73 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 
 // out[h] = sum_c w_c o_c with w_c = e^(m_c - M) / sum_c l_c e^(m_c - M) over
 // the live chunks of query head h. Each thread takes one 16-byte column of the
-// head and every cl_n-th chunk (its loads independent of each other); the
-// chunk lanes are then summed in order through LDS.
+// head and every CLN-th chunk; its first kPre chunks are loaded with the
+// position and the chunk maxima, before anything is known of which are live.
+// The chunk lanes are then summed in order through LDS.
 template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const int* pos_dev, int max_ctx, int nchunks,
                                                            float* out) {
     constexpr int COLS4 = HD / 4;
     constexpr int CLN = 256 / COLS4;
+    constexpr int kPre = 12;
+    constexpr int kMlPer = kAttnMaxChunks / 256;
     __shared__ float wts[kAttnMaxChunks];
     __shared__ float part[2][4];
     __shared__ float4 cred[256];
     const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float* hml = ws.ml + (size_t)h * nchunks * 2;
+    const int col = t % COLS4, cl = t / COLS4;
+    const float* po = ws.o + (size_t)h * nchunks * HD + col * 4;
+    float4 pre[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        const int c = min(cl + k * CLN, nchunks - 1);
+        pre[k] = *reinterpret_cast<const float4*>(po + (size_t)c * HD);
+    }
+    float2 mlv[kMlPer];
+#pragma unroll
+    for (int k = 0; k < kMlPer; ++k) {
+        const int c = min(t + 256 * k, nchunks - 1);
+        mlv[k] = *reinterpret_cast<const float2*>(hml + 2 * c);
+    }
     const int len = min(*pos_dev + 1, max_ctx);
     const int live = (len + kAttnChunk - 1) / kAttnChunk;
-    const float* hml = ws.ml + (size_t)h * nchunks * 2;
-    // M and L over the chunks: each wave a strided share, then across the four waves
+    // M and L over the live chunks: each thread its strided share, then the waves, then the four waves
     float M = -INFINITY;
-    for (int c = t; c < live; c += 256) M = fmaxf(M, hml[2 * c]);
+#pragma unroll
+    for (int k = 0; k < kMlPer; ++k)
+        if (t + 256 * k < live) M = fmaxf(M, mlv[k].x);
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
     if (lane == 0) part[0][wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
     float L = 0.f;
-    for (int c = t; c < live; c += 256) {
-        const float e = __expf(hml[2 * c] - M);
-        wts[c] = e;
-        L += hml[2 * c + 1] * e;
+#pragma unroll
+    for (int k = 0; k < kMlPer; ++k) {
+        const int c = t + 256 * k;
+        if (c < live) {
+            const float e = __expf(mlv[k].x - M);
+            wts[c] = e;
+            L += mlv[k].y * e;
+        }
     }
     for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
     if (lane == 0) part[1][wave] = L;
     __syncthreads();
     const float inv = 1.0f / ((part[1][0] + part[1][1]) + (part[1][2] + part[1][3]));
-    const int col = t % COLS4, cl = t / COLS4;
-    const float* po = ws.o + (size_t)h * nchunks * HD + col * 4;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-    for (int c = cl; c < live; c += CLN) {
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        const int c = cl + k * CLN;
+        if (c < live) {
+            const float w = wts[c];
+            acc.x = fmaf(w, pre[k].x, acc.x);
+            acc.y = fmaf(w, pre[k].y, acc.y);
+            acc.z = fmaf(w, pre[k].z, acc.z);
+            acc.w = fmaf(w, pre[k].w, acc.w);
+        }
+    }
+    for (int c = cl + kPre * CLN; c < live; c += CLN) {
         const float4 v = *reinterpret_cast<const float4*>(po + (size_t)c * HD);
         const float w = wts[c];
         acc.x = fmaf(w, v.x, acc.x);
@@ -319,6 +418,17 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
         }
         o4.x *= inv, o4.y *= inv, o4.z *= inv, o4.w *= inv;
         *reinterpret_cast<float4*>(out + (size_t)h * HD + t * 4) = o4;
+    }
+}
+
+// table[p][i] = (cos, sin) of p * base^(-2i/head_dim), the angle and its cosine
+// and sine in f64 (as rope_kv_kernel takes them), rounded to fp32.
+__global__ void __launch_bounds__(256) rope_table_kernel(float2* table, int half, int head_dim, double base, int rows) {
+    const double lb = log(base);
+    for (int u = blockIdx.x * 256 + threadIdx.x; u < rows * half; u += gridDim.x * 256) {
+        const int p = u / half, i = u % half;
+        const double angle = (double)p * exp(-((double)(2 * i) / (double)head_dim) * lb);
+        table[u] = make_float2((float)cos(angle), (float)sin(angle));
     }
 }
 
@@ -399,12 +509,28 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_final_kernel(const floa
     if (t == 0) *out = idx == 0x7fffffff ? 0 : idx;
 }
 
-// out = table[token mod rows] (the next token's embedding row).
+// out = table[token mod rows] (the next token's embedding row). With `parts`
+// (one workgroup) also parts[0] = sum out^2 (threads' strided shares, then a
+// fixed tree), the partial sum a fused rmsnorm prologue reads.
 __global__ void __launch_bounds__(256) embed_row_kernel(const float* table, int rows, int n, const int* token,
-                                                        float* out) {
+                                                        float* out, float* parts) {
+    __shared__ float red[256];
     const int r = ((*token % rows) + rows) % rows;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        out[i] = table[(size_t)r * n + i];
+    float ss = 0.f;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float v = table[(size_t)r * n + i];
+        out[i] = v;
+        ss = fmaf(v, v, ss);
+    }
+    if (!parts) return;
+    const int t = threadIdx.x;
+    red[t] = ss;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (t < s) red[t] += red[t + s];
+        __syncthreads();
+    }
+    if (t == 0) parts[0] = red[0];
 }
 
 // Advances the decode position by one (the last launch of a captured step).
@@ -433,45 +559,101 @@ size_t attention_workspace_bytes(int nq, int hd, int max_ctx) {
     return (nq * nchunks * 2 + nq * nchunks * (size_t)hd) * sizeof(float);
 }
 
-template <int HD, int MAXG>
-static void launch_attention_t(const float* q, const __half* kc, const __half* vc, const int* pos, int nkv, int group,
-                               int max_ctx, AttnWork ws, int nchunks, float* out, hipStream_t stream) {
+struct AttnLaunch {
+    const float* q;
+    const float* kv_new;
+    __half* kc;
+    __half* vc;
+    const float2* rope;
+    const int* pos;
+    int nkv, group, max_ctx, nchunks;
+    AttnWork ws;
+    float* out;
+};
+
+template <int HD, int MAXG, bool ROPE>
+static void launch_attention_t(const AttnLaunch& a, hipStream_t stream) {
     const float scale = 1.0f / sqrtf((float)HD);
-    hipLaunchKernelGGL((attention_kernel<HD, MAXG>), dim3(nkv, nchunks), dim3(kAttnThreads), 0, stream, q, kc, vc, pos,
-                       nkv, group, max_ctx, scale, ws, nchunks);
-    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(nkv * group), dim3(256), 0, stream, ws, pos, max_ctx, nchunks,
-                       out);
+    hipLaunchKernelGGL((attention_kernel<HD, MAXG, ROPE>), dim3(a.nkv, a.nchunks), dim3(kAttnThreads), 0, stream, a.q,
+                       a.kv_new, a.kc, a.vc, a.rope, a.pos, a.nkv, a.group, a.max_ctx, scale, a.ws, a.nchunks);
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.nkv * a.group), dim3(256), 0, stream, a.ws, a.pos, a.max_ctx,
+                       a.nchunks, a.out);
 }
 
-template <int HD>
-static void launch_attention_hd(const float* q, const __half* kc, const __half* vc, const int* pos, int nkv, int group,
-                                int max_ctx, AttnWork ws, int nchunks, float* out, hipStream_t stream) {
-    if (group <= 1)
-        launch_attention_t<HD, 1>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
-    else if (group <= 2)
-        launch_attention_t<HD, 2>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
-    else if (group <= 4)
-        launch_attention_t<HD, 4>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+template <int HD, bool ROPE>
+static void launch_attention_hd(const AttnLaunch& a, hipStream_t stream) {
+    if (a.group <= 1)
+        launch_attention_t<HD, 1, ROPE>(a, stream);
+    else if (a.group <= 2)
+        launch_attention_t<HD, 2, ROPE>(a, stream);
+    else if (a.group <= 4)
+        launch_attention_t<HD, 4, ROPE>(a, stream);
     else
-        launch_attention_t<HD, 8>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+        launch_attention_t<HD, 8, ROPE>(a, stream);
+}
+
+template <bool ROPE>
+static hipError_t launch_attention_any(int hd, const AttnLaunch& a, hipStream_t stream) {
+    // every chunk of the allocation is launched (the grid stays fixed while the
+    // position advances under a captured graph); chunks past the position leave at once
+    if (hd == 64)
+        launch_attention_hd<64, ROPE>(a, stream);
+    else if (hd == 128)
+        launch_attention_hd<128, ROPE>(a, stream);
+    else
+        launch_attention_hd<256, ROPE>(a, stream);
+    return hipGetLastError();
+}
+
+static bool attention_shape_ok(int nq, int nkv, int hd, int max_ctx) {
+    return nkv >= 1 && nq % nkv == 0 && nq / nkv <= kAttnMaxGroup && (hd == 64 || hd == 128 || hd == 256) &&
+           max_ctx <= kAttnMaxChunks * kAttnChunk;
 }
 
 hipError_t launch_attention(const float* q, const __half* kc, const __half* vc, const int* pos, int nq, int nkv,
                             int hd, int max_ctx, void* workspace, float* out, hipStream_t stream) {
-    if (nkv < 1 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || (hd != 64 && hd != 128 && hd != 256) ||
-        max_ctx > kAttnMaxChunks * kAttnChunk)
-        return hipErrorInvalidValue;
-    const int nchunks = (max_ctx + kAttnChunk - 1) / kAttnChunk;
-    const int group = nq / nkv;
-    const AttnWork ws = attn_work(workspace, nq, hd, nchunks);
-    // every chunk of the allocation is launched (the grid stays fixed while the
-    // position advances under a captured graph); chunks past the position leave at once
-    if (hd == 64)
-        launch_attention_hd<64>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
-    else if (hd == 128)
-        launch_attention_hd<128>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
-    else
-        launch_attention_hd<256>(q, kc, vc, pos, nkv, group, max_ctx, ws, nchunks, out, stream);
+    if (!attention_shape_ok(nq, nkv, hd, max_ctx)) return hipErrorInvalidValue;
+    AttnLaunch a;
+    a.q = q;
+    a.kv_new = nullptr;
+    a.kc = const_cast<__half*>(kc);  // read only without ROPE
+    a.vc = const_cast<__half*>(vc);
+    a.rope = nullptr;
+    a.pos = pos;
+    a.nkv = nkv;
+    a.group = nq / nkv;
+    a.max_ctx = max_ctx;
+    a.nchunks = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    a.ws = attn_work(workspace, nq, hd, a.nchunks);
+    a.out = out;
+    return launch_attention_any<false>(hd, a, stream);
+}
+
+hipError_t launch_attention_rope(const float* qkv, const float2* rope_table, __half* kc, __half* vc, const int* pos,
+                                 int nq, int nkv, int hd, int max_ctx, void* workspace, float* out,
+                                 hipStream_t stream) {
+    if (!attention_shape_ok(nq, nkv, hd, max_ctx)) return hipErrorInvalidValue;
+    AttnLaunch a;
+    a.q = qkv;
+    a.kv_new = qkv + (size_t)nq * hd;
+    a.kc = kc;
+    a.vc = vc;
+    a.rope = rope_table;
+    a.pos = pos;
+    a.nkv = nkv;
+    a.group = nq / nkv;
+    a.max_ctx = max_ctx;
+    a.nchunks = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    a.ws = attn_work(workspace, nq, hd, a.nchunks);
+    a.out = out;
+    return launch_attention_any<true>(hd, a, stream);
+}
+
+hipError_t launch_rope_table(float2* table, int head_dim, double base, int rows, hipStream_t stream) {
+    const int half = head_dim / 2;
+    int grid = (rows * half + 255) / 256;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(rope_table_kernel, dim3(grid), dim3(256), 0, stream, table, half, head_dim, base, rows);
     return hipGetLastError();
 }
 
@@ -493,10 +675,12 @@ hipError_t launch_argmax(const float* v, int n, int* out, void* workspace, hipSt
     return hipGetLastError();
 }
 
-hipError_t launch_embed_row(const float* table, int rows, int n, const int* token, float* out, hipStream_t stream) {
+hipError_t launch_embed_row(const float* table, int rows, int n, const int* token, float* out, float* parts,
+                            hipStream_t stream) {
     int grid = (n + 255) / 256;
     if (grid > 256) grid = 256;
-    hipLaunchKernelGGL(embed_row_kernel, dim3(grid), dim3(256), 0, stream, table, rows, n, token, out);
+    if (parts) grid = 1;
+    hipLaunchKernelGGL(embed_row_kernel, dim3(grid), dim3(256), 0, stream, table, rows, n, token, out, parts);
     return hipGetLastError();
 }
 

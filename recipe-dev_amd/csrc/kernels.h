@@ -20,12 +20,29 @@ struct MvParams {
     float* y;
     int64_t ldy;
     int G;  // lanes that share one row (power of two, 8..64)
+    int block = 256;  // threads per workgroup (the launch's block size)
     // F16 weights only: rows at or past `split` come from P2 (row - split), so
     // that two weights of one width run as one launch (an MoE router and its
     // shared-expert gate). split >= rows: P alone.
     Planes P2;
     int64_t split;
+    // Decode-step fusions (quantized weights, one fp32 activation row):
+    // prologue: when norm_w is set, x is replaced by x * norm_w / sqrt(ss / K + eps)
+    // with ss the in-order sum of norm_nparts partial sums of squares of x;
+    // epilogue (epi): kEpiPlain writes y; kEpiGlu takes rows as (gate, up)
+    // pairs and writes y[i] = silu(row 2i) * row 2i+1; kEpiResidual adds each
+    // row into resid (resid[r] += row r) and writes one partial sum of squares
+    // of the updated resid rows per workgroup to parts_out[blockIdx.x].
+    int epi = 0;
+    float* resid = nullptr;
+    float* parts_out = nullptr;
+    const float* norm_w = nullptr;
+    const float* norm_parts = nullptr;
+    int norm_nparts = 0;
+    float eps = 0.f;
 };
+
+enum Epilogue : int { kEpiPlain = 0, kEpiGlu = 1, kEpiResidual = 2 };
 
 struct LaunchShape {
     int G = 64;       // lanes per row group
@@ -46,6 +63,12 @@ hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const Lau
 hipError_t launch_dequant(int fmt, const Planes& P, int64_t rows, int cols, float* out, hipStream_t stream);
 
 size_t matvec_lds_bytes(int fmt, int xtype, int M, int cols);
+
+// The decode-step fused product (M = 1, fp32 activations, quantized weight):
+// the launch shape it uses (its grid is the number of partial sums a
+// kEpiResidual launch writes) and the launch itself.
+LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus);
+hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream);
 
 // Matrix-core product for 1 <= M <= 32 activation rows (quantized formats).
 hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, int cus, hipStream_t stream,

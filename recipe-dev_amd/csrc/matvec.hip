@@ -47,7 +47,7 @@ struct StepWalk {
 
 __device__ __forceinline__ StepWalk make_walk(const MvParams& p, int R, int g) {
     StepWalk w;
-    const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
+    const int wpb = p.block >> 6, wave = threadIdx.x >> 6;
     w.rows_per_wave = (int64_t)(64 / p.G) * R;
     w.tiles = (p.rows + w.rows_per_wave - 1) / w.rows_per_wave;
     w.tile = (int64_t)blockIdx.x * wpb + wave;
@@ -82,18 +82,44 @@ __device__ __forceinline__ void load_rows(const MvParams& p, const StepWalk& w, 
     }
 }
 
-template <int M, int R>
-__device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int g, float (&acc)[R][M]) {
+// The tile's cross-lane sums and its epilogue (MvParams::epi; the fused
+// epilogues run with M = 1 and, for kEpiGlu, an even R, so that a lane group
+// holds each (gate, up) row pair). `ss` gathers the lane's share of the
+// residual sum of squares.
+template <int M, int R, bool NORM = false>
+__device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int g, float (&acc)[R][M], float& ss,
+                                            float norm_scale = 1.f) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int mm = 0; mm < M; ++mm) acc[r][mm] = group_sum(acc[r][mm], p.G);
+        for (int mm = 0; mm < M; ++mm) {
+            acc[r][mm] = group_sum(acc[r][mm], p.G);
+            if constexpr (NORM) acc[r][mm] *= norm_scale;
+        }
     if (g == p.G - 1) {
+        if (p.epi == kEpiPlain) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (row0 + r < p.rows)
+            for (int r = 0; r < R; ++r)
+                if (row0 + r < p.rows)
 #pragma unroll
-                for (int mm = 0; mm < M; ++mm) p.y[(int64_t)mm * p.ldy + row0 + r] = acc[r][mm];
+                    for (int mm = 0; mm < M; ++mm) p.y[(int64_t)mm * p.ldy + row0 + r] = acc[r][mm];
+        } else if (p.epi == kEpiGlu) {
+            // silu(gate) * up, silu(v) = v * sigmoid(v), sigmoid = 0.5 (tanh(v / 2) + 1) (recipe.rs:22662-22668)
+#pragma unroll
+            for (int r = 0; r + 1 < R; r += 2)
+                if (row0 + r + 1 < p.rows) {
+                    const float gt = acc[r][0];
+                    p.y[(row0 + r) / 2] = gt * (0.5f * (tanhf(0.5f * gt) + 1.0f)) * acc[r + 1][0];
+                }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row0 + r < p.rows) {
+                    const float v = p.resid[row0 + r] + acc[r][0];
+                    p.resid[row0 + r] = v;
+                    ss = fmaf(v, v, ss);
+                }
+        }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -115,9 +141,10 @@ __device__ __forceinline__ void load_rows_rs(const MvParams& p, __amdgpu_buffer_
 
 // One step of matvec_int: the lane's chunk of its R rows against the staged
 // digits of every activation row; the tile's reduction after its last step.
-template <int FMT, int M, int R>
+template <int FMT, int M, int R, bool NORM = false>
 __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, int sub, int g, const ChunkData<FMT> (&d)[R],
-                                         float (&acc)[R][M], const uint4* xd, const uint4* xb) {
+                                         float (&acc)[R][M], const uint4* xd, const uint4* xb, float& ss,
+                                         float norm_scale = 1.f) {
     constexpr int XP = Traits<FMT>::XP;
     const int nch = p.P.nch;
     const int c = w.chunk();
@@ -137,18 +164,47 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
                 if (row0 + r < p.rows) dot_int<FMT, 1>(d[r], c, xv, bv, &acc[r][mm]);
         }
     }
-    if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
+    if (w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, ss, norm_scale);
+}
+
+// rmsnorm prologue. The staged activations are x * norm_w (per column); the
+// common factor 1 / sqrt(ss / K + eps) multiplies the finished products, so
+// the partial sums of squares (ss = their in-order sum: lane l adds parts
+// l, l + 64, ..., then a fixed DPP tree) are only needed at the first tile's
+// end, and every wave forms the factor itself (no barrier on the way in).
+constexpr int kNormPartsPerLane = 16;  // up to 1024 partial sums
+
+__device__ __forceinline__ void issue_norm_parts(const MvParams& p, float (&v)[kNormPartsPerLane]) {
+    // straight-line loads from clamped indices; the duplicates are dropped in norm_scale_of
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < kNormPartsPerLane; ++j) {
+        const int i = lane + 64 * j;
+        v[j] = p.norm_parts[i < p.norm_nparts ? i : p.norm_nparts - 1];
+    }
+}
+
+__device__ __forceinline__ float norm_scale_of(const MvParams& p, const float (&v)[kNormPartsPerLane]) {
+    const int lane = threadIdx.x & 63;
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormPartsPerLane; ++j) a += lane + 64 * j < p.norm_nparts ? v[j] : 0.f;
+    a = group_sum(a, 64);
+    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
+    return 1.0f / sqrtf(a / (float)p.K + p.eps);
 }
 
 // Quantized weights, integer dot of staged activation digits (chunk.h,
 // stage.h). Two register buffers alternate: while one step is computed, the
 // loads of the next are in flight, and the buffer just computed is refilled
 // for the step after that. The first two steps' weight loads are issued
-// before the activations are staged.
-template <int FMT, int M, int R, bool XF32>
+// before the activations are staged. NORM: the rmsnorm prologue (M = 1,
+// fp32 activations).
+template <int FMT, int M, int R, bool XF32, bool NORM = false>
 __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     constexpr int XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
+    __shared__ float block_scalar[8];  // the waves' residual sums of squares
     const int nch = p.P.nch;
     uint4* xd = smem;
     uint4* xb = smem + M * XP * nch;
@@ -159,38 +215,54 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     wb.next();
 
     ChunkData<FMT> A[R], B[R];
-    if (stage_items<FMT>(nch, M) <= kStageNJ * (int)blockDim.x) {
-        StageItem<XF32> it[kStageNJ];
-        stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, M, it);
+    float parts[kNormPartsPerLane];
+    if constexpr (NORM) issue_norm_parts(p, parts);
+    if (stage_items<FMT>(nch, M) <= kStageNJ * p.block) {
+        StageItem<XF32, NORM> it[kStageNJ];
+        stage_multi_issue<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, it, p.norm_w);
         // keep the activation loads ahead of the weight loads: waiting for them
         // then leaves the weight loads in flight
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
         load_rows_rs<FMT, R>(p, rs, wa, sub, A);
         load_rows_rs<FMT, R>(p, rs, wb, sub, B);
-        stage_multi_finish<FMT, XF32>(nch, p.K, M, it, xd, reinterpret_cast<float*>(xb));
+        stage_multi_finish<FMT, XF32, NORM>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb));
     } else {
         load_rows_rs<FMT, R>(p, rs, wa, sub, A);
         load_rows_rs<FMT, R>(p, rs, wb, sub, B);
-        stage_all<FMT, XF32>(nch, p.K, p.x, p.ldx, M, xd, reinterpret_cast<float*>(xb));
+        stage_all<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, xd, reinterpret_cast<float*>(xb), p.norm_w);
     }
     __syncthreads();
+    float norm_scale = 1.f;
+    if constexpr (NORM) norm_scale = norm_scale_of(p, parts);
 
     float acc[R][M];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
+    float ss = 0.f;
     while (wa.valid()) {
-        step_int<FMT, M, R>(p, wa, sub, g, A, acc, xd, xb);
+        step_int<FMT, M, R, NORM>(p, wa, sub, g, A, acc, xd, xb, ss, norm_scale);
         wa = wb;
         wa.next();
         load_rows_rs<FMT, R>(p, rs, wa, sub, A);
         if (!wb.valid()) break;
-        step_int<FMT, M, R>(p, wb, sub, g, B, acc, xd, xb);
+        step_int<FMT, M, R, NORM>(p, wb, sub, g, B, acc, xd, xb, ss, norm_scale);
         wb = wa;
         wb.next();
         load_rows_rs<FMT, R>(p, rs, wb, sub, B);
+    }
+    if (p.epi == kEpiResidual) {  // the workgroup's partial sum of squares, waves in order
+        ss = group_sum(ss, 64);
+        __syncthreads();
+        if (lane == 63) block_scalar[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.f;
+            for (int w = 0; w < (p.block >> 6); ++w) t += block_scalar[w];
+            p.parts_out[blockIdx.x] = t;
+        }
     }
 }
 
@@ -205,9 +277,9 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
     ChunkData<F16> cur[R];
     load_rows<F16, R>(p, w, sub, cur);
     if constexpr (XF32)
-        stage_f32_quads(nch, p.K, p.x, p.ldx, M, reinterpret_cast<float4*>(smem));
+        stage_f32_quads(nch, p.K, p.x, p.ldx, M, p.block, reinterpret_cast<float4*>(smem));
     else
-        stage_f16_pairs(nch, p.K, p.x, p.ldx, M, smem);
+        stage_f16_pairs(nch, p.K, p.x, p.ldx, M, p.block, smem);
     __syncthreads();
 
     float acc[R][M];
@@ -216,6 +288,7 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
     bool loaded = true;
+    float unused_ss = 0.f;  // F16 weights take the plain epilogue only
     while (w.valid()) {
         if (!loaded) load_rows<F16, R>(p, w, sub, cur);
         loaded = false;
@@ -240,7 +313,7 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
                     if (row0 + r < p.rows) dot_f16w<M>(cur[r], xv, acc[r]);
             }
         }
-        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
+        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc, unused_ss);
         w.next();
     }
 }
@@ -304,8 +377,10 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
 }
 
 template <typename K>
-static hipError_t launch_kernel(K kernel, const MvParams& p, const LaunchShape& s, size_t lds, hipStream_t stream,
+static hipError_t launch_kernel(K kernel, const MvParams& p_in, const LaunchShape& s, size_t lds, hipStream_t stream,
                                 hipEvent_t ev0, hipEvent_t ev1) {
+    MvParams p = p_in;
+    p.block = s.block;
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);
@@ -354,6 +429,36 @@ hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const Lau
         case Q4_K: return launch_fmt<Q4_K>(xtype, M, p, s, stream, ev0, ev1);
         case Q6_K: return launch_fmt<Q6_K>(xtype, M, p, s, stream, ev0, ev1);
         case F16: return launch_fmt<F16>(xtype, M, p, s, stream, ev0, ev1);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus) {
+    LaunchShape s = plan_matvec(fmt, rows, cols, 1, X_F32, cus);
+    s.R = 2;  // a lane group holds a (gate, up) row pair for kEpiGlu
+    const int64_t rows_per_wave = (int64_t)(64 / s.G) * s.R;
+    const int64_t tiles = (rows + rows_per_wave - 1) / rows_per_wave;
+    const int wpb = s.block / 64;
+    int64_t grid = (tiles + wpb - 1) / wpb;
+    if (grid > s.grid) grid = s.grid;
+    s.grid = grid < 1 ? 1 : (int)grid;
+    return s;
+}
+
+template <int FMT>
+static hipError_t launch_fused_fmt(const MvParams& p, const LaunchShape& s, hipStream_t stream) {
+    const size_t lds = matvec_lds_bytes(FMT, X_F32, 1, p.K);
+    if (p.norm_w) return launch_kernel(matvec_int<FMT, 1, 2, true, true>, p, s, lds, stream, nullptr, nullptr);
+    return launch_kernel(matvec_int<FMT, 1, 2, true>, p, s, lds, stream, nullptr, nullptr);
+}
+
+hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream) {
+    if (s.R != 2 || s.block > 512 || (p.norm_w && p.norm_nparts > kNormPartsPerLane * 64)) return hipErrorInvalidValue;
+    switch (fmt) {
+        case Q4_0: return launch_fused_fmt<Q4_0>(p, s, stream);
+        case Q8_0: return launch_fused_fmt<Q8_0>(p, s, stream);
+        case Q4_K: return launch_fused_fmt<Q4_K>(p, s, stream);
+        case Q6_K: return launch_fused_fmt<Q6_K>(p, s, stream);
         default: return hipErrorInvalidValue;
     }
 }

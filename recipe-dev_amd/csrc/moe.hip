@@ -22,6 +22,8 @@
 
 namespace rq {
 
+constexpr int kMoeThreads = 256;  // workgroup size of the MoE kernels (four waves)
+
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
 
 size_t moe_workspace_bytes(const MoeDims& d) {
@@ -186,7 +188,7 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
 }
 
 template <int FMT, bool XF32, int S>
-__global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
+__global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
                                                        MoeBank up_sh, const void* x, MoeWorkspace ws, float* route_dense,
                                                        int G) {
     constexpr int XP = Traits<FMT>::XP;
@@ -196,7 +198,7 @@ __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, M
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
-    const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
+    const int wpb = kMoeThreads >> 6, wave = threadIdx.x >> 6;
     const int routed = d.top * d.hidden;
     const int total_rows = routed + d.hidden_shared;
     const int rows_per_wave = 64 / G;
@@ -224,7 +226,7 @@ __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, M
     // the first chunk's weights are requested before the activations are staged
     ChunkData<FMT> dg, du;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, dg, du);
-    stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, xd, reinterpret_cast<float*>(xb));
+    stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb));
     __syncthreads();
     bool fetched = true;
     for (; tile < tiles; tile += gridDim.x * wpb) {
@@ -250,7 +252,7 @@ __global__ void __launch_bounds__(256) moe_glu_kernel(MoeDims d, MoeBank gate, M
 }
 
 template <int FMT>
-__global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
+__global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
                                                         float* y, int G) {
     constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
@@ -261,7 +263,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, 
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
-    const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6;
+    const int wpb = kMoeThreads >> 6, wave = threadIdx.x >> 6;
     const int rows_per_wave = 64 / G;
     const int tiles = (d.d_model + rows_per_wave - 1) / rows_per_wave;
     // Chunk c of output row n: chunk lc of slot s's expert down row, or of the shared expert's.
@@ -285,7 +287,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDims d, MoeBank down, 
     float w;
     int lc;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd, w, lc);
-    stage_all<FMT, true>(nch, K, ws.h, 0, 1, xd, reinterpret_cast<float*>(xb));
+    stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb));
     __syncthreads();
     bool fetched = true;
     for (; tile < tiles; tile += gridDim.x * wpb) {
@@ -333,7 +335,8 @@ static hipError_t glu_launch(const MoeDims& d, const MoeBank& gate, const MoeBan
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, stream, d, gate, up, gate_sh, up_sh, x, ws, route_dense, G);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMoeThreads), lds, stream, d, gate, up, gate_sh, up_sh, x, ws,
+                       route_dense, G);
     return hipGetLastError();
 }
 
@@ -388,7 +391,7 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(moe_down_kernel<FMT>, dim3(grid), dim3(256), lds, stream, d, down, down_sh, ws, y, G);
+    hipLaunchKernelGGL(moe_down_kernel<FMT>, dim3(grid), dim3(kMoeThreads), lds, stream, d, down, down_sh, ws, y, G);
     return hipGetLastError();
 }
 

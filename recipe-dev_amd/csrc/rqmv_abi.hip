@@ -2,6 +2,7 @@
 #include <stdlib.h>
 
 #include <mutex>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -21,6 +22,7 @@ struct rqmv_weight {
     uint8_t* dev;
     size_t dev_bytes;
     int device;
+    bool glu = false;  // rows are (gate, up) pairs (rqmv_glu_weight_create)
 };
 
 namespace {
@@ -220,6 +222,27 @@ int rqmv_expert_bank_create(int format, int64_t experts, int64_t rows, int64_t c
     return create(format, experts, rows, cols, gguf_bytes, nbytes, out);
 }
 
+int rqmv_glu_weight_create(int format, int64_t rows, int64_t cols, const void* gate_gguf, const void* up_gguf,
+                           size_t nbytes_each, rqmv_weight** out) {
+    if (!gate_gguf || !up_gguf || !out) return fail(RQMV_EINVAL, "NULL argument");
+    if (format == rq::F16 || format == rq::F32) return fail(RQMV_EINVAL, "a GLU pair must be quantized");
+    const int64_t want = rq::gguf_bytes(format, rows, cols);
+    if (rows <= 0 || want < 0 || (size_t)want != nbytes_each)
+        return fail(RQMV_EINVAL, "gate and up must each hold rows x cols GGUF blocks");
+    // rows interleaved: row 2i = gate row i, row 2i + 1 = up row i
+    const size_t rb = (size_t)want / (size_t)rows;
+    std::vector<uint8_t> pairs(2 * (size_t)want);
+    const uint8_t* g = static_cast<const uint8_t*>(gate_gguf);
+    const uint8_t* u = static_cast<const uint8_t*>(up_gguf);
+    for (int64_t i = 0; i < rows; ++i) {
+        std::memcpy(pairs.data() + (2 * i) * rb, g + i * rb, rb);
+        std::memcpy(pairs.data() + (2 * i + 1) * rb, u + i * rb, rb);
+    }
+    int rc = create(format, 1, 2 * rows, cols, pairs.data(), pairs.size(), out);
+    if (rc == RQMV_OK) (*out)->glu = true;
+    return rc;
+}
+
 int rqmv_weight_destroy(rqmv_weight* w) {
     if (!w) return RQMV_OK;
     hipError_t e = hipFree(w->dev);
@@ -280,6 +303,65 @@ int rqmv_matvec_timed(const rqmv_weight* w, const void* x_dev, int x_dtype, int 
     return matvec_rows(w, 0, w->rows * w->experts, x_dev, x_dtype, m, ldx, y_dev, ldy,
                        static_cast<hipStream_t>(stream), info, static_cast<hipEvent_t>(start_event),
                        static_cast<hipEvent_t>(stop_event));
+}
+
+int rqmv_residual_parts(const rqmv_weight* w, int* nparts) {
+    DeviceInfo info;
+    int rc = check_launch(w, &info);
+    if (rc != RQMV_OK) return rc;
+    if (!nparts) return fail(RQMV_EINVAL, "nparts is NULL");
+    *nparts = rq::plan_fused(w->fmt, w->rows * w->experts, w->cols, info.cus).grid;
+    return RQMV_OK;
+}
+
+int rqmv_matvec_fused(const rqmv_weight* w, const float* x_dev, float* y_dev, const rqmv_fusion* f, void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(w, &info);
+    if (rc != RQMV_OK) return rc;
+    if (!f || !x_dev) return fail(RQMV_EINVAL, "fused: NULL argument");
+    if (w->fmt == rq::F16 || w->experts != 1) return fail(RQMV_EINVAL, "fused: a plain quantized weight is required");
+    if (reinterpret_cast<uintptr_t>(x_dev) % 16 != 0) return fail(RQMV_EINVAL, "fused: x must be 16-byte aligned");
+    rq::MvParams p;
+    p.P = planes_of(w, 0);
+    p.P2 = p.P;
+    p.rows = w->rows;
+    p.split = p.rows;
+    p.K = (int)w->cols;
+    p.x = x_dev;
+    p.ldx = w->cols;
+    p.y = y_dev;
+    p.ldy = w->rows;
+    if (rq::matvec_lds_bytes(w->fmt, RQMV_DTYPE_F32, 1, (int)w->cols) > info.lds_limit)
+        return fail(RQMV_EINVAL, "fused: cols too large for one LDS stage");
+    const rq::LaunchShape s = rq::plan_fused(w->fmt, w->rows, w->cols, info.cus);
+    p.G = s.G;
+    switch (f->epilogue) {
+        case RQMV_EPI_PLAIN:
+            if (!y_dev) return fail(RQMV_EINVAL, "fused: y is NULL");
+            break;
+        case RQMV_EPI_GLU:
+            if (!w->glu || !y_dev) return fail(RQMV_EINVAL, "fused: the GLU epilogue needs a GLU weight and y");
+            p.epi = rq::kEpiGlu;
+            break;
+        case RQMV_EPI_RESIDUAL:
+            if (!f->residual || !f->parts_out) return fail(RQMV_EINVAL, "fused: residual and parts_out are required");
+            p.epi = rq::kEpiResidual;
+            p.resid = f->residual;
+            p.parts_out = f->parts_out;
+            break;
+        default: return fail(RQMV_EINVAL, "fused: unknown epilogue");
+    }
+    if (f->norm_weight) {
+        if (!f->norm_parts || f->norm_nparts < 1 || f->norm_nparts > 1024 || !(f->eps >= 0.f) ||
+            reinterpret_cast<uintptr_t>(f->norm_weight) % 16 != 0)
+            return fail(RQMV_EINVAL, "fused: the norm needs 1..1024 partial sums, eps >= 0 and 16-byte aligned scales");
+        p.norm_w = f->norm_weight;
+        p.norm_parts = f->norm_parts;
+        p.norm_nparts = f->norm_nparts;
+        p.eps = f->eps;
+    }
+    hipError_t e = rq::launch_matvec_fused(w->fmt, p, s, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "fused matvec launch");
 }
 
 int rqmv_expert_matvec(const rqmv_weight* bank, int64_t expert, const void* x_dev, int x_dtype, int m, int64_t ldx,
@@ -447,6 +529,36 @@ int rqmv_attention(const float* q, const void* k_cache, const void* v_cache, con
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "attention launch");
 }
 
+int rqmv_rope_table(float* table, int head_dim, double base, int rows, void* stream) {
+    if (!table || head_dim <= 0 || head_dim % 2 || rows <= 0 || !(base > 1.0))
+        return fail(RQMV_EINVAL, "rope_table: bad arguments");
+    hipError_t e = rq::launch_rope_table(reinterpret_cast<float2*>(table), head_dim, base, rows,
+                                         static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "rope_table launch");
+}
+
+int rqmv_attention_rope(const float* qkv, const float* rope_table, void* k_cache, void* v_cache, const int* pos,
+                        int q_heads, int kv_heads, int head_dim, int max_ctx, void* workspace, size_t workspace_bytes,
+                        float* out, void* stream) {
+    if (!qkv || !rope_table || !k_cache || !v_cache || !pos || !workspace || !out || q_heads <= 0 || kv_heads <= 0 ||
+        max_ctx <= 0)
+        return fail(RQMV_EINVAL, "attention_rope: bad arguments");
+    if (q_heads % kv_heads || q_heads / kv_heads > 8 || (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+        max_ctx > 65536)
+        return fail(RQMV_EINVAL,
+                    "attention_rope: q_heads must be 1..8 x kv_heads, head_dim 64, 128 or 256, max_ctx at most 65536");
+    if (((uintptr_t)qkv | (uintptr_t)rope_table | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out |
+         (uintptr_t)workspace) & 15)
+        return fail(RQMV_EINVAL, "attention_rope: pointers must be 16-byte aligned");
+    if (workspace_bytes < rq::attention_workspace_bytes(q_heads, head_dim, max_ctx))
+        return fail(RQMV_EINVAL, "attention_rope: workspace too small");
+    hipError_t e = rq::launch_attention_rope(qkv, reinterpret_cast<const float2*>(rope_table),
+                                             static_cast<__half*>(k_cache), static_cast<__half*>(v_cache), pos, q_heads,
+                                             kv_heads, head_dim, max_ctx, workspace, out,
+                                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "attention_rope launch");
+}
+
 int rqmv_silu_mul(const float* gate_up, int n, float* out, void* stream) {
     if (!gate_up || !out || n <= 0) return fail(RQMV_EINVAL, "silu_mul: bad arguments");
     hipError_t e = rq::launch_silu_mul(gate_up, n, out, static_cast<hipStream_t>(stream));
@@ -466,9 +578,10 @@ int rqmv_argmax(const float* values, int n, int* out, void* workspace, size_t wo
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "argmax launch");
 }
 
-int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, void* stream) {
+int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, float* parts_out,
+                   void* stream) {
     if (!table || !token || !out || rows <= 0 || n <= 0) return fail(RQMV_EINVAL, "embed_row: bad arguments");
-    hipError_t e = rq::launch_embed_row(table, rows, n, token, out, static_cast<hipStream_t>(stream));
+    hipError_t e = rq::launch_embed_row(table, rows, n, token, out, parts_out, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "embed_row launch");
 }
 

@@ -32,13 +32,15 @@ __device__ __forceinline__ int stage_items(int nch, int M) {
     return M * nch * Traits<FMT>::BLK * 4;
 }
 
-template <bool XF32>
+template <bool XF32, bool NORM = false>
 struct StageItem {
     uint4 raw[XF32 ? 2 : 1];
+    uint4 nw[NORM ? 2 : 1];  // the item's eight norm scales (NORM only)
 };
 
-template <int FMT, bool XF32>
-__device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* xv, int64_t ldx, StageItem<XF32>& it) {
+template <int FMT, bool XF32, bool NORM = false>
+__device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* xv, int64_t ldx,
+                                            StageItem<XF32, NORM>& it, const float* norm_w = nullptr) {
     constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK;
     const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
     int k0 = c * CW + b * 32 + q * 8;
@@ -47,6 +49,10 @@ __device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* x
         const float* xm = static_cast<const float*>(xv) + (int64_t)m * ldx + k0;
         it.raw[0] = *reinterpret_cast<const uint4*>(xm);
         it.raw[1] = *reinterpret_cast<const uint4*>(xm + 4);
+        if constexpr (NORM) {
+            it.nw[0] = *reinterpret_cast<const uint4*>(norm_w + k0);
+            it.nw[1] = *reinterpret_cast<const uint4*>(norm_w + k0 + 4);
+        }
     } else {
         it.raw[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xv) + (int64_t)m * ldx + k0);
     }
@@ -81,8 +87,9 @@ __device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* ou
 
 // Encodes item u and stores it into LDS. Every lane of the item's quad must
 // run it together (the block maximum and sums move through DPP).
-template <int FMT, bool XF32>
-__device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageItem<XF32>& it, uint4* xd, float* xbf) {
+template <int FMT, bool XF32, bool NORM = false>
+__device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageItem<XF32, NORM>& it, uint4* xd,
+                                             float* xbf) {
     constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP;
     const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
     const bool live = c * CW + b * 32 < K;
@@ -92,6 +99,13 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
         for (int t = 0; t < 4; ++t) {
             v[t] = __builtin_bit_cast(float, word(it.raw[0], t));
             v[4 + t] = __builtin_bit_cast(float, word(it.raw[1], t));
+        }
+        if constexpr (NORM) {  // rmsnorm's per-column scale; its common factor is applied to the products
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[t] *= __builtin_bit_cast(float, word(it.nw[0], t));
+                v[4 + t] *= __builtin_bit_cast(float, word(it.nw[1], t));
+            }
         }
     } else {
 #pragma unroll
@@ -167,36 +181,41 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
 // (stage_multi_finish).
 constexpr int kStageNJ = 4;
 
-template <int FMT, bool XF32>
-__device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x, int64_t ldx, int M,
-                                                  StageItem<XF32> (&it)[kStageNJ]) {
+// `nthreads` is the workgroup's size, passed in rather than read from the
+// dispatch packet (blockDim), whose read is a memory round trip at the start
+// of every workgroup.
+template <int FMT, bool XF32, bool NORM = false>
+__device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x, int64_t ldx, int M, int nthreads,
+                                                  StageItem<XF32, NORM> (&it)[kStageNJ],
+                                                  const float* norm_w = nullptr) {
     const int total = stage_items<FMT>(nch, M);
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
-        const int u = (int)threadIdx.x + j * (int)blockDim.x;
-        stage_issue<FMT, XF32>(u < total ? u : (int)threadIdx.x % 4, nch, K, x, ldx, it[j]);
+        const int u = (int)threadIdx.x + j * nthreads;
+        stage_issue<FMT, XF32, NORM>(u < total ? u : (int)threadIdx.x % 4, nch, K, x, ldx, it[j], norm_w);
     }
 }
 
-template <int FMT, bool XF32>
-__device__ __forceinline__ void stage_multi_finish(int nch, int K, int M, const StageItem<XF32> (&it)[kStageNJ],
-                                                   uint4* xd, float* xbf) {
+template <int FMT, bool XF32, bool NORM = false>
+__device__ __forceinline__ void stage_multi_finish(int nch, int K, int M, int nthreads,
+                                                   const StageItem<XF32, NORM> (&it)[kStageNJ], uint4* xd, float* xbf) {
     const int total = stage_items<FMT>(nch, M);
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
-        const int u = (int)threadIdx.x + j * (int)blockDim.x;
-        if (u < total) stage_finish<FMT, XF32>(u, nch, K, it[j], xd, xbf);
+        const int u = (int)threadIdx.x + j * nthreads;
+        if (u < total) stage_finish<FMT, XF32, NORM>(u, nch, K, it[j], xd, xbf);
     }
 }
 
 // Plain loop (used when a block has more items than kStageNJ per thread).
-template <int FMT, bool XF32>
-__device__ __forceinline__ void stage_all(int nch, int K, const void* x, int64_t ldx, int M, uint4* xd, float* xbf) {
+template <int FMT, bool XF32, bool NORM = false>
+__device__ __forceinline__ void stage_all(int nch, int K, const void* x, int64_t ldx, int M, int nthreads, uint4* xd,
+                                          float* xbf, const float* norm_w = nullptr) {
     const int total = stage_items<FMT>(nch, M);
-    for (int u = threadIdx.x; u < total; u += blockDim.x) {
-        StageItem<XF32> it;
-        stage_issue<FMT, XF32>(u, nch, K, x, ldx, it);
-        stage_finish<FMT, XF32>(u, nch, K, it, xd, xbf);
+    for (int u = threadIdx.x; u < total; u += nthreads) {
+        StageItem<XF32, NORM> it;
+        stage_issue<FMT, XF32, NORM>(u, nch, K, x, ldx, it, norm_w);
+        stage_finish<FMT, XF32, NORM>(u, nch, K, it, xd, xbf);
     }
 }
 
@@ -207,20 +226,22 @@ __host__ __device__ inline size_t stage_bytes_int(int fmt, int M, int nch) {
 }
 
 // F16 weights: fp16 activations as natural pairs, or fp32 activations.
-__device__ __forceinline__ void stage_f16_pairs(int nch, int K, const void* xv, int64_t ldx, int M, uint4* xq) {
+__device__ __forceinline__ void stage_f16_pairs(int nch, int K, const void* xv, int64_t ldx, int M, int nthreads,
+                                                uint4* xq) {
     const uint16_t* x = static_cast<const uint16_t*>(xv);
     const int total = M * 8 * nch;
-    for (int u = threadIdx.x; u < total; u += blockDim.x) {
+    for (int u = threadIdx.x; u < total; u += nthreads) {
         const int c = u % nch, mj = u / nch, j = mj % 8, m = mj / 8;
         const int k0 = c * 64 + j * 8;
         xq[u] = k0 < K ? *reinterpret_cast<const uint4*>(x + (int64_t)m * ldx + k0) : make_uint4(0, 0, 0, 0);
     }
 }
 
-__device__ __forceinline__ void stage_f32_quads(int nch, int K, const void* xv, int64_t ldx, int M, float4* xf) {
+__device__ __forceinline__ void stage_f32_quads(int nch, int K, const void* xv, int64_t ldx, int M, int nthreads,
+                                                float4* xf) {
     const float* x = static_cast<const float*>(xv);
     const int total = M * 16 * nch;
-    for (int u = threadIdx.x; u < total; u += blockDim.x) {
+    for (int u = threadIdx.x; u < total; u += nthreads) {
         const int c = u % nch, mj = u / nch, j = mj % 16, m = mj / 16;
         const int k0 = c * 64 + j * 4;
         xf[u] = k0 < K ? *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k0) : make_float4(0.f, 0.f, 0.f, 0.f);

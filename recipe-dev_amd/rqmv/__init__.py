@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_void_p
 
 import numpy as np
 
@@ -66,7 +66,13 @@ class _Lib:
         L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_void_p]
         L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
-        L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
+        L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.rqmv_rope_table.argtypes = [c_void_p, c_int, c_double, c_int, c_void_p]
+        L.rqmv_attention_rope.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                          c_void_p, c_size_t, c_void_p, c_void_p]
+        L.rqmv_glu_weight_create.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]
+        L.rqmv_matvec_fused.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.rqmv_residual_parts.argtypes = [c_void_p, POINTER(c_int)]
         L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t)]
         L.rqmv_repack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
         L.rqmv_unpack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
@@ -261,6 +267,7 @@ class Weight:
         self.fmt, self.rows, self.cols = _fmt(fmt), rows, cols
         self.experts = 1 if experts is None else experts
         self.gguf_nbytes = gguf.nbytes
+        self.glu = False
 
     def info(self):
         f, r, c, e, b = c_int(), c_int64(), c_int64(), c_int64(), c_size_t()
@@ -444,6 +451,20 @@ def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, pos
                                     workspace.ptr, workspace.nbytes, out.ptr, _sh(stream)), "rqmv_attention")
 
 
+def rope_table(head_dim: int, base: float, rows: int, stream: Stream | None = None) -> DeviceBuffer:
+    t = DeviceBuffer(rows * head_dim * 4)
+    _check(lib().lib.rqmv_rope_table(t.ptr, head_dim, base, rows, _sh(stream)), "rqmv_rope_table")
+    return t
+
+
+def attention_rope(qkv: DeviceBuffer, table: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer,
+                   pos: DeviceBuffer, q_heads: int, kv_heads: int, head_dim: int, max_ctx: int, workspace: DeviceBuffer,
+                   out: DeviceBuffer, stream: Stream | None = None):
+    _check(lib().lib.rqmv_attention_rope(qkv.ptr, table.ptr, k_cache.ptr, v_cache.ptr, pos.ptr, q_heads, kv_heads,
+                                         head_dim, max_ctx, workspace.ptr, workspace.nbytes, out.ptr, _sh(stream)),
+           "rqmv_attention_rope")
+
+
 def silu_mul(gate_up: DeviceBuffer, n: int, out: DeviceBuffer, stream: Stream | None = None):
     _check(lib().lib.rqmv_silu_mul(gate_up.ptr, n, out.ptr, _sh(stream)), "rqmv_silu_mul")
 
@@ -457,5 +478,49 @@ def advance(pos: DeviceBuffer, stream: Stream | None = None):
 
 
 def embed_row(table: DeviceBuffer, rows: int, n: int, token: DeviceBuffer, out: DeviceBuffer,
-              stream: Stream | None = None):
-    _check(lib().lib.rqmv_embed_row(table.ptr, rows, n, token.ptr, out.ptr, _sh(stream)), "rqmv_embed_row")
+              stream: Stream | None = None, parts_out: DeviceBuffer | None = None):
+    _check(lib().lib.rqmv_embed_row(table.ptr, rows, n, token.ptr, out.ptr, parts_out.ptr if parts_out else None,
+                                    _sh(stream)), "rqmv_embed_row")
+
+
+# ------------------------------------------------------- fused products ----
+
+EPI_PLAIN, EPI_GLU, EPI_RESIDUAL = 0, 1, 2
+
+
+class Fusion(ctypes.Structure):
+    _fields_ = [("norm_weight", c_void_p), ("norm_parts", c_void_p), ("norm_nparts", c_int), ("eps", c_float),
+                ("epilogue", c_int), ("residual", c_void_p), ("parts_out", c_void_p)]
+
+
+def glu_weight(fmt, rows: int, cols: int, gate: np.ndarray, up: np.ndarray) -> Weight:
+    """A (gate, up) pair as one weight of 2 x rows interleaved rows."""
+    g = np.ascontiguousarray(gate).view(np.uint8).reshape(-1)
+    u = np.ascontiguousarray(up).view(np.uint8).reshape(-1)
+    if g.nbytes != u.nbytes:
+        raise ValueError("gate and up differ in size")
+    h = c_void_p()
+    _check(lib().lib.rqmv_glu_weight_create(_fmt(fmt), rows, cols, g.ctypes.data, u.ctypes.data, g.nbytes, byref(h)),
+           "rqmv_glu_weight_create")
+    w = Weight.__new__(Weight)
+    w.handle = h.value
+    w.fmt, w.rows, w.cols, w.experts = _fmt(fmt), 2 * rows, cols, 1
+    w.gguf_nbytes = 2 * g.nbytes
+    w.glu = True
+    return w
+
+
+def residual_parts(weight: Weight) -> int:
+    n = c_int()
+    _check(lib().lib.rqmv_residual_parts(weight.handle, byref(n)), "rqmv_residual_parts")
+    return n.value
+
+
+def matvec_fused(weight: Weight, x: DeviceBuffer, y: DeviceBuffer | None, epilogue: int = EPI_PLAIN,
+                 norm_weight: DeviceBuffer | None = None, norm_parts: DeviceBuffer | None = None, norm_nparts: int = 0,
+                 eps: float = 0.0, residual: DeviceBuffer | None = None, parts_out: DeviceBuffer | None = None,
+                 stream: Stream | None = None):
+    f = Fusion(norm_weight.ptr if norm_weight else None, norm_parts.ptr if norm_parts else None, norm_nparts, eps,
+               epilogue, residual.ptr if residual else None, parts_out.ptr if parts_out else None)
+    _check(lib().lib.rqmv_matvec_fused(weight.handle, x.ptr, y.ptr if y else None, byref(f), _sh(stream)),
+           "rqmv_matvec_fused")

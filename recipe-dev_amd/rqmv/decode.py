@@ -4,23 +4,23 @@ One step runs, for a token held in device memory at a position held in device
 memory (so that a captured step replays at the next position):
 
     x = embed[token]
-    per layer:  xn = rmsnorm(x) * attn_norm            (x += previous FFN output first)
-                qkv = W_qkv xn                          (one fused projection, [q | k | v] heads)
+    per layer:  qkv = W_qkv rmsnorm(x) * attn_norm        (one fused projection, [q | k | v] heads)
                 rotate q, k (NeoX); append k, v (fp16) to the layer's cache at pos
-                a = attention(q, cache[0..pos])         (grouped-query, 1/sqrt(head_dim))
-                o = W_o a
-                xn = rmsnorm(x += o) * ffn_norm
-                gu = W_gate|up xn                       (one fused projection, [gate | up] rows)
-                h = silu(gate) * up
-                f = W_down h
-    xn = rmsnorm(x += f) * out_norm;  logits = W_head xn;  token = argmax(logits);  pos += 1
+                a = attention(q, cache[0..pos])          (grouped-query, 1/sqrt(head_dim))
+                x += W_o a
+                h = silu(W_gate xn) * (W_up xn),  xn = rmsnorm(x) * ffn_norm
+                x += W_down h
+    logits = W_head rmsnorm(x) * out_norm;  token = argmax(logits);  pos += 1
 
 This is recipe's attention block and SiLU-GLU feed-forward (lower_attention,
 recipe.rs:23056-23150; lower_normalize, recipe.rs:23190-23210; silu(gate) * up,
 recipe.rs:23279-23286, 22662-22668) run one position at a time. Every
-projection is a quantized matrix-vector product of librqmv; the norms, rotary,
-attention, SiLU-GLU, argmax and embedding gather are librqmv's decode helpers.
-The residual stream and every activation are fp32; the KV cache is fp16.
+projection is a quantized matrix-vector product of librqmv, with the norms,
+the SiLU-GLU product and the residual adds folded into the products
+(rqmv_matvec_fused): a residual epilogue leaves per-workgroup partial sums of
+squares of x that the next product's norm prologue adds up; the rotary and the
+cache append are folded into attention (rqmv_attention_rope). Six launches per
+layer: QKV, attention (two), output, gate/up, down. The residual stream and every activation are fp32; the KV cache is fp16.
 """
 from __future__ import annotations
 
@@ -28,8 +28,9 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (DTYPE_F32, DeviceBuffer, Graph, Stream, Weight, add_rmsnorm, advance, argmax, argmax_workspace,
-               attention, attention_workspace, embed_row, rope_kv, silu_mul)
+from . import (EPI_GLU, EPI_PLAIN, EPI_RESIDUAL, DeviceBuffer, Graph, Stream, Weight, advance, argmax,
+               argmax_workspace, attention_rope, attention_workspace, embed_row, glu_weight, matvec_fused,
+               residual_parts, rope_table)
 
 
 @dataclass(frozen=True)
@@ -64,13 +65,14 @@ class DecoderShape:
 @dataclass
 class LayerTensors:
     """One layer's tensors as the file stores them: fp32 norm scales and GGUF
-    blocks of the fused projections (rows of W_q, W_k, W_v stacked; rows of
-    W_gate then W_up stacked)."""
+    blocks (rows of W_q, W_k, W_v stacked as one QKV projection; W_gate and
+    W_up as ffn_gate and ffn_up)."""
     attn_norm: np.ndarray
     qkv: np.ndarray
     o: np.ndarray
     ffn_norm: np.ndarray
-    gate_up: np.ndarray
+    gate: np.ndarray
+    up: np.ndarray
     down: np.ndarray
 
 
@@ -94,18 +96,19 @@ class DecodeModel:
         self.v_cache = [DeviceBuffer(cache_bytes) for _ in range(s.layers)]
         f32 = 4
         self.x = DeviceBuffer(s.d * f32)
-        self.xn = DeviceBuffer(s.d * f32)
         self.qkv = DeviceBuffer(s.qkv_rows * f32)
         self.attn = DeviceBuffer(s.d * f32)
-        self.o = DeviceBuffer(s.d * f32)
-        self.gu = DeviceBuffer(2 * s.ffn * f32)
         self.h = DeviceBuffer(s.ffn * f32)
-        self.f = DeviceBuffer(s.d * f32)
+        # partial sums of squares of x: after the embedding or a down
+        # projection (parts_a), after an output projection (parts_b)
+        self.parts_a = DeviceBuffer(1024 * f32)
+        self.parts_b = DeviceBuffer(1024 * f32)
         self.logits = DeviceBuffer(s.vocab * f32)
         self.token = DeviceBuffer(4)
         self.pos = DeviceBuffer(4)
         self.workspace = attention_workspace(s.q_heads, s.kv_heads, s.head_dim, self.max_ctx)
         self.argmax_ws = argmax_workspace()
+        self.rope = rope_table(s.head_dim, s.rope_base, self.max_ctx)
 
     # ---------------------------------------------------------------- setup
     def set_layer(self, index: int, t: LayerTensors):
@@ -115,9 +118,12 @@ class DecodeModel:
             "qkv": Weight(s.proj_fmt, s.qkv_rows, s.d, t.qkv),
             "o": Weight(s.proj_fmt, s.d, s.d, t.o),
             "ffn_norm": DeviceBuffer.from_array(np.ascontiguousarray(t.ffn_norm, dtype=np.float32)),
-            "gate_up": Weight(s.proj_fmt, 2 * s.ffn, s.d, t.gate_up),
+            "gate_up": glu_weight(s.proj_fmt, s.ffn, s.d, t.gate, t.up),
             "down": Weight(s.proj_fmt, s.d, s.ffn, t.down),
         }
+        L = self.layers[index]
+        L["o_parts"] = residual_parts(L["o"])
+        L["down_parts"] = residual_parts(L["down"])
 
     def set_cache(self, index: int, k: np.ndarray, v: np.ndarray):
         """Prefill layer `index`'s cache: k, v are fp16 bits [kv_heads, n, head_dim]
@@ -143,21 +149,20 @@ class DecodeModel:
         s = self.shape
         if any(layer is None for layer in self.layers):
             raise RuntimeError("every layer must be set before a step")
-        embed_row(self.embed, s.vocab, s.d, self.token, self.x, stream)
+        embed_row(self.embed, s.vocab, s.d, self.token, self.x, stream, parts_out=self.parts_a)
+        na = 1
         for i, L in enumerate(self.layers):
-            add_rmsnorm(self.x, self.f if i else None, L["attn_norm"], s.d, s.eps, self.xn, stream)
-            L["qkv"].matvec(self.xn, DTYPE_F32, 1, s.d, self.qkv, s.qkv_rows, stream)
-            rope_kv(self.qkv, self.pos, s.q_heads, s.kv_heads, s.head_dim, s.rope_base, self.k_cache[i],
-                    self.v_cache[i], self.max_ctx, stream)
-            attention(self.qkv, self.k_cache[i], self.v_cache[i], self.pos, s.q_heads, s.kv_heads, s.head_dim,
-                      self.max_ctx, self.workspace, self.attn, stream)
-            L["o"].matvec(self.attn, DTYPE_F32, 1, s.d, self.o, s.d, stream)
-            add_rmsnorm(self.x, self.o, L["ffn_norm"], s.d, s.eps, self.xn, stream)
-            L["gate_up"].matvec(self.xn, DTYPE_F32, 1, s.d, self.gu, 2 * s.ffn, stream)
-            silu_mul(self.gu, s.ffn, self.h, stream)
-            L["down"].matvec(self.h, DTYPE_F32, 1, s.ffn, self.f, s.d, stream)
-        add_rmsnorm(self.x, self.f, self.out_norm, s.d, s.eps, self.xn, stream)
-        self.head.matvec(self.xn, DTYPE_F32, 1, s.d, self.logits, s.vocab, stream)
+            matvec_fused(L["qkv"], self.x, self.qkv, EPI_PLAIN, L["attn_norm"], self.parts_a, na, s.eps, stream=stream)
+            attention_rope(self.qkv, self.rope, self.k_cache[i], self.v_cache[i], self.pos, s.q_heads, s.kv_heads,
+                           s.head_dim, self.max_ctx, self.workspace, self.attn, stream)
+            matvec_fused(L["o"], self.attn, None, EPI_RESIDUAL, residual=self.x, parts_out=self.parts_b,
+                         stream=stream)
+            matvec_fused(L["gate_up"], self.x, self.h, EPI_GLU, L["ffn_norm"], self.parts_b, L["o_parts"],
+                         s.eps, stream=stream)
+            matvec_fused(L["down"], self.h, None, EPI_RESIDUAL, residual=self.x, parts_out=self.parts_a,
+                         stream=stream)
+            na = L["down_parts"]
+        matvec_fused(self.head, self.x, self.logits, EPI_PLAIN, self.out_norm, self.parts_a, na, s.eps, stream=stream)
         argmax(self.logits, s.vocab, self.token, self.argmax_ws, stream)
         advance(self.pos, stream)
 

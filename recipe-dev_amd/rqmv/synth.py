@@ -225,7 +225,8 @@ class DecoderSynth:
         self._base = {
             "qkv": (qkv_rows, s.d, weights(f, qkv_rows, s.d, seed, "dec.qkv")),
             "o": (s.d, s.d, weights(f, s.d, s.d, seed, "dec.o")),
-            "gate_up": (2 * s.ffn, s.d, weights(f, 2 * s.ffn, s.d, seed, "dec.gate_up")),
+            "gate": (s.ffn, s.d, weights(f, s.ffn, s.d, seed, "dec.gate")),
+            "up": (s.ffn, s.d, weights(f, s.ffn, s.d, seed, "dec.up")),
             "down": (s.d, s.ffn, weights(f, s.d, s.ffn, seed, "dec.down")),
         }
         self._kv_base = None
@@ -241,7 +242,7 @@ class DecoderSynth:
         f = self.shape.proj_fmt
         w = {k: layer_variant(f, b, self.seed, f"dec.l{index}.{k}") for k, (_, _, b) in self._base.items()}
         return LayerTensors(attn_norm=self._norm(f"dec.l{index}.attn_norm"), qkv=w["qkv"], o=w["o"],
-                            ffn_norm=self._norm(f"dec.l{index}.ffn_norm"), gate_up=w["gate_up"], down=w["down"])
+                            ffn_norm=self._norm(f"dec.l{index}.ffn_norm"), gate=w["gate"], up=w["up"], down=w["down"])
 
     def cache(self, index: int, ctx: int):
         """fp16 bits [kv_heads, ctx, head_dim] of keys and values for layer `index`."""

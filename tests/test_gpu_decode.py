@@ -219,3 +219,147 @@ def test_decode_real_head_shapes(gpu):
     want = R.step(3, ctx)
     assert rel_err(logits, want) < 1e-3
     assert model.read_token() == int(np.argmax(logits))
+
+
+# ------------------------------------------------------- fused products ----
+
+def _mv_ref(fmt, w, rows, cols, x):
+    import oracle
+    return oracle.dequant_rows(fmt, w, rows, cols).reshape(rows, cols).astype(np.float64) @ np.asarray(x, np.float64)
+
+
+@pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 6144, 4096), ("q8_0", 4096, 4096), ("q6_k", 512, 1024),
+                                           ("q4_0", 300, 4096)])
+def test_fused_norm_prologue(gpu, fmt, rows, cols):
+    w = synth.weights(fmt, rows, cols, seed=rows + cols)
+    W = gpu.Weight(fmt, rows, cols, w)
+    x = (RNG.standard_normal(cols) * 30).astype(np.float32)
+    nw = (1 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
+    # the partial sums may be split any way: three parts here
+    parts = np.array([np.sum(x[:1000].astype(np.float64) ** 2), np.sum(x[1000:1500].astype(np.float64) ** 2),
+                      np.sum(x[1500:].astype(np.float64) ** 2)], dtype=np.float32)
+    X, NW, P, Y = (gpu.DeviceBuffer.from_array(a) for a in (x, nw, parts, np.zeros(rows, np.float32)))
+    gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, NW, P, 3, 1e-5)
+    gpu.synchronize()
+    want = _mv_ref(fmt, w, rows, cols, ref.rmsnorm(x, nw, 1e-5))
+    assert rel_err(Y.download(np.float32), want) < 1e-3
+
+
+@pytest.mark.parametrize("fmt,n,cols", [("q4_k", 14336, 4096), ("q4_k", 512, 256), ("q8_0", 1000, 512)])
+def test_fused_glu_epilogue(gpu, fmt, n, cols):
+    g = synth.weights(fmt, n, cols, seed=3)
+    u = synth.weights(fmt, n, cols, seed=4)
+    W = gpu.glu_weight(fmt, n, cols, g, u)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    X, Y = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * n)
+    gpu.matvec_fused(W, X, Y, gpu.EPI_GLU)
+    gpu.synchronize()
+    want = ref.silu_mul(_mv_ref(fmt, g, n, cols, x), _mv_ref(fmt, u, n, cols, x))
+    assert rel_err(Y.download(np.float32), want) < 1e-3
+    # a plain product over the pair weight writes the rows interleaved
+    Z = gpu.DeviceBuffer(8 * n)
+    W.matvec(X, gpu.DTYPE_F32, 1, cols, Z, 2 * n)
+    gpu.synchronize()
+    z = Z.download(np.float32)
+    assert rel_err(z[0::2], _mv_ref(fmt, g, n, cols, x)) < 1e-3
+    assert rel_err(z[1::2], _mv_ref(fmt, u, n, cols, x)) < 1e-3
+
+
+@pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 4096, 14336), ("q4_k", 4096, 4096), ("q6_k", 256, 512)])
+def test_fused_residual_epilogue_and_parts(gpu, fmt, rows, cols):
+    w = synth.weights(fmt, rows, cols, seed=9)
+    W = gpu.Weight(fmt, rows, cols, w)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    r0 = (RNG.standard_normal(rows) * 50).astype(np.float32)
+    n = gpu.residual_parts(W)
+    assert 1 <= n <= 1024
+    X, R, P = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(r0), gpu.DeviceBuffer(4 * n)
+    gpu.matvec_fused(W, X, None, gpu.EPI_RESIDUAL, residual=R, parts_out=P)
+    gpu.synchronize()
+    r1 = R.download(np.float32)
+    delta = _mv_ref(fmt, w, rows, cols, x)
+    assert rel_err(r1.astype(np.float64) - r0, delta) < 1e-3
+    parts = P.download(np.float32, n)
+    assert abs(float(np.sum(parts, dtype=np.float64)) - float(np.sum(r1.astype(np.float64) ** 2))) \
+        <= 1e-5 * float(np.sum(r1.astype(np.float64) ** 2))
+    # the parts feed a following norm prologue exactly as a full sum would
+    w2 = synth.weights("q4_k", 512, rows, seed=10)
+    W2 = gpu.Weight("q4_k", 512, rows, w2)
+    nw = np.ones(rows, np.float32)
+    NW, Y = gpu.DeviceBuffer.from_array(nw), gpu.DeviceBuffer(4 * 512)
+    gpu.matvec_fused(W2, R, Y, gpu.EPI_PLAIN, NW, P, n, 1e-5)
+    gpu.synchronize()
+    assert rel_err(Y.download(np.float32), _mv_ref("q4_k", w2, 512, rows, ref.rmsnorm(r1, nw, 1e-5))) < 1e-3
+
+
+def test_embed_row_parts(gpu):
+    rows, n = 7, 4096
+    table = RNG.standard_normal((rows, n)).astype(np.float32)
+    T, O, P = gpu.DeviceBuffer.from_array(table), gpu.DeviceBuffer(4 * n), gpu.DeviceBuffer(4)
+    gpu.embed_row(T, rows, n, _i32(gpu, 3), O, parts_out=P)
+    gpu.synchronize()
+    assert np.array_equal(O.download(np.float32), table[3])
+    want = float(np.sum(table[3].astype(np.float64) ** 2))
+    assert abs(float(P.download(np.float32, 1)[0]) - want) <= 1e-5 * want
+
+
+def test_fused_rejects_bad_arguments(gpu):
+    w = synth.weights("q4_k", 64, 256, seed=1)
+    W = gpu.Weight("q4_k", 64, 256, w)
+    X, Y = gpu.DeviceBuffer(4 * 256), gpu.DeviceBuffer(4 * 64)
+    with pytest.raises(gpu.RqmvError):
+        gpu.matvec_fused(W, X, Y, gpu.EPI_GLU)  # not a pair weight
+    with pytest.raises(gpu.RqmvError):
+        gpu.matvec_fused(W, X, None, gpu.EPI_RESIDUAL)  # no residual
+    P = gpu.DeviceBuffer(4 * 2048)
+    with pytest.raises(gpu.RqmvError):
+        gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, X, P, 2000, 1e-5)  # too many parts
+
+
+@pytest.mark.parametrize("nq,nkv,hd", [(32, 8, 128), (4, 2, 64), (8, 1, 256)])
+@pytest.mark.parametrize("pos", [0, 63, 64, 300, 4099])
+def test_attention_rope_fused(gpu, nq, nkv, hd, pos):
+    """Rotary, cache append and attention in one call, against the f64
+    reference (the new key and value rounded to fp16 as the cache holds them)."""
+    max_ctx, base = 4100, 500000.0
+    qkv = RNG.standard_normal((nq + 2 * nkv) * hd).astype(np.float32)
+    kc = RNG.standard_normal((nkv, max_ctx, hd)).astype(np.float16)
+    vc = RNG.standard_normal((nkv, max_ctx, hd)).astype(np.float16)
+    Q = gpu.DeviceBuffer.from_array(qkv)
+    K = gpu.DeviceBuffer.from_array(kc.view(np.uint16))
+    V = gpu.DeviceBuffer.from_array(vc.view(np.uint16))
+    T = gpu.rope_table(hd, base, max_ctx)
+    ws = gpu.attention_workspace(nq, nkv, hd, max_ctx)
+    O = gpu.DeviceBuffer(nq * hd * 4)
+    gpu.attention_rope(Q, T, K, V, _i32(gpu, pos), nq, nkv, hd, max_ctx, ws, O)
+    gpu.synchronize()
+    assert np.array_equal(Q.download(np.float32), qkv)  # qkv is not modified
+    q_ref = ref.rope_neox(qkv[:nq * hd].reshape(nq, hd), pos, base)
+    k_ref = ref.rope_neox(qkv[nq * hd:(nq + nkv) * hd].reshape(nkv, hd), pos, base)
+    v_new = qkv[(nq + nkv) * hd:].reshape(nkv, hd)
+    k_all = kc.astype(np.float64)
+    v_all = vc.astype(np.float64)
+    k_all[:, pos] = k_ref.astype(np.float32).astype(np.float16)
+    v_all[:, pos] = v_new.astype(np.float16)
+    want = ref.attention(q_ref, k_all, v_all, pos + 1)
+    assert rel_err(O.download(np.float32), want.reshape(-1)) < 1e-5
+    kg = K.download(np.uint16).reshape(nkv, max_ctx, hd).view(np.float16)
+    vg = V.download(np.uint16).reshape(nkv, max_ctx, hd).view(np.float16)
+    k16 = k_ref.astype(np.float16).astype(np.float64)
+    assert np.all(np.abs(kg[:, pos].astype(np.float64) - k16) <= np.abs(k16) * 2 ** -10 + 2 ** -24)
+    assert np.array_equal(vg[:, pos], v_new.astype(np.float16))
+    others = np.ones(max_ctx, bool)
+    others[pos] = False
+    assert np.array_equal(kg[:, others], kc[:, others]) and np.array_equal(vg[:, others], vc[:, others])
+
+
+def test_rope_table_matches_rope_kv(gpu):
+    hd, base, rows = 128, 500000.0, 300
+    T = gpu.rope_table(hd, base, rows)
+    gpu.synchronize()
+    t = T.download(np.float32).reshape(rows, hd // 2, 2)
+    i = np.arange(hd // 2)
+    for p in (0, 1, 77, 299):
+        ang = p * np.exp(-(2.0 * i / hd) * np.log(base))
+        assert np.array_equal(t[p, :, 0], np.cos(ang).astype(np.float32))
+        assert np.array_equal(t[p, :, 1], np.sin(ang).astype(np.float32))

@@ -102,7 +102,7 @@ def test_decoder_with_zero_projections_is_head_of_normed_embedding():
     layers = []
     for i in range(s.layers):
         t = D.layer(i)
-        layers.append(LayerTensors(t.attn_norm, t.qkv, _zero_scales(s.proj_fmt, t.o), t.ffn_norm, t.gate_up,
+        layers.append(LayerTensors(t.attn_norm, t.qkv, _zero_scales(s.proj_fmt, t.o), t.ffn_norm, t.gate, t.up,
                                    _zero_scales(s.proj_fmt, t.down)))
     embed = D.embed()[: s.vocab]
     R = ref.DecoderReference(s, embed, D.out_norm(), D.head(), layers, [D.cache(i, 4) for i in range(s.layers)], 8)
