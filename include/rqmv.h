@@ -193,11 +193,8 @@ int rqmv_silu_mul(const float* gate_up, int n, float* out, void* stream);
 int rqmv_argmax_workspace_size(size_t* bytes);
 int rqmv_argmax(const float* values, int n, int* out, void* workspace, size_t workspace_bytes, void* stream);
 
-/* out = table[token mod rows] (rows x n fp32): the next token's embedding.
- * parts_out (may be NULL) receives one partial sum of squares of out, for a
- * fused rmsnorm prologue (rqmv_matvec_fused, norm_nparts = 1). */
-int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, float* parts_out,
-                   void* stream);
+/* out = table[token mod rows] (rows x n fp32): the next token's embedding. */
+int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, void* stream);
 
 /* A gate and an up projection of one width stored as one weight of 2 x rows
  * rows, (gate_i, up_i) interleaved, for the fused SiLU-GLU epilogue. Each of
@@ -208,35 +205,26 @@ int rqmv_glu_weight_create(int format, int64_t rows, int64_t cols, const void* g
 
 /* A decode-step product with its neighbours folded in (one fp32 activation
  * row, a plain quantized weight):
- *   prologue (norm_weight != NULL): x is read as rmsnorm(x) * norm_weight,
- *     x_i * norm_weight_i / sqrt(ss / cols + eps), where ss is the in-order
- *     sum of the norm_nparts (1..1024) partial sums of squares of x that a
- *     residual epilogue or rqmv_embed_row left in norm_parts;
- *   epilogue RQMV_EPI_PLAIN: y = W x;
+ *   prologue (norm_weight != NULL): the product reads u = x + delta (delta
+ *     may be NULL), normalised: u_i * norm_weight_i / sqrt(sum u^2 / cols +
+ *     eps); when x_out is not NULL, u itself is written there (the updated
+ *     residual stream; x_out must differ from x and delta);
+ *   epilogue RQMV_EPI_PLAIN: y = W u';
  *   epilogue RQMV_EPI_GLU (a rqmv_glu_weight_create weight): y_i =
- *     silu(gate_i x) * (up_i x), silu(v) = v * 0.5 (tanh(v / 2) + 1);
- *   epilogue RQMV_EPI_RESIDUAL: residual_r += (W x)_r for every row, and
- *     parts_out receives rqmv_residual_parts(weight) partial sums of squares
- *     of the updated residual (y is not written).
- * recipe runs these as separate nodes (Normalize, Contraction, the SiLU-GLU
- * product and the residual add: recipe.rs:23190-23210, 4532-4604,
+ *     silu(gate_i u') * (up_i u'), silu(v) = v * 0.5 (tanh(v / 2) + 1).
+ * recipe runs these as separate nodes (the residual add, Normalize,
+ * Contraction and the SiLU-GLU product: recipe.rs:23190-23210, 4532-4604,
  * 23279-23286); the fusion saves their launches and activation round trips. */
-enum { RQMV_EPI_PLAIN = 0, RQMV_EPI_GLU = 1, RQMV_EPI_RESIDUAL = 2 };
+enum { RQMV_EPI_PLAIN = 0, RQMV_EPI_GLU = 1 };
 typedef struct {
     const float* norm_weight;
-    const float* norm_parts;
-    int norm_nparts;
     float eps;
+    const float* delta;
+    float* x_out;
     int epilogue;
-    float* residual;
-    float* parts_out;
 } rqmv_fusion;
 int rqmv_matvec_fused(const rqmv_weight* weight, const float* x_dev, float* y_dev, const rqmv_fusion* fusion,
                       void* stream);
-
-/* The number of partial sums a RQMV_EPI_RESIDUAL product over `weight`
- * writes (what a following fused norm passes as norm_nparts). */
-int rqmv_residual_parts(const rqmv_weight* weight, int* nparts);
 
 /* *pos += 1 on the device (the last launch of a captured decode step). */
 int rqmv_advance(int* pos, void* stream);

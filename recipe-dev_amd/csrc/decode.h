@@ -20,8 +20,7 @@ hipError_t launch_rope_table(float2* table, int head_dim, double base, int rows,
 hipError_t launch_silu_mul(const float* gu, int n, float* out, hipStream_t stream);
 size_t argmax_workspace_bytes();
 hipError_t launch_argmax(const float* v, int n, int* out, void* workspace, hipStream_t stream);
-hipError_t launch_embed_row(const float* table, int rows, int n, const int* token, float* out, float* parts,
-                            hipStream_t stream);
+hipError_t launch_embed_row(const float* table, int rows, int n, const int* token, float* out, hipStream_t stream);
 hipError_t launch_advance(int* pos, hipStream_t stream);
 
 }  // namespace rq

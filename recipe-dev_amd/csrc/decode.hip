@@ -509,28 +509,11 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_final_kernel(const floa
     if (t == 0) *out = idx == 0x7fffffff ? 0 : idx;
 }
 
-// out = table[token mod rows] (the next token's embedding row). With `parts`
-// (one workgroup) also parts[0] = sum out^2 (threads' strided shares, then a
-// fixed tree), the partial sum a fused rmsnorm prologue reads.
+// out = table[token mod rows] (the next token's embedding row).
 __global__ void __launch_bounds__(256) embed_row_kernel(const float* table, int rows, int n, const int* token,
-                                                        float* out, float* parts) {
-    __shared__ float red[256];
+                                                        float* out) {
     const int r = ((*token % rows) + rows) % rows;
-    float ss = 0.f;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        const float v = table[(size_t)r * n + i];
-        out[i] = v;
-        ss = fmaf(v, v, ss);
-    }
-    if (!parts) return;
-    const int t = threadIdx.x;
-    red[t] = ss;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (t < s) red[t] += red[t + s];
-        __syncthreads();
-    }
-    if (t == 0) parts[0] = red[0];
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) out[i] = table[(size_t)r * n + i];
 }
 
 // Advances the decode position by one (the last launch of a captured step).
@@ -675,12 +658,10 @@ hipError_t launch_argmax(const float* v, int n, int* out, void* workspace, hipSt
     return hipGetLastError();
 }
 
-hipError_t launch_embed_row(const float* table, int rows, int n, const int* token, float* out, float* parts,
-                            hipStream_t stream) {
+hipError_t launch_embed_row(const float* table, int rows, int n, const int* token, float* out, hipStream_t stream) {
     int grid = (n + 255) / 256;
     if (grid > 256) grid = 256;
-    if (parts) grid = 1;
-    hipLaunchKernelGGL(embed_row_kernel, dim3(grid), dim3(256), 0, stream, table, rows, n, token, out, parts);
+    hipLaunchKernelGGL(embed_row_kernel, dim3(grid), dim3(256), 0, stream, table, rows, n, token, out);
     return hipGetLastError();
 }
 

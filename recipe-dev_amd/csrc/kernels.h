@@ -27,22 +27,20 @@ struct MvParams {
     Planes P2;
     int64_t split;
     // Decode-step fusions (quantized weights, one fp32 activation row):
-    // prologue: when norm_w is set, x is replaced by x * norm_w / sqrt(ss / K + eps)
-    // with ss the in-order sum of norm_nparts partial sums of squares of x;
-    // epilogue (epi): kEpiPlain writes y; kEpiGlu takes rows as (gate, up)
-    // pairs and writes y[i] = silu(row 2i) * row 2i+1; kEpiResidual adds each
-    // row into resid (resid[r] += row r) and writes one partial sum of squares
-    // of the updated resid rows per workgroup to parts_out[blockIdx.x].
+    // prologue (norm_w set): x is read as u = x + delta (delta optional), u is
+    // written to x_out (when set, by workgroup 0), and the product takes
+    // rmsnorm(u) * norm_w = u * norm_w / sqrt(sum u^2 / K + eps), the common
+    // factor applied to the finished products; epilogue (epi): kEpiPlain
+    // writes y, kEpiGlu takes rows as (gate, up) pairs and writes
+    // y[i] = silu(row 2i) * row 2i+1.
     int epi = 0;
-    float* resid = nullptr;
-    float* parts_out = nullptr;
     const float* norm_w = nullptr;
-    const float* norm_parts = nullptr;
-    int norm_nparts = 0;
+    const float* delta = nullptr;
+    float* x_out = nullptr;
     float eps = 0.f;
 };
 
-enum Epilogue : int { kEpiPlain = 0, kEpiGlu = 1, kEpiResidual = 2 };
+enum Epilogue : int { kEpiPlain = 0, kEpiGlu = 1 };
 
 struct LaunchShape {
     int G = 64;       // lanes per row group
@@ -65,8 +63,7 @@ hipError_t launch_dequant(int fmt, const Planes& P, int64_t rows, int cols, floa
 size_t matvec_lds_bytes(int fmt, int xtype, int M, int cols);
 
 // The decode-step fused product (M = 1, fp32 activations, quantized weight):
-// the launch shape it uses (its grid is the number of partial sums a
-// kEpiResidual launch writes) and the launch itself.
+// the launch shape it uses and the launch itself.
 LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus);
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream);
 

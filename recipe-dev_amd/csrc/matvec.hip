@@ -82,12 +82,11 @@ __device__ __forceinline__ void load_rows(const MvParams& p, const StepWalk& w, 
     }
 }
 
-// The tile's cross-lane sums and its epilogue (MvParams::epi; the fused
-// epilogues run with M = 1 and, for kEpiGlu, an even R, so that a lane group
-// holds each (gate, up) row pair). `ss` gathers the lane's share of the
-// residual sum of squares.
+// The tile's cross-lane sums and its epilogue (MvParams::epi; the GLU
+// epilogue runs with M = 1 and an even R, so that a lane group holds each
+// (gate, up) row pair). NORM: the rmsnorm factor multiplies the sums first.
 template <int M, int R, bool NORM = false>
-__device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int g, float (&acc)[R][M], float& ss,
+__device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int g, float (&acc)[R][M],
                                             float norm_scale = 1.f) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -103,21 +102,13 @@ __device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int
                 if (row0 + r < p.rows)
 #pragma unroll
                     for (int mm = 0; mm < M; ++mm) p.y[(int64_t)mm * p.ldy + row0 + r] = acc[r][mm];
-        } else if (p.epi == kEpiGlu) {
+        } else {
             // silu(gate) * up, silu(v) = v * sigmoid(v), sigmoid = 0.5 (tanh(v / 2) + 1) (recipe.rs:22662-22668)
 #pragma unroll
             for (int r = 0; r + 1 < R; r += 2)
                 if (row0 + r + 1 < p.rows) {
                     const float gt = acc[r][0];
                     p.y[(row0 + r) / 2] = gt * (0.5f * (tanhf(0.5f * gt) + 1.0f)) * acc[r + 1][0];
-                }
-        } else {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows) {
-                    const float v = p.resid[row0 + r] + acc[r][0];
-                    p.resid[row0 + r] = v;
-                    ss = fmaf(v, v, ss);
                 }
         }
     }
@@ -143,8 +134,7 @@ __device__ __forceinline__ void load_rows_rs(const MvParams& p, __amdgpu_buffer_
 // digits of every activation row; the tile's reduction after its last step.
 template <int FMT, int M, int R, bool NORM = false>
 __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, int sub, int g, const ChunkData<FMT> (&d)[R],
-                                         float (&acc)[R][M], const uint4* xd, const uint4* xb, float& ss,
-                                         float norm_scale = 1.f) {
+                                         float (&acc)[R][M], const uint4* xd, const uint4* xb, float norm_scale = 1.f) {
     constexpr int XP = Traits<FMT>::XP;
     const int nch = p.P.nch;
     const int c = w.chunk();
@@ -164,106 +154,88 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
                 if (row0 + r < p.rows) dot_int<FMT, 1>(d[r], c, xv, bv, &acc[r][mm]);
         }
     }
-    if (w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, ss, norm_scale);
-}
-
-// rmsnorm prologue. The staged activations are x * norm_w (per column); the
-// common factor 1 / sqrt(ss / K + eps) multiplies the finished products, so
-// the partial sums of squares (ss = their in-order sum: lane l adds parts
-// l, l + 64, ..., then a fixed DPP tree) are only needed at the first tile's
-// end, and every wave forms the factor itself (no barrier on the way in).
-constexpr int kNormPartsPerLane = 16;  // up to 1024 partial sums
-
-__device__ __forceinline__ void issue_norm_parts(const MvParams& p, float (&v)[kNormPartsPerLane]) {
-    // straight-line loads from clamped indices; the duplicates are dropped in norm_scale_of
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int j = 0; j < kNormPartsPerLane; ++j) {
-        const int i = lane + 64 * j;
-        v[j] = p.norm_parts[i < p.norm_nparts ? i : p.norm_nparts - 1];
-    }
-}
-
-__device__ __forceinline__ float norm_scale_of(const MvParams& p, const float (&v)[kNormPartsPerLane]) {
-    const int lane = threadIdx.x & 63;
-    float a = 0.f;
-#pragma unroll
-    for (int j = 0; j < kNormPartsPerLane; ++j) a += lane + 64 * j < p.norm_nparts ? v[j] : 0.f;
-    a = group_sum(a, 64);
-    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
-    return 1.0f / sqrtf(a / (float)p.K + p.eps);
+    if (w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, norm_scale);
 }
 
 // Quantized weights, integer dot of staged activation digits (chunk.h,
-// stage.h). Two register buffers alternate: while one step is computed, the
-// loads of the next are in flight, and the buffer just computed is refilled
-// for the step after that. The first two steps' weight loads are issued
-// before the activations are staged. NORM: the rmsnorm prologue (M = 1,
-// fp32 activations).
+// stage.h). A ring of NB register buffers: while one step is computed, the
+// loads of the next NB - 1 are in flight, and the buffer just computed is
+// refilled for the step NB ahead. All NB first steps' weight loads are issued
+// before the activations are staged, so the staging overlaps them. NORM: the
+// rmsnorm prologue (M = 1, fp32 activations).
+template <int M, int R>
+constexpr int ring_depth() {
+    return 2;  // deeper rings (3, 4) measured slower on gfx950 at batch 1
+}
+
 template <int FMT, int M, int R, bool XF32, bool NORM = false>
 __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     constexpr int XP = Traits<FMT>::XP;
+    constexpr int NB = ring_depth<M, R>();
     extern __shared__ uint4 smem[];
-    __shared__ float block_scalar[8];  // the waves' residual sums of squares
+    __shared__ float block_scalar[8];  // NORM: the waves' sums of squares
     const int nch = p.P.nch;
     uint4* xd = smem;
     uint4* xb = smem + M * XP * nch;
     const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane / p.G;
     const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
-    StepWalk wa = make_walk(p, R, g);
-    StepWalk wb = wa;
-    wb.next();
+    StepWalk w[NB];
+    w[0] = make_walk(p, R, g);
+#pragma unroll
+    for (int i = 1; i < NB; ++i) {
+        w[i] = w[i - 1];
+        w[i].next();
+    }
 
-    ChunkData<FMT> A[R], B[R];
-    float parts[kNormPartsPerLane];
-    if constexpr (NORM) issue_norm_parts(p, parts);
+    ChunkData<FMT> buf[NB][R];
+    NormIn nin{};
+    float ssq = 0.f;  // NORM: this thread's share of sum (x + delta)^2
+    if constexpr (NORM) nin = NormIn{p.norm_w, p.delta, blockIdx.x == 0 ? p.x_out : nullptr};
     if (stage_items<FMT>(nch, M) <= kStageNJ * p.block) {
         StageItem<XF32, NORM> it[kStageNJ];
-        stage_multi_issue<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, it, p.norm_w);
+        stage_multi_issue<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, it, nin);
         // keep the activation loads ahead of the weight loads: waiting for them
         // then leaves the weight loads in flight
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
-        load_rows_rs<FMT, R>(p, rs, wa, sub, A);
-        load_rows_rs<FMT, R>(p, rs, wb, sub, B);
-        stage_multi_finish<FMT, XF32, NORM>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb));
+#pragma unroll
+        for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
+        stage_multi_finish<FMT, XF32, NORM>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb), nin, &ssq);
     } else {
-        load_rows_rs<FMT, R>(p, rs, wa, sub, A);
-        load_rows_rs<FMT, R>(p, rs, wb, sub, B);
-        stage_all<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, xd, reinterpret_cast<float*>(xb), p.norm_w);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
+        stage_all<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, xd, reinterpret_cast<float*>(xb), nin, &ssq);
+    }
+    if constexpr (NORM) {
+        ssq = group_sum(ssq, 64);
+        if (lane == 63) block_scalar[threadIdx.x >> 6] = ssq;
     }
     __syncthreads();
     float norm_scale = 1.f;
-    if constexpr (NORM) norm_scale = norm_scale_of(p, parts);
+    if constexpr (NORM) {  // the waves' sums in order: every workgroup forms the same factor
+        float t = 0.f;
+        for (int i = 0; i < (p.block >> 6); ++i) t += block_scalar[i];
+        norm_scale = 1.0f / sqrtf(t / (float)p.K + p.eps);
+    }
 
     float acc[R][M];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
-    float ss = 0.f;
-    while (wa.valid()) {
-        step_int<FMT, M, R, NORM>(p, wa, sub, g, A, acc, xd, xb, ss, norm_scale);
-        wa = wb;
-        wa.next();
-        load_rows_rs<FMT, R>(p, rs, wa, sub, A);
-        if (!wb.valid()) break;
-        step_int<FMT, M, R, NORM>(p, wb, sub, g, B, acc, xd, xb, ss, norm_scale);
-        wb = wa;
-        wb.next();
-        load_rows_rs<FMT, R>(p, rs, wb, sub, B);
-    }
-    if (p.epi == kEpiResidual) {  // the workgroup's partial sum of squares, waves in order
-        ss = group_sum(ss, 64);
-        __syncthreads();
-        if (lane == 63) block_scalar[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float t = 0.f;
-            for (int w = 0; w < (p.block >> 6); ++w) t += block_scalar[w];
-            p.parts_out[blockIdx.x] = t;
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (!w[i].valid()) goto done;
+            step_int<FMT, M, R, NORM>(p, w[i], sub, g, buf[i], acc, xd, xb, norm_scale);
+            // this buffer takes the step after the latest one issued
+            w[i] = w[(i + NB - 1) % NB];
+            w[i].next();
+            load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
         }
     }
+done:
+    return;
 }
 
 // F16 weights (router-sized): fp16 activations through v_dot2_f32_f16, fp32
@@ -288,7 +260,6 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
     bool loaded = true;
-    float unused_ss = 0.f;  // F16 weights take the plain epilogue only
     while (w.valid()) {
         if (!loaded) load_rows<F16, R>(p, w, sub, cur);
         loaded = false;
@@ -313,7 +284,7 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
                     if (row0 + r < p.rows) dot_f16w<M>(cur[r], xv, acc[r]);
             }
         }
-        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc, unused_ss);
+        if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
         w.next();
     }
 }
@@ -436,6 +407,7 @@ hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const Lau
 LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus) {
     LaunchShape s = plan_matvec(fmt, rows, cols, 1, X_F32, cus);
     s.R = 2;  // a lane group holds a (gate, up) row pair for kEpiGlu
+    if (s.block > 512) s.block = 512;
     const int64_t rows_per_wave = (int64_t)(64 / s.G) * s.R;
     const int64_t tiles = (rows + rows_per_wave - 1) / rows_per_wave;
     const int wpb = s.block / 64;
@@ -453,7 +425,7 @@ static hipError_t launch_fused_fmt(const MvParams& p, const LaunchShape& s, hipS
 }
 
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream) {
-    if (s.R != 2 || s.block > 512 || (p.norm_w && p.norm_nparts > kNormPartsPerLane * 64)) return hipErrorInvalidValue;
+    if (s.R != 2 || s.block > 512) return hipErrorInvalidValue;
     switch (fmt) {
         case Q4_0: return launch_fused_fmt<Q4_0>(p, s, stream);
         case Q8_0: return launch_fused_fmt<Q8_0>(p, s, stream);

@@ -305,15 +305,6 @@ int rqmv_matvec_timed(const rqmv_weight* w, const void* x_dev, int x_dtype, int 
                        static_cast<hipEvent_t>(stop_event));
 }
 
-int rqmv_residual_parts(const rqmv_weight* w, int* nparts) {
-    DeviceInfo info;
-    int rc = check_launch(w, &info);
-    if (rc != RQMV_OK) return rc;
-    if (!nparts) return fail(RQMV_EINVAL, "nparts is NULL");
-    *nparts = rq::plan_fused(w->fmt, w->rows * w->experts, w->cols, info.cus).grid;
-    return RQMV_OK;
-}
-
 int rqmv_matvec_fused(const rqmv_weight* w, const float* x_dev, float* y_dev, const rqmv_fusion* f, void* stream) {
     DeviceInfo info;
     int rc = check_launch(w, &info);
@@ -335,30 +326,27 @@ int rqmv_matvec_fused(const rqmv_weight* w, const float* x_dev, float* y_dev, co
         return fail(RQMV_EINVAL, "fused: cols too large for one LDS stage");
     const rq::LaunchShape s = rq::plan_fused(w->fmt, w->rows, w->cols, info.cus);
     p.G = s.G;
+    if (!y_dev) return fail(RQMV_EINVAL, "fused: y is NULL");
     switch (f->epilogue) {
-        case RQMV_EPI_PLAIN:
-            if (!y_dev) return fail(RQMV_EINVAL, "fused: y is NULL");
-            break;
+        case RQMV_EPI_PLAIN: break;
         case RQMV_EPI_GLU:
-            if (!w->glu || !y_dev) return fail(RQMV_EINVAL, "fused: the GLU epilogue needs a GLU weight and y");
+            if (!w->glu) return fail(RQMV_EINVAL, "fused: the GLU epilogue needs a GLU weight");
             p.epi = rq::kEpiGlu;
-            break;
-        case RQMV_EPI_RESIDUAL:
-            if (!f->residual || !f->parts_out) return fail(RQMV_EINVAL, "fused: residual and parts_out are required");
-            p.epi = rq::kEpiResidual;
-            p.resid = f->residual;
-            p.parts_out = f->parts_out;
             break;
         default: return fail(RQMV_EINVAL, "fused: unknown epilogue");
     }
     if (f->norm_weight) {
-        if (!f->norm_parts || f->norm_nparts < 1 || f->norm_nparts > 1024 || !(f->eps >= 0.f) ||
-            reinterpret_cast<uintptr_t>(f->norm_weight) % 16 != 0)
-            return fail(RQMV_EINVAL, "fused: the norm needs 1..1024 partial sums, eps >= 0 and 16-byte aligned scales");
+        if (!(f->eps >= 0.f)) return fail(RQMV_EINVAL, "fused: eps must be >= 0");
+        if (((uintptr_t)f->norm_weight | (uintptr_t)f->delta | (uintptr_t)f->x_out) & 15)
+            return fail(RQMV_EINVAL, "fused: norm weight, delta and x_out must be 16-byte aligned");
+        if (f->x_out && (f->x_out == x_dev || f->x_out == f->delta))
+            return fail(RQMV_EINVAL, "fused: x_out must be a buffer other than x and delta");
         p.norm_w = f->norm_weight;
-        p.norm_parts = f->norm_parts;
-        p.norm_nparts = f->norm_nparts;
+        p.delta = f->delta;
+        p.x_out = f->x_out;
         p.eps = f->eps;
+    } else if (f->delta || f->x_out) {
+        return fail(RQMV_EINVAL, "fused: delta and x_out come with the norm prologue");
     }
     hipError_t e = rq::launch_matvec_fused(w->fmt, p, s, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "fused matvec launch");
@@ -578,10 +566,9 @@ int rqmv_argmax(const float* values, int n, int* out, void* workspace, size_t wo
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "argmax launch");
 }
 
-int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, float* parts_out,
-                   void* stream) {
+int rqmv_embed_row(const float* table, int rows, int n, const int* token, float* out, void* stream) {
     if (!table || !token || !out || rows <= 0 || n <= 0) return fail(RQMV_EINVAL, "embed_row: bad arguments");
-    hipError_t e = rq::launch_embed_row(table, rows, n, token, out, parts_out, static_cast<hipStream_t>(stream));
+    hipError_t e = rq::launch_embed_row(table, rows, n, token, out, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "embed_row launch");
 }
 

@@ -36,11 +36,21 @@ template <bool XF32, bool NORM = false>
 struct StageItem {
     uint4 raw[XF32 ? 2 : 1];
     uint4 nw[NORM ? 2 : 1];  // the item's eight norm scales (NORM only)
+    uint4 dl[NORM ? 2 : 1];  // the item's eight residual deltas (NORM only)
+};
+
+// The rmsnorm prologue's operands (NORM staging, fp32 activations): per-column
+// scales, an optional delta added to x first, and where workgroup 0 writes
+// x + delta (null elsewhere).
+struct NormIn {
+    const float* w;
+    const float* delta;
+    float* x_out;
 };
 
 template <int FMT, bool XF32, bool NORM = false>
 __device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* xv, int64_t ldx,
-                                            StageItem<XF32, NORM>& it, const float* norm_w = nullptr) {
+                                            StageItem<XF32, NORM>& it, const NormIn& nin = NormIn{}) {
     constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK;
     const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
     int k0 = c * CW + b * 32 + q * 8;
@@ -50,8 +60,14 @@ __device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* x
         it.raw[0] = *reinterpret_cast<const uint4*>(xm);
         it.raw[1] = *reinterpret_cast<const uint4*>(xm + 4);
         if constexpr (NORM) {
-            it.nw[0] = *reinterpret_cast<const uint4*>(norm_w + k0);
-            it.nw[1] = *reinterpret_cast<const uint4*>(norm_w + k0 + 4);
+            it.nw[0] = *reinterpret_cast<const uint4*>(nin.w + k0);
+            it.nw[1] = *reinterpret_cast<const uint4*>(nin.w + k0 + 4);
+            if (nin.delta) {
+                it.dl[0] = *reinterpret_cast<const uint4*>(nin.delta + k0);
+                it.dl[1] = *reinterpret_cast<const uint4*>(nin.delta + k0 + 4);
+            } else {
+                it.dl[0] = it.dl[1] = make_uint4(0, 0, 0, 0);
+            }
         }
     } else {
         it.raw[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xv) + (int64_t)m * ldx + k0);
@@ -85,11 +101,45 @@ __device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* ou
     out[3] = __builtin_amdgcn_perm(D, C, 0x07050301u);
 }
 
+// Encodes eight values of a 32-value block whose maximum magnitude is amax:
+// x = rint(v * 30583 / amax) as digit words (nibble formats: four words, one
+// per balanced hex digit; Q8_0: two low-byte words, then two high-byte words),
+// the integer sum of the eight in `sum`; returns the block scale amax / 30583.
+template <int FMT>
+__device__ __forceinline__ float encode_item(const float (&v)[8], float amax, uint32_t (&w4)[4], int& sum) {
+    const float inv = amax > 0.f ? kXMax / amax : 0.f;
+    int xi[8];
+    sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int t = (int)__builtin_rintf(v[k] * inv);
+        xi[k] = t < -30583 ? -30583 : (t > 30583 ? 30583 : t);
+        sum += xi[k];
+    }
+    if constexpr (FMT == Q8_0) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            uint32_t uu[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) uu[e] = ((uint32_t)(xi[4 * w + e] + 0x8080) ^ 0x8080u) & 0xffffu;
+            const uint32_t pa = uu[0] | (uu[1] << 16), pb = uu[2] | (uu[3] << 16);
+            w4[w] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
+            w4[2 + w] = __builtin_amdgcn_perm(pb, pa, 0x07050301u);
+        }
+    } else {
+        uint32_t uu[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) uu[e] = (uint32_t)(xi[e] + 0x8888) ^ 0x8888u;
+        nibble_transpose(uu, w4);
+    }
+    return amax * (1.0f / kXMax);
+}
+
 // Encodes item u and stores it into LDS. Every lane of the item's quad must
 // run it together (the block maximum and sums move through DPP).
 template <int FMT, bool XF32, bool NORM = false>
 __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageItem<XF32, NORM>& it, uint4* xd,
-                                             float* xbf) {
+                                             float* xbf, const NormIn& nin = NormIn{}, float* ss = nullptr) {
     constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP;
     const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
     const bool live = c * CW + b * 32 < K;
@@ -100,7 +150,26 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
             v[t] = __builtin_bit_cast(float, word(it.raw[0], t));
             v[4 + t] = __builtin_bit_cast(float, word(it.raw[1], t));
         }
-        if constexpr (NORM) {  // rmsnorm's per-column scale; its common factor is applied to the products
+        if constexpr (NORM) {
+            // u = x + delta; its squares for the norm and (workgroup 0) its
+            // copy; then rmsnorm's per-column scale (the common factor is
+            // applied to the products)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[t] += __builtin_bit_cast(float, word(it.dl[0], t));
+                v[4 + t] += __builtin_bit_cast(float, word(it.dl[1], t));
+            }
+            if (c * CW + b * 32 < K) {
+                float s2 = 0.f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) s2 = fmaf(v[k], v[k], s2);
+                *ss += s2;
+                if (nin.x_out) {
+                    float* xo = nin.x_out + (c * CW + b * 32 + q * 8);
+                    *reinterpret_cast<float4*>(xo) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4*>(xo + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                }
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 v[t] *= __builtin_bit_cast(float, word(it.nw[0], t));
@@ -120,44 +189,23 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
     amax = fmaxf(amax, dpp_quad_f32<0xB1>(amax));  // quad_perm [1,0,3,2]
     amax = fmaxf(amax, dpp_quad_f32<0x4E>(amax));  // quad_perm [2,3,0,1]
     if (!live) amax = 0.f;
-    const float inv = amax > 0.f ? kXMax / amax : 0.f;
-    const float s = amax * (1.0f / kXMax);
-    int xi[8];
-    int sum = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int t = (int)__builtin_rintf(v[k] * inv);
-        xi[k] = t < -30583 ? -30583 : (t > 30583 ? 30583 : t);
-        sum += xi[k];
-    }
+    uint32_t w4[4];
+    int sum;
+    const float s = encode_item<FMT>(v, amax, w4, sum);
     uint32_t* xdw = reinterpret_cast<uint32_t*>(xd);
     if constexpr (FMT == Q8_0) {
-        uint32_t lo[2], hi[2];
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            uint32_t uu[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) uu[e] = ((uint32_t)(xi[4 * w + e] + 0x8080) ^ 0x8080u) & 0xffffu;
-            const uint32_t pa = uu[0] | (uu[1] << 16), pb = uu[2] | (uu[3] << 16);
-            lo[w] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
-            hi[w] = __builtin_amdgcn_perm(pb, pa, 0x07050301u);
-        }
         // low-byte words 2q, 2q+1 in parts 0-1, high-byte words in parts 2-3
         const int part = q >> 1, comp = (q & 1) * 2;
         uint32_t* lo_at = xdw + ((m * XP + part) * nch + c) * 4 + comp;
         uint32_t* hi_at = xdw + ((m * XP + 2 + part) * nch + c) * 4 + comp;
-        lo_at[0] = lo[0];
-        lo_at[1] = lo[1];
-        hi_at[0] = hi[0];
-        hi_at[1] = hi[1];
+        lo_at[0] = w4[0];
+        lo_at[1] = w4[1];
+        hi_at[0] = w4[2];
+        hi_at[1] = w4[3];
     } else {
-        uint32_t uu[8], o[4];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) uu[e] = (uint32_t)(xi[e] + 0x8888) ^ 0x8888u;
-        nibble_transpose(uu, o);
         // digit i, word 4b + q of the chunk: part 2i + b, component q
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xdw[((m * XP + 2 * i + b) * nch + c) * 4 + q] = o[i];
+        for (int i = 0; i < 4; ++i) xdw[((m * XP + 2 * i + b) * nch + c) * 4 + q] = w4[i];
     }
     // block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -)
     const int pair = sum + dpp_i32<0xB1>(sum);   // this half block (16 values)
@@ -187,35 +235,36 @@ constexpr int kStageNJ = 4;
 template <int FMT, bool XF32, bool NORM = false>
 __device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x, int64_t ldx, int M, int nthreads,
                                                   StageItem<XF32, NORM> (&it)[kStageNJ],
-                                                  const float* norm_w = nullptr) {
+                                                  const NormIn& nin = NormIn{}) {
     const int total = stage_items<FMT>(nch, M);
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
         const int u = (int)threadIdx.x + j * nthreads;
-        stage_issue<FMT, XF32, NORM>(u < total ? u : (int)threadIdx.x % 4, nch, K, x, ldx, it[j], norm_w);
+        stage_issue<FMT, XF32, NORM>(u < total ? u : (int)threadIdx.x % 4, nch, K, x, ldx, it[j], nin);
     }
 }
 
 template <int FMT, bool XF32, bool NORM = false>
 __device__ __forceinline__ void stage_multi_finish(int nch, int K, int M, int nthreads,
-                                                   const StageItem<XF32, NORM> (&it)[kStageNJ], uint4* xd, float* xbf) {
+                                                   const StageItem<XF32, NORM> (&it)[kStageNJ], uint4* xd, float* xbf,
+                                                   const NormIn& nin = NormIn{}, float* ss = nullptr) {
     const int total = stage_items<FMT>(nch, M);
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
         const int u = (int)threadIdx.x + j * nthreads;
-        if (u < total) stage_finish<FMT, XF32, NORM>(u, nch, K, it[j], xd, xbf);
+        if (u < total) stage_finish<FMT, XF32, NORM>(u, nch, K, it[j], xd, xbf, nin, ss);
     }
 }
 
 // Plain loop (used when a block has more items than kStageNJ per thread).
 template <int FMT, bool XF32, bool NORM = false>
 __device__ __forceinline__ void stage_all(int nch, int K, const void* x, int64_t ldx, int M, int nthreads, uint4* xd,
-                                          float* xbf, const float* norm_w = nullptr) {
+                                          float* xbf, const NormIn& nin = NormIn{}, float* ss = nullptr) {
     const int total = stage_items<FMT>(nch, M);
     for (int u = threadIdx.x; u < total; u += nthreads) {
         StageItem<XF32, NORM> it;
-        stage_issue<FMT, XF32, NORM>(u, nch, K, x, ldx, it, norm_w);
-        stage_finish<FMT, XF32, NORM>(u, nch, K, it, xd, xbf);
+        stage_issue<FMT, XF32, NORM>(u, nch, K, x, ldx, it, nin);
+        stage_finish<FMT, XF32, NORM>(u, nch, K, it, xd, xbf, nin, ss);
     }
 }
 

@@ -66,13 +66,12 @@ class _Lib:
         L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_void_p]
         L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
-        L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
         L.rqmv_rope_table.argtypes = [c_void_p, c_int, c_double, c_int, c_void_p]
         L.rqmv_attention_rope.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                           c_void_p, c_size_t, c_void_p, c_void_p]
         L.rqmv_glu_weight_create.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]
         L.rqmv_matvec_fused.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
-        L.rqmv_residual_parts.argtypes = [c_void_p, POINTER(c_int)]
         L.rqmv_layout_bytes.argtypes = [c_int, c_int64, c_int64, POINTER(c_size_t)]
         L.rqmv_repack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
         L.rqmv_unpack_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p]
@@ -478,19 +477,18 @@ def advance(pos: DeviceBuffer, stream: Stream | None = None):
 
 
 def embed_row(table: DeviceBuffer, rows: int, n: int, token: DeviceBuffer, out: DeviceBuffer,
-              stream: Stream | None = None, parts_out: DeviceBuffer | None = None):
-    _check(lib().lib.rqmv_embed_row(table.ptr, rows, n, token.ptr, out.ptr, parts_out.ptr if parts_out else None,
-                                    _sh(stream)), "rqmv_embed_row")
+              stream: Stream | None = None):
+    _check(lib().lib.rqmv_embed_row(table.ptr, rows, n, token.ptr, out.ptr, _sh(stream)), "rqmv_embed_row")
 
 
 # ------------------------------------------------------- fused products ----
 
-EPI_PLAIN, EPI_GLU, EPI_RESIDUAL = 0, 1, 2
+EPI_PLAIN, EPI_GLU = 0, 1
 
 
 class Fusion(ctypes.Structure):
-    _fields_ = [("norm_weight", c_void_p), ("norm_parts", c_void_p), ("norm_nparts", c_int), ("eps", c_float),
-                ("epilogue", c_int), ("residual", c_void_p), ("parts_out", c_void_p)]
+    _fields_ = [("norm_weight", c_void_p), ("eps", c_float), ("delta", c_void_p), ("x_out", c_void_p),
+                ("epilogue", c_int)]
 
 
 def glu_weight(fmt, rows: int, cols: int, gate: np.ndarray, up: np.ndarray) -> Weight:
@@ -510,17 +508,9 @@ def glu_weight(fmt, rows: int, cols: int, gate: np.ndarray, up: np.ndarray) -> W
     return w
 
 
-def residual_parts(weight: Weight) -> int:
-    n = c_int()
-    _check(lib().lib.rqmv_residual_parts(weight.handle, byref(n)), "rqmv_residual_parts")
-    return n.value
-
-
-def matvec_fused(weight: Weight, x: DeviceBuffer, y: DeviceBuffer | None, epilogue: int = EPI_PLAIN,
-                 norm_weight: DeviceBuffer | None = None, norm_parts: DeviceBuffer | None = None, norm_nparts: int = 0,
-                 eps: float = 0.0, residual: DeviceBuffer | None = None, parts_out: DeviceBuffer | None = None,
-                 stream: Stream | None = None):
-    f = Fusion(norm_weight.ptr if norm_weight else None, norm_parts.ptr if norm_parts else None, norm_nparts, eps,
-               epilogue, residual.ptr if residual else None, parts_out.ptr if parts_out else None)
-    _check(lib().lib.rqmv_matvec_fused(weight.handle, x.ptr, y.ptr if y else None, byref(f), _sh(stream)),
-           "rqmv_matvec_fused")
+def matvec_fused(weight: Weight, x: DeviceBuffer, y: DeviceBuffer, epilogue: int = EPI_PLAIN,
+                 norm_weight: DeviceBuffer | None = None, eps: float = 0.0, delta: DeviceBuffer | None = None,
+                 x_out: DeviceBuffer | None = None, stream: Stream | None = None):
+    f = Fusion(norm_weight.ptr if norm_weight else None, eps, delta.ptr if delta else None,
+               x_out.ptr if x_out else None, epilogue)
+    _check(lib().lib.rqmv_matvec_fused(weight.handle, x.ptr, y.ptr, byref(f), _sh(stream)), "rqmv_matvec_fused")

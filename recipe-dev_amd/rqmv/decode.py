@@ -17,9 +17,10 @@ recipe.rs:23056-23150; lower_normalize, recipe.rs:23190-23210; silu(gate) * up,
 recipe.rs:23279-23286, 22662-22668) run one position at a time. Every
 projection is a quantized matrix-vector product of librqmv, with the norms,
 the SiLU-GLU product and the residual adds folded into the products
-(rqmv_matvec_fused): a residual epilogue leaves per-workgroup partial sums of
-squares of x that the next product's norm prologue adds up; the rotary and the
-cache append are folded into attention (rqmv_attention_rope). Six launches per
+(rqmv_matvec_fused): a product's output is added to the residual stream by the
+next product's prologue, which also takes the sum of squares for its norm and
+writes the updated stream (two buffers, alternating); the rotary and the cache
+append are folded into attention (rqmv_attention_rope). Six launches per
 layer: QKV, attention (two), output, gate/up, down. The residual stream and every activation are fp32; the KV cache is fp16.
 """
 from __future__ import annotations
@@ -28,9 +29,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (EPI_GLU, EPI_PLAIN, EPI_RESIDUAL, DeviceBuffer, Graph, Stream, Weight, advance, argmax,
-               argmax_workspace, attention_rope, attention_workspace, embed_row, glu_weight, matvec_fused,
-               residual_parts, rope_table)
+from . import (EPI_GLU, EPI_PLAIN, DeviceBuffer, Graph, Stream, Weight, advance, argmax, argmax_workspace,
+               attention_rope, attention_workspace, embed_row, glu_weight, matvec_fused, rope_table)
 
 
 @dataclass(frozen=True)
@@ -95,14 +95,12 @@ class DecodeModel:
         self.k_cache = [DeviceBuffer(cache_bytes) for _ in range(s.layers)]
         self.v_cache = [DeviceBuffer(cache_bytes) for _ in range(s.layers)]
         f32 = 4
-        self.x = DeviceBuffer(s.d * f32)
+        self.xs = [DeviceBuffer(s.d * f32), DeviceBuffer(s.d * f32)]  # the residual stream, alternating
         self.qkv = DeviceBuffer(s.qkv_rows * f32)
         self.attn = DeviceBuffer(s.d * f32)
+        self.y_o = DeviceBuffer(s.d * f32)  # output projection, added by the next prologue
         self.h = DeviceBuffer(s.ffn * f32)
-        # partial sums of squares of x: after the embedding or a down
-        # projection (parts_a), after an output projection (parts_b)
-        self.parts_a = DeviceBuffer(1024 * f32)
-        self.parts_b = DeviceBuffer(1024 * f32)
+        self.y_f = DeviceBuffer(s.d * f32)  # down projection, added by the next prologue
         self.logits = DeviceBuffer(s.vocab * f32)
         self.token = DeviceBuffer(4)
         self.pos = DeviceBuffer(4)
@@ -121,9 +119,6 @@ class DecodeModel:
             "gate_up": glu_weight(s.proj_fmt, s.ffn, s.d, t.gate, t.up),
             "down": Weight(s.proj_fmt, s.d, s.ffn, t.down),
         }
-        L = self.layers[index]
-        L["o_parts"] = residual_parts(L["o"])
-        L["down_parts"] = residual_parts(L["down"])
 
     def set_cache(self, index: int, k: np.ndarray, v: np.ndarray):
         """Prefill layer `index`'s cache: k, v are fp16 bits [kv_heads, n, head_dim]
@@ -149,20 +144,26 @@ class DecodeModel:
         s = self.shape
         if any(layer is None for layer in self.layers):
             raise RuntimeError("every layer must be set before a step")
-        embed_row(self.embed, s.vocab, s.d, self.token, self.x, stream, parts_out=self.parts_a)
-        na = 1
+        xs = self.xs
+        embed_row(self.embed, s.vocab, s.d, self.token, xs[0], stream)
+        cur, pending = 0, None  # pending: the down projection not yet added to the stream
         for i, L in enumerate(self.layers):
-            matvec_fused(L["qkv"], self.x, self.qkv, EPI_PLAIN, L["attn_norm"], self.parts_a, na, s.eps, stream=stream)
+            if pending is None:
+                matvec_fused(L["qkv"], xs[cur], self.qkv, EPI_PLAIN, L["attn_norm"], s.eps, stream=stream)
+            else:
+                matvec_fused(L["qkv"], xs[cur], self.qkv, EPI_PLAIN, L["attn_norm"], s.eps, pending, xs[1 - cur],
+                             stream=stream)
+                cur = 1 - cur
             attention_rope(self.qkv, self.rope, self.k_cache[i], self.v_cache[i], self.pos, s.q_heads, s.kv_heads,
                            s.head_dim, self.max_ctx, self.workspace, self.attn, stream)
-            matvec_fused(L["o"], self.attn, None, EPI_RESIDUAL, residual=self.x, parts_out=self.parts_b,
+            matvec_fused(L["o"], self.attn, self.y_o, EPI_PLAIN, stream=stream)
+            matvec_fused(L["gate_up"], xs[cur], self.h, EPI_GLU, L["ffn_norm"], s.eps, self.y_o, xs[1 - cur],
                          stream=stream)
-            matvec_fused(L["gate_up"], self.x, self.h, EPI_GLU, L["ffn_norm"], self.parts_b, L["o_parts"],
-                         s.eps, stream=stream)
-            matvec_fused(L["down"], self.h, None, EPI_RESIDUAL, residual=self.x, parts_out=self.parts_a,
-                         stream=stream)
-            na = L["down_parts"]
-        matvec_fused(self.head, self.x, self.logits, EPI_PLAIN, self.out_norm, self.parts_a, na, s.eps, stream=stream)
+            cur = 1 - cur
+            matvec_fused(L["down"], self.h, self.y_f, EPI_PLAIN, stream=stream)
+            pending = self.y_f
+        matvec_fused(self.head, xs[cur], self.logits, EPI_PLAIN, self.out_norm, s.eps, pending, xs[1 - cur],
+                     stream=stream)
         argmax(self.logits, s.vocab, self.token, self.argmax_ws, stream)
         advance(self.pos, stream)
 

@@ -229,20 +229,28 @@ def _mv_ref(fmt, w, rows, cols, x):
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 6144, 4096), ("q8_0", 4096, 4096), ("q6_k", 512, 1024),
-                                           ("q4_0", 300, 4096)])
-def test_fused_norm_prologue(gpu, fmt, rows, cols):
+                                           ("q4_0", 300, 4096), ("q4_k", 256, 14336)])
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_fused_norm_prologue(gpu, fmt, rows, cols, with_delta):
     w = synth.weights(fmt, rows, cols, seed=rows + cols)
     W = gpu.Weight(fmt, rows, cols, w)
     x = (RNG.standard_normal(cols) * 30).astype(np.float32)
+    d = (RNG.standard_normal(cols) * 5).astype(np.float32)
     nw = (1 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
-    # the partial sums may be split any way: three parts here
-    parts = np.array([np.sum(x[:1000].astype(np.float64) ** 2), np.sum(x[1000:1500].astype(np.float64) ** 2),
-                      np.sum(x[1500:].astype(np.float64) ** 2)], dtype=np.float32)
-    X, NW, P, Y = (gpu.DeviceBuffer.from_array(a) for a in (x, nw, parts, np.zeros(rows, np.float32)))
-    gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, NW, P, 3, 1e-5)
+    X, D, NW, Y = (gpu.DeviceBuffer.from_array(a) for a in (x, d, nw, np.zeros(rows, np.float32)))
+    XO = gpu.DeviceBuffer(4 * cols)
+    if with_delta:
+        gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, NW, 1e-5, D, XO)
+        u = x + d  # one fp32 add, as the kernel takes it
+    else:
+        gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, NW, 1e-5)
+        u = x
     gpu.synchronize()
-    want = _mv_ref(fmt, w, rows, cols, ref.rmsnorm(x, nw, 1e-5))
+    want = _mv_ref(fmt, w, rows, cols, ref.rmsnorm(u, nw, 1e-5))
     assert rel_err(Y.download(np.float32), want) < 1e-3
+    if with_delta:
+        assert np.array_equal(XO.download(np.float32), u)
+    assert np.array_equal(X.download(np.float32), x)  # x itself is not modified
 
 
 @pytest.mark.parametrize("fmt,n,cols", [("q4_k", 14336, 4096), ("q4_k", 512, 256), ("q8_0", 1000, 512)])
@@ -265,55 +273,16 @@ def test_fused_glu_epilogue(gpu, fmt, n, cols):
     assert rel_err(z[1::2], _mv_ref(fmt, u, n, cols, x)) < 1e-3
 
 
-@pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 4096, 14336), ("q4_k", 4096, 4096), ("q6_k", 256, 512)])
-def test_fused_residual_epilogue_and_parts(gpu, fmt, rows, cols):
-    w = synth.weights(fmt, rows, cols, seed=9)
-    W = gpu.Weight(fmt, rows, cols, w)
-    x = RNG.standard_normal(cols).astype(np.float32)
-    r0 = (RNG.standard_normal(rows) * 50).astype(np.float32)
-    n = gpu.residual_parts(W)
-    assert 1 <= n <= 1024
-    X, R, P = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(r0), gpu.DeviceBuffer(4 * n)
-    gpu.matvec_fused(W, X, None, gpu.EPI_RESIDUAL, residual=R, parts_out=P)
-    gpu.synchronize()
-    r1 = R.download(np.float32)
-    delta = _mv_ref(fmt, w, rows, cols, x)
-    assert rel_err(r1.astype(np.float64) - r0, delta) < 1e-3
-    parts = P.download(np.float32, n)
-    assert abs(float(np.sum(parts, dtype=np.float64)) - float(np.sum(r1.astype(np.float64) ** 2))) \
-        <= 1e-5 * float(np.sum(r1.astype(np.float64) ** 2))
-    # the parts feed a following norm prologue exactly as a full sum would
-    w2 = synth.weights("q4_k", 512, rows, seed=10)
-    W2 = gpu.Weight("q4_k", 512, rows, w2)
-    nw = np.ones(rows, np.float32)
-    NW, Y = gpu.DeviceBuffer.from_array(nw), gpu.DeviceBuffer(4 * 512)
-    gpu.matvec_fused(W2, R, Y, gpu.EPI_PLAIN, NW, P, n, 1e-5)
-    gpu.synchronize()
-    assert rel_err(Y.download(np.float32), _mv_ref("q4_k", w2, 512, rows, ref.rmsnorm(r1, nw, 1e-5))) < 1e-3
-
-
-def test_embed_row_parts(gpu):
-    rows, n = 7, 4096
-    table = RNG.standard_normal((rows, n)).astype(np.float32)
-    T, O, P = gpu.DeviceBuffer.from_array(table), gpu.DeviceBuffer(4 * n), gpu.DeviceBuffer(4)
-    gpu.embed_row(T, rows, n, _i32(gpu, 3), O, parts_out=P)
-    gpu.synchronize()
-    assert np.array_equal(O.download(np.float32), table[3])
-    want = float(np.sum(table[3].astype(np.float64) ** 2))
-    assert abs(float(P.download(np.float32, 1)[0]) - want) <= 1e-5 * want
-
-
 def test_fused_rejects_bad_arguments(gpu):
     w = synth.weights("q4_k", 64, 256, seed=1)
     W = gpu.Weight("q4_k", 64, 256, w)
-    X, Y = gpu.DeviceBuffer(4 * 256), gpu.DeviceBuffer(4 * 64)
+    X, Y, D = gpu.DeviceBuffer(4 * 256), gpu.DeviceBuffer(4 * 64), gpu.DeviceBuffer(4 * 256)
     with pytest.raises(gpu.RqmvError):
         gpu.matvec_fused(W, X, Y, gpu.EPI_GLU)  # not a pair weight
     with pytest.raises(gpu.RqmvError):
-        gpu.matvec_fused(W, X, None, gpu.EPI_RESIDUAL)  # no residual
-    P = gpu.DeviceBuffer(4 * 2048)
+        gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, delta=D)  # a delta without the norm
     with pytest.raises(gpu.RqmvError):
-        gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, X, P, 2000, 1e-5)  # too many parts
+        gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, D, 1e-5, D, X)  # x_out over x
 
 
 @pytest.mark.parametrize("nq,nkv,hd", [(32, 8, 128), (4, 2, 64), (8, 1, 256)])
