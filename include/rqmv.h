@@ -229,6 +229,37 @@ int rqmv_matvec_fused(const rqmv_weight* weight, const float* x_dev, float* y_de
 /* *pos += 1 on the device (the last launch of a captured decode step). */
 int rqmv_advance(int* pos, void* stream);
 
+/* GGUF v3 files (recipe's mod gguf, recipe.rs:9783-10327; Gguf::open 10069,
+ * tensor / value / data 10141-10174). The file is mapped read-only; a split
+ * model (<prefix>-<n>-of-<count>.gguf with split.count) is opened whole from
+ * its first shard. Names and strings returned stay valid until
+ * rqmv_gguf_close. Shapes are in GGML order: dims[0] is the row width. None
+ * of these touch a device except rqmv_gguf_weight_create. */
+typedef struct rqmv_gguf rqmv_gguf;
+int rqmv_gguf_open(const char* path, rqmv_gguf** out);
+int rqmv_gguf_close(rqmv_gguf* file);
+int rqmv_gguf_tensor_count(const rqmv_gguf* file, int64_t* count);
+/* dims holds up to 8 entries. */
+int rqmv_gguf_tensor_info(const rqmv_gguf* file, int64_t index, const char** name, int* ggml_type, int* n_dims,
+                          int64_t* dims, size_t* nbytes);
+int rqmv_gguf_find_tensor(const rqmv_gguf* file, const char* name, int64_t* index);
+/* The tensor's bytes in the mapped file, in its GGML block layout. */
+int rqmv_gguf_tensor_data(const rqmv_gguf* file, int64_t index, const void** data, size_t* nbytes);
+int rqmv_gguf_metadata_count(const rqmv_gguf* file, int64_t* count);
+/* Key `index` (file order) and its GGUF value type (0..12). */
+int rqmv_gguf_metadata_key(const rqmv_gguf* file, int64_t index, const char** key, int* value_type);
+/* A nonnegative integer of any width (GgufValue::integer), a float (F32 or
+ * F64), a string; arrays by element. */
+int rqmv_gguf_get_int(const rqmv_gguf* file, const char* key, int64_t* out);
+int rqmv_gguf_get_float(const rqmv_gguf* file, const char* key, double* out);
+int rqmv_gguf_get_string(const rqmv_gguf* file, const char* key, const char** out);
+int rqmv_gguf_get_array(const rqmv_gguf* file, const char* key, int* element_type, int64_t* count);
+int rqmv_gguf_get_array_int(const rqmv_gguf* file, const char* key, int64_t index, int64_t* out);
+int rqmv_gguf_get_array_string(const rqmv_gguf* file, const char* key, int64_t index, const char** out);
+/* A device weight from a named tensor, straight from the mapped bytes: [k, n]
+ * is n rows of k, [k, n, experts] an expert bank (recipe.rs:18286-18292). */
+int rqmv_gguf_weight_create(const rqmv_gguf* file, const char* name, rqmv_weight** out);
+
 /* Host-only loader functions (no device needed): the repacked layout's size
  * and the repack / unpack themselves, for inspection and testing. */
 int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* bytes);

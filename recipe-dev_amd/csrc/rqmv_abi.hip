@@ -1,6 +1,7 @@
 // C-ABI entry points of librqmv (declared in include/rqmv.h).
 #include <stdlib.h>
 
+#include <memory>
 #include <mutex>
 #include <cstring>
 #include <string>
@@ -9,6 +10,7 @@
 #include "../../include/rqmv.h"
 #include "kernels.h"
 #include "decode.h"
+#include "gguf.h"
 #include "moe.h"
 #include "repack.h"
 
@@ -23,6 +25,10 @@ struct rqmv_weight {
     size_t dev_bytes;
     int device;
     bool glu = false;  // rows are (gate, up) pairs (rqmv_glu_weight_create)
+};
+
+struct rqmv_gguf {
+    std::unique_ptr<rq::GgufFile> file;
 };
 
 namespace {
@@ -576,6 +582,178 @@ int rqmv_advance(int* pos, void* stream) {
     if (!pos) return fail(RQMV_EINVAL, "advance: NULL position");
     hipError_t e = rq::launch_advance(pos, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "advance launch");
+}
+
+// ------------------------------------------------------------ GGUF files ----
+
+int rqmv_gguf_open(const char* path, rqmv_gguf** out) {
+    if (!path || !out) return fail(RQMV_EINVAL, "gguf_open: NULL argument");
+    *out = nullptr;
+    std::string error;
+    std::unique_ptr<rq::GgufFile> f = rq::gguf_open(path, &error);
+    if (!f) return fail(RQMV_EINVAL, error);
+    rqmv_gguf* g = new rqmv_gguf;
+    g->file = std::move(f);
+    *out = g;
+    return RQMV_OK;
+}
+
+int rqmv_gguf_close(rqmv_gguf* g) {
+    delete g;
+    return RQMV_OK;
+}
+
+int rqmv_gguf_tensor_count(const rqmv_gguf* g, int64_t* count) {
+    if (!g || !count) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    *count = (int64_t)g->file->tensors.size();
+    return RQMV_OK;
+}
+
+int rqmv_gguf_tensor_info(const rqmv_gguf* g, int64_t index, const char** name, int* ggml_type, int* n_dims,
+                          int64_t* dims, size_t* nbytes) {
+    if (!g) return fail(RQMV_EINVAL, "gguf: NULL handle");
+    if (index < 0 || index >= (int64_t)g->file->tensors.size()) return fail(RQMV_EINVAL, "gguf: tensor index out of range");
+    const rq::GgufTensor& t = g->file->tensors[(size_t)index];
+    if (name) *name = t.name.c_str();
+    if (ggml_type) *ggml_type = (int)t.type;
+    if (n_dims) *n_dims = (int)t.shape.size();
+    if (dims)
+        for (size_t d = 0; d < t.shape.size(); ++d) dims[d] = (int64_t)t.shape[d];
+    if (nbytes) *nbytes = (size_t)t.bytes;
+    return RQMV_OK;
+}
+
+int rqmv_gguf_find_tensor(const rqmv_gguf* g, const char* name, int64_t* index) {
+    if (!g || !name || !index) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    for (size_t k = 0; k < g->file->tensors.size(); ++k)
+        if (g->file->tensors[k].name == name) {
+            *index = (int64_t)k;
+            return RQMV_OK;
+        }
+    return fail(RQMV_EINVAL, std::string("tensor ") + name + " is absent");
+}
+
+int rqmv_gguf_tensor_data(const rqmv_gguf* g, int64_t index, const void** data, size_t* nbytes) {
+    if (!g || !data) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    if (index < 0 || index >= (int64_t)g->file->tensors.size()) return fail(RQMV_EINVAL, "gguf: tensor index out of range");
+    const rq::GgufTensor& t = g->file->tensors[(size_t)index];
+    *data = g->file->bytes(t);
+    if (nbytes) *nbytes = (size_t)t.bytes;
+    return RQMV_OK;
+}
+
+int rqmv_gguf_metadata_count(const rqmv_gguf* g, int64_t* count) {
+    if (!g || !count) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    *count = (int64_t)g->file->metadata.size();
+    return RQMV_OK;
+}
+
+int rqmv_gguf_metadata_key(const rqmv_gguf* g, int64_t index, const char** key, int* value_type) {
+    if (!g || !key) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    if (index < 0 || index >= (int64_t)g->file->metadata.size()) return fail(RQMV_EINVAL, "gguf: key index out of range");
+    *key = g->file->metadata[(size_t)index].first.c_str();
+    if (value_type) *value_type = (int)g->file->metadata[(size_t)index].second.type;
+    return RQMV_OK;
+}
+
+namespace {
+const rq::GgufValue* gguf_value(const rqmv_gguf* g, const char* key, int* rc) {
+    if (!g || !key) {
+        *rc = fail(RQMV_EINVAL, "gguf: NULL argument");
+        return nullptr;
+    }
+    const rq::GgufValue* v = g->file->value(key);
+    if (!v) *rc = fail(RQMV_EINVAL, std::string(key) + " is absent");
+    return v;
+}
+const rq::GgufValue* gguf_element(const rqmv_gguf* g, const char* key, int64_t index, int* rc) {
+    const rq::GgufValue* v = gguf_value(g, key, rc);
+    if (!v) return nullptr;
+    if (v->type != 9) {
+        *rc = fail(RQMV_EINVAL, std::string(key) + " is not an array");
+        return nullptr;
+    }
+    if (index < 0 || index >= (int64_t)v->array.size()) {
+        *rc = fail(RQMV_EINVAL, std::string(key) + ": index out of range");
+        return nullptr;
+    }
+    return &v->array[(size_t)index];
+}
+int int_of(const rq::GgufValue* v, const char* key, int64_t* out) {
+    uint64_t u;
+    if (!v->integer(&u) || u > (uint64_t)INT64_MAX)
+        return fail(RQMV_EINVAL, std::string(key) + " is not a nonnegative integer");
+    *out = (int64_t)u;
+    return RQMV_OK;
+}
+}  // namespace
+
+int rqmv_gguf_get_int(const rqmv_gguf* g, const char* key, int64_t* out) {
+    int rc = RQMV_OK;
+    const rq::GgufValue* v = gguf_value(g, key, &rc);
+    if (!v) return rc;
+    if (!out) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    return int_of(v, key, out);
+}
+
+int rqmv_gguf_get_float(const rqmv_gguf* g, const char* key, double* out) {
+    int rc = RQMV_OK;
+    const rq::GgufValue* v = gguf_value(g, key, &rc);
+    if (!v) return rc;
+    if (!out || !v->real(out)) return fail(RQMV_EINVAL, std::string(key) + " is not a float");
+    return RQMV_OK;
+}
+
+int rqmv_gguf_get_string(const rqmv_gguf* g, const char* key, const char** out) {
+    int rc = RQMV_OK;
+    const rq::GgufValue* v = gguf_value(g, key, &rc);
+    if (!v) return rc;
+    if (!out || v->type != 8) return fail(RQMV_EINVAL, std::string(key) + " is not a string");
+    *out = v->s.c_str();
+    return RQMV_OK;
+}
+
+int rqmv_gguf_get_array(const rqmv_gguf* g, const char* key, int* element_type, int64_t* count) {
+    int rc = RQMV_OK;
+    const rq::GgufValue* v = gguf_value(g, key, &rc);
+    if (!v) return rc;
+    if (v->type != 9) return fail(RQMV_EINVAL, std::string(key) + " is not an array");
+    if (element_type) *element_type = (int)v->array_type;
+    if (count) *count = (int64_t)v->array.size();
+    return RQMV_OK;
+}
+
+int rqmv_gguf_get_array_int(const rqmv_gguf* g, const char* key, int64_t index, int64_t* out) {
+    int rc = RQMV_OK;
+    const rq::GgufValue* v = gguf_element(g, key, index, &rc);
+    if (!v) return rc;
+    if (!out) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    return int_of(v, key, out);
+}
+
+int rqmv_gguf_get_array_string(const rqmv_gguf* g, const char* key, int64_t index, const char** out) {
+    int rc = RQMV_OK;
+    const rq::GgufValue* v = gguf_element(g, key, index, &rc);
+    if (!v) return rc;
+    if (!out || v->type != 8) return fail(RQMV_EINVAL, std::string(key) + ": element is not a string");
+    *out = v->s.c_str();
+    return RQMV_OK;
+}
+
+int rqmv_gguf_weight_create(const rqmv_gguf* g, const char* name, rqmv_weight** out) {
+    if (!g || !name || !out) return fail(RQMV_EINVAL, "gguf: NULL argument");
+    const rq::GgufTensor* t = g->file->tensor(name);
+    if (!t) return fail(RQMV_EINVAL, std::string("tensor ") + name + " is absent");
+    if (t->type != rq::F16 && t->type != rq::Q4_0 && t->type != rq::Q8_0 && t->type != rq::Q4_K && t->type != rq::Q6_K)
+        return fail(RQMV_EINVAL, "tensor " + t->name + " has GGML type " + std::to_string(t->type) +
+                                     "; the library takes F16, Q4_0, Q8_0, Q4_K and Q6_K");
+    // GGML order: shape[0] is the row width (cols), shape[1] the rows, shape[2] the experts
+    const size_t nd = t->shape.size();
+    if (nd < 1 || nd > 3) return fail(RQMV_EINVAL, "tensor " + t->name + " must have 1 to 3 dimensions");
+    const int64_t cols = (int64_t)t->shape[0];
+    const int64_t rows = nd >= 2 ? (int64_t)t->shape[1] : 1;
+    const int64_t experts = nd == 3 ? (int64_t)t->shape[2] : 1;
+    return create((int)t->type, experts, rows, cols, g->file->bytes(*t), (size_t)t->bytes, out);
 }
 
 int rqmv_layout_bytes(int format, int64_t rows, int64_t cols, size_t* bytes) {

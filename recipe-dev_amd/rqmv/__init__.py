@@ -67,6 +67,22 @@ class _Lib:
         L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
         L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
+        L.rqmv_gguf_open.argtypes = [c_char_p, c_void_p]
+        L.rqmv_gguf_close.argtypes = [c_void_p]
+        L.rqmv_gguf_tensor_count.argtypes = [c_void_p, POINTER(c_int64)]
+        L.rqmv_gguf_tensor_info.argtypes = [c_void_p, c_int64, POINTER(c_char_p), POINTER(c_int), POINTER(c_int),
+                                            POINTER(c_int64), POINTER(c_size_t)]
+        L.rqmv_gguf_find_tensor.argtypes = [c_void_p, c_char_p, POINTER(c_int64)]
+        L.rqmv_gguf_tensor_data.argtypes = [c_void_p, c_int64, POINTER(c_void_p), POINTER(c_size_t)]
+        L.rqmv_gguf_metadata_count.argtypes = [c_void_p, POINTER(c_int64)]
+        L.rqmv_gguf_metadata_key.argtypes = [c_void_p, c_int64, POINTER(c_char_p), POINTER(c_int)]
+        L.rqmv_gguf_get_int.argtypes = [c_void_p, c_char_p, POINTER(c_int64)]
+        L.rqmv_gguf_get_float.argtypes = [c_void_p, c_char_p, POINTER(c_double)]
+        L.rqmv_gguf_get_string.argtypes = [c_void_p, c_char_p, POINTER(c_char_p)]
+        L.rqmv_gguf_get_array.argtypes = [c_void_p, c_char_p, POINTER(c_int), POINTER(c_int64)]
+        L.rqmv_gguf_get_array_int.argtypes = [c_void_p, c_char_p, c_int64, POINTER(c_int64)]
+        L.rqmv_gguf_get_array_string.argtypes = [c_void_p, c_char_p, c_int64, POINTER(c_char_p)]
+        L.rqmv_gguf_weight_create.argtypes = [c_void_p, c_char_p, c_void_p]
         L.rqmv_rope_table.argtypes = [c_void_p, c_int, c_double, c_int, c_void_p]
         L.rqmv_attention_rope.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                           c_void_p, c_size_t, c_void_p, c_void_p]
@@ -514,3 +530,117 @@ def matvec_fused(weight: Weight, x: DeviceBuffer, y: DeviceBuffer, epilogue: int
     f = Fusion(norm_weight.ptr if norm_weight else None, eps, delta.ptr if delta else None,
                x_out.ptr if x_out else None, epilogue)
     _check(lib().lib.rqmv_matvec_fused(weight.handle, x.ptr, y.ptr, byref(f), _sh(stream)), "rqmv_matvec_fused")
+
+
+# ------------------------------------------------------------ GGUF files ----
+
+GGUF_ARRAY = 9
+
+
+class GgufTensorInfo:
+    def __init__(self, name: str, ggml_type: int, shape: tuple, nbytes: int, index: int):
+        self.name, self.ggml_type, self.shape, self.nbytes, self.index = name, ggml_type, shape, nbytes, index
+
+    def __repr__(self):
+        return f"GgufTensorInfo({self.name!r}, type={self.ggml_type}, shape={self.shape}, nbytes={self.nbytes})"
+
+
+class Gguf:
+    """A GGUF v3 file (or split model) opened by librqmv's reader (Gguf::open,
+    recipe.rs:10069): metadata, tensor descriptors, mapped tensor bytes and
+    device weights by tensor name."""
+
+    def __init__(self, path: str):
+        h = c_void_p()
+        _check(lib().lib.rqmv_gguf_open(os.fsencode(path), byref(h)), "rqmv_gguf_open")
+        self.handle = h.value
+        n = c_int64()
+        _check(lib().lib.rqmv_gguf_tensor_count(self.handle, byref(n)), "rqmv_gguf_tensor_count")
+        self._tensors = []
+        for i in range(n.value):
+            name, ty, nd, nb = c_char_p(), c_int(), c_int(), c_size_t()
+            dims = (c_int64 * 8)()
+            _check(lib().lib.rqmv_gguf_tensor_info(self.handle, i, byref(name), byref(ty), byref(nd), dims, byref(nb)),
+                   "rqmv_gguf_tensor_info")
+            self._tensors.append(GgufTensorInfo(name.value.decode(), ty.value, tuple(dims[:nd.value]), nb.value, i))
+        self._by_name = {t.name: t for t in self._tensors}
+
+    def tensors(self) -> list:
+        return list(self._tensors)
+
+    def tensor(self, name: str) -> GgufTensorInfo | None:
+        return self._by_name.get(name)
+
+    def data(self, name: str) -> np.ndarray:
+        """The tensor's bytes as stored (a copy out of the mapping)."""
+        t = self._by_name[name]
+        p, nb = c_void_p(), c_size_t()
+        _check(lib().lib.rqmv_gguf_tensor_data(self.handle, t.index, byref(p), byref(nb)), "rqmv_gguf_tensor_data")
+        return np.ctypeslib.as_array((ctypes.c_uint8 * nb.value).from_address(p.value)).copy()
+
+    def keys(self) -> list:
+        n = c_int64()
+        _check(lib().lib.rqmv_gguf_metadata_count(self.handle, byref(n)), "rqmv_gguf_metadata_count")
+        out = []
+        for i in range(n.value):
+            k, ty = c_char_p(), c_int()
+            _check(lib().lib.rqmv_gguf_metadata_key(self.handle, i, byref(k), byref(ty)), "rqmv_gguf_metadata_key")
+            out.append((k.value.decode(), ty.value))
+        return out
+
+    def get_int(self, key: str) -> int:
+        v = c_int64()
+        _check(lib().lib.rqmv_gguf_get_int(self.handle, key.encode(), byref(v)), "rqmv_gguf_get_int")
+        return v.value
+
+    def get_float(self, key: str) -> float:
+        v = c_double()
+        _check(lib().lib.rqmv_gguf_get_float(self.handle, key.encode(), byref(v)), "rqmv_gguf_get_float")
+        return v.value
+
+    def get_string(self, key: str) -> str:
+        v = c_char_p()
+        _check(lib().lib.rqmv_gguf_get_string(self.handle, key.encode(), byref(v)), "rqmv_gguf_get_string")
+        return v.value.decode()
+
+    def get_array(self, key: str) -> list:
+        ty, n = c_int(), c_int64()
+        _check(lib().lib.rqmv_gguf_get_array(self.handle, key.encode(), byref(ty), byref(n)), "rqmv_gguf_get_array")
+        out = []
+        for i in range(n.value):
+            if ty.value == 8:
+                v = c_char_p()
+                _check(lib().lib.rqmv_gguf_get_array_string(self.handle, key.encode(), i, byref(v)), "array")
+                out.append(v.value.decode())
+            else:
+                v = c_int64()
+                _check(lib().lib.rqmv_gguf_get_array_int(self.handle, key.encode(), i, byref(v)), "array")
+                out.append(v.value)
+        return out
+
+    def weight(self, name: str) -> Weight:
+        """A device weight straight from the mapped tensor ([k, n]: n rows of k;
+        [k, n, experts]: an expert bank)."""
+        t = self._by_name.get(name)
+        h = c_void_p()
+        _check(lib().lib.rqmv_gguf_weight_create(self.handle, name.encode(), byref(h)), "rqmv_gguf_weight_create")
+        w = Weight.__new__(Weight)
+        w.handle = h.value
+        w.fmt = t.ggml_type
+        w.cols = t.shape[0]
+        w.rows = t.shape[1] if len(t.shape) > 1 else 1
+        w.experts = t.shape[2] if len(t.shape) > 2 else 1
+        w.gguf_nbytes = t.nbytes
+        w.glu = False
+        return w
+
+    def close(self):
+        if self.handle:
+            lib().lib.rqmv_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -186,3 +186,87 @@ class DecodeModel:
         for L in self.layers:
             total += sum(L[k].gguf_nbytes for k in ("qkv", "o", "gate_up", "down"))
         return total
+
+
+# ------------------------------------------------------------- from GGUF ----
+
+_GGML_FORMAT = {2: "q4_0", 8: "q8_0", 12: "q4_k", 14: "q6_k"}
+
+
+def _f32_vector(g, name: str) -> np.ndarray:
+    t = g.tensor(name)
+    if t is None:
+        raise ValueError(f"{name} is absent")
+    raw = g.data(name)
+    if t.ggml_type == 0:
+        return raw.view(np.float32).copy()
+    if t.ggml_type == 1:
+        return raw.view(np.float16).astype(np.float32)
+    raise ValueError(f"{name} must be F32 or F16, not GGML type {t.ggml_type}")
+
+
+def from_gguf(path: str, max_ctx: int) -> DecodeModel:
+    """A DecodeModel from a llama-style GGUF file, with recipe's tensor names
+    (token_embd, blk.N.attn_norm / attn_q / attn_k / attn_v or attn_qkv /
+    attn_output / ffn_norm / ffn_gate / ffn_up / ffn_down, output_norm,
+    output; recipe.rs:14382-14457, 17798-17860) and hyperparameters
+    (<arch>.block_count, embedding_length, attention.head_count(_kv),
+    feed_forward_length, rope.freq_base (default 10000),
+    attention.layer_norm_rms_epsilon (default 1e-5); recipe.rs:17806-17936).
+    Separate Q, K and V projections are stacked into one QKV weight, gate and
+    up become one pair weight; blocks are uploaded from the mapped file."""
+    from . import Gguf
+
+    g = Gguf(path)
+    arch = g.get_string("general.architecture")
+
+    def meta_int(key):
+        return g.get_int(f"{arch}.{key}")
+
+    def meta_float(key, default):
+        try:
+            return g.get_float(f"{arch}.{key}")
+        except Exception:
+            return default
+
+    layers = meta_int("block_count")
+    d = meta_int("embedding_length")
+    nq = meta_int("attention.head_count")
+    try:
+        nkv = meta_int("attention.head_count_kv")
+    except Exception:
+        nkv = nq
+    ffn = meta_int("feed_forward_length")
+    embed_info = g.tensor("token_embd.weight")
+    if embed_info is None or embed_info.shape[0] != d:
+        raise ValueError("token_embd.weight must be [embedding_length, vocabulary]")
+    vocab = embed_info.shape[1]
+    head_info = g.tensor("output.weight")
+    if head_info is None:
+        raise ValueError("output.weight is absent")
+    q0 = g.tensor("blk.0.attn_qkv.weight") or g.tensor("blk.0.attn_q.weight")
+    if q0 is None or q0.ggml_type not in _GGML_FORMAT or head_info.ggml_type not in _GGML_FORMAT:
+        raise ValueError("projections and the head must be Q4_0, Q8_0, Q4_K or Q6_K")
+    shape = DecoderShape(layers=layers, d=d, q_heads=nq, kv_heads=nkv, head_dim=d // nq, ffn=ffn, vocab=vocab,
+                         rope_base=meta_float("rope.freq_base", 10000.0),
+                         eps=meta_float("attention.layer_norm_rms_epsilon", 1e-5),
+                         proj_fmt=_GGML_FORMAT[q0.ggml_type], head_fmt=_GGML_FORMAT[head_info.ggml_type])
+    if embed_info.ggml_type == 0:
+        embed = g.data("token_embd.weight").view(np.float32).reshape(vocab, d)
+    elif embed_info.ggml_type == 1:
+        embed = g.data("token_embd.weight").view(np.float16).astype(np.float32).reshape(vocab, d)
+    else:
+        raise ValueError("token_embd.weight must be F32 or F16")
+    model = DecodeModel(shape, max_ctx, embed, _f32_vector(g, "output_norm.weight"), g.data("output.weight"))
+    for i in range(layers):
+        p = f"blk.{i}."
+        if g.tensor(p + "attn_qkv.weight") is not None:
+            qkv = g.data(p + "attn_qkv.weight")
+        else:
+            qkv = np.concatenate([g.data(p + "attn_q.weight"), g.data(p + "attn_k.weight"), g.data(p + "attn_v.weight")])
+        model.set_layer(i, LayerTensors(attn_norm=_f32_vector(g, p + "attn_norm.weight"), qkv=qkv,
+                                        o=g.data(p + "attn_output.weight"), ffn_norm=_f32_vector(g, p + "ffn_norm.weight"),
+                                        gate=g.data(p + "ffn_gate.weight"), up=g.data(p + "ffn_up.weight"),
+                                        down=g.data(p + "ffn_down.weight")))
+    g.close()
+    return model

@@ -332,3 +332,82 @@ def test_rope_table_matches_rope_kv(gpu):
         ang = p * np.exp(-(2.0 * i / hd) * np.log(base))
         assert np.array_equal(t[p, :, 0], np.cos(ang).astype(np.float32))
         assert np.array_equal(t[p, :, 1], np.sin(ang).astype(np.float32))
+
+
+# ------------------------------------------------------------------ GGUF ----
+
+def _write_llama_gguf(path, shape, D, layers_t, head, embed):
+    import gguf_writer as gw
+    from rqmv.decode import DecoderShape  # noqa: F401
+    gt = {"q4_0": 2, "q8_0": 8, "q4_k": 12, "q6_k": 14}
+    s = shape
+    qkv_rows = s.qkv_rows
+    meta = [("general.architecture", gw.STRING, "llama"), ("llama.block_count", gw.U32, s.layers),
+            ("llama.embedding_length", gw.U32, s.d), ("llama.attention.head_count", gw.U32, s.q_heads),
+            ("llama.attention.head_count_kv", gw.U32, s.kv_heads), ("llama.feed_forward_length", gw.U32, s.ffn),
+            ("llama.rope.freq_base", gw.F32, s.rope_base), ("llama.attention.layer_norm_rms_epsilon", gw.F32, s.eps)]
+    tensors = [("token_embd.weight", [s.d, s.vocab], 0, embed.astype(np.float32).tobytes())]
+    pf = gt[s.proj_fmt]
+    for i, t in enumerate(layers_t):
+        rb = t.qkv.nbytes // qkv_rows
+        nq, nk = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
+        q, k, v = t.qkv[:nq * rb], t.qkv[nq * rb:(nq + nk) * rb], t.qkv[(nq + nk) * rb:]
+        p = f"blk.{i}."
+        tensors += [(p + "attn_norm.weight", [s.d], 0, t.attn_norm.astype(np.float32).tobytes()),
+                    (p + "attn_q.weight", [s.d, nq], pf, q.tobytes()),
+                    (p + "attn_k.weight", [s.d, nk], pf, k.tobytes()),
+                    (p + "attn_v.weight", [s.d, nk], pf, v.tobytes()),
+                    (p + "attn_output.weight", [s.d, s.d], pf, t.o.tobytes()),
+                    (p + "ffn_norm.weight", [s.d], 0, t.ffn_norm.astype(np.float32).tobytes()),
+                    (p + "ffn_gate.weight", [s.d, s.ffn], pf, t.gate.tobytes()),
+                    (p + "ffn_up.weight", [s.d, s.ffn], pf, t.up.tobytes()),
+                    (p + "ffn_down.weight", [s.ffn, s.d], pf, t.down.tobytes())]
+    tensors += [("output_norm.weight", [s.d], 0, D.out_norm().astype(np.float32).tobytes()),
+                ("output.weight", [s.d, s.vocab], gt[s.head_fmt], head.tobytes())]
+    gw.write(path, meta, tensors)
+
+
+def test_decode_from_gguf_matches_reference(gpu, tmp_path):
+    from rqmv.decode import from_gguf
+    shape = DecoderShape(layers=2, d=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=384)
+    D = synth.DecoderSynth(shape, seed=8, norm_std=0.1)
+    layers = [D.layer(i) for i in range(shape.layers)]
+    head, embed = D.head(), D.embed()
+    path = str(tmp_path / "tiny-llama.gguf")
+    _write_llama_gguf(path, shape, D, layers, head, embed)
+    max_ctx = 8
+    model = from_gguf(path, max_ctx)
+    assert model.shape.proj_fmt == "q4_k" and model.shape.kv_heads == 2 and model.shape.vocab == 384
+    R = ref.DecoderReference(shape, embed, D.out_norm(), head, layers,
+                             [(np.zeros((2, 0, 64), np.uint16), np.zeros((2, 0, 64), np.uint16))] * 2, max_ctx)
+    stream = gpu.Stream()
+    model.set_position(5, 0)
+    token, pos = 5, 0
+    for _ in range(3):  # a fresh sequence from position 0
+        model.enqueue_step(stream)
+        stream.synchronize()
+        logits = model.read_logits()
+        assert rel_err(logits, R.step(token, pos)) < 1e-3
+        token, pos = model.read_token(), pos + 1
+    stream.close()
+
+
+def test_gguf_weight_matches_bytes(gpu, tmp_path):
+    import gguf_writer as gw
+    path = str(tmp_path / "w.gguf")
+    w = synth.q6_k(48, 1024, seed=3)
+    bank = synth.q4_k(3 * 64, 512, seed=4)
+    gw.write(path, [], [("blk.0.ffn_down.weight", [1024, 48], 14, w.tobytes()),
+                        ("blk.0.ffn_up_exps.weight", [512, 64, 3], 12, bank.tobytes())])
+    g = gpu.Gguf(path)
+    W = g.weight("blk.0.ffn_down.weight")
+    assert W.info()["rows"] == 48 and W.info()["cols"] == 1024
+    assert np.array_equal(W.unpack(), w)
+    B = g.weight("blk.0.ffn_up_exps.weight")
+    assert B.info()["experts"] == 3 and B.info()["rows"] == 64
+    assert np.array_equal(B.unpack(), bank)
+    x = RNG.standard_normal(1024).astype(np.float32)
+    import oracle
+    assert rel_err(gpu.contract(W, x), oracle.matvec_f64("q6_k", w, 48, 1024, x)[0]) < 1e-3
+    with pytest.raises(gpu.RqmvError):
+        g.weight("absent")
