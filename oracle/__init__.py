@@ -49,6 +49,8 @@ def lib():
                                   c_void_p, c_void_p]
         L.orc_q4k_q81_reference.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
         L.orc_q4k_xorshift_rows.argtypes = [c_uint32, c_int64, c_uint16, c_void_p]
+        L.orc_q8_records.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_void_p]
+        L.orc_int8_matvec.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int, c_int, c_void_p]
         _lib = L
     return _lib
 
@@ -149,3 +151,25 @@ def q4k_xorshift_rows(seed: int, rows: int, scale_bits: int) -> np.ndarray:
     out = np.empty(rows * 16 * 144, np.uint8)
     lib().orc_q4k_xorshift_rows(seed, rows, scale_bits, out.ctypes.data)
     return out
+
+
+def q8_records(x: np.ndarray, step: int):
+    """recipe's int(8) activation records of one position: (d float32 (K/32,), codes int8 (K,))."""
+    xs = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    d = np.empty(xs.size // 32, np.float32)
+    codes = np.empty(xs.size, np.int8)
+    rc = lib().orc_q8_records(xs.ctypes.data, xs.size, step, d.ctypes.data, codes.ctypes.data)
+    assert rc == 0, rc
+    return d, codes
+
+
+def int8_matvec(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray, step: int = 32,
+                tail: bool = False) -> np.ndarray:
+    """recipe's int(8) sum over GGUF block rows: x (M, cols) float32 -> y (M, rows) float32."""
+    g = _as_bytes(gguf)
+    xs = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+    y = np.empty((xs.shape[0], rows), np.float32)
+    rc = lib().orc_int8_matvec(_fmt(fmt), g.ctypes.data, rows, cols, xs.ctypes.data, xs.shape[0], step,
+                               1 if tail else 0, y.ctypes.data)
+    assert rc == 0, rc
+    return y

@@ -476,3 +476,276 @@ void orc_q4k_xorshift_rows(uint32_t seed, int64_t rows, uint16_t scale_bits, uin
         }
     }
 }
+
+/* ---- recipe's int(8) sum ---------------------------------------------------
+ * Restated from amd-nv-cpu.ll (contraction_forward_gemv_wave_body, 1231-2241)
+ * and the slice helpers build.rs:743-915, with recipe's 32 GPU lanes kept as
+ * arrays. fp32 throughout; the Makefile builds without contraction, so every
+ * product and sum below rounds on its own, and fmaf is the state's madd. */
+
+#define ORC_LANES 32
+
+/* amd-nv-cpu.ll:1469-1470: the partner replaces the lane's extreme when its
+ * magnitude is larger, or equal with a larger signed value. */
+static int q8_partner_wins(float partner, float own) {
+    const float ap = fabsf(partner), ao = fabsf(own);
+    return ap > ao || (ap == ao && partner > own);
+}
+
+/* amd-nv-cpu.ll:1408-1500. */
+int orc_q8_records(const float* x, int64_t k, int step, float* d, int8_t* codes) {
+    if (k <= 0 || k % 32 != 0 || (step != 32 && step != 256)) return -1;
+    const int64_t blocks = k / 32, span = step / 32;
+    for (int64_t g0 = 0; g0 < blocks; g0 += span) {
+        const int64_t g1 = g0 + span < blocks ? g0 + span : blocks;
+        float lane[ORC_LANES], next[ORC_LANES];
+        for (int v = 0; v < ORC_LANES; ++v) {
+            float acc = 0.0f;
+            for (int64_t b = g0; b < g1; ++b) {
+                const float value = x[b * 32 + v];
+                if (fabsf(value) > fabsf(acc)) acc = value;
+            }
+            lane[v] = acc;
+        }
+        for (int off = ORC_LANES / 2; off > 0; off >>= 1) {
+            for (int v = 0; v < ORC_LANES; ++v)
+                next[v] = q8_partner_wins(lane[v ^ off], lane[v]) ? lane[v ^ off] : lane[v];
+            memcpy(lane, next, sizeof lane);
+        }
+        const float extreme = lane[0];
+        const int nonzero = fabsf(extreme) > 0.0f;
+        const float safe = nonzero ? extreme : 1.0f;
+        const float inverse_raw = -127.0f / safe;
+        const float d_raw = 1.0f / inverse_raw;
+        const float inverse = nonzero ? inverse_raw : 0.0f;
+        const float step_d = nonzero ? d_raw : 0.0f;
+        for (int64_t b = g0; b < g1; ++b) {
+            d[b] = step_d;
+            for (int v = 0; v < 32; ++v) {
+                const float scaled = x[b * 32 + v] * inverse;
+                int code = (int)nearbyintf(scaled); /* round half to even in the default mode */
+                if (code < -128) code = -128;
+                if (code > 127) code = 127;
+                codes[b * 32 + v] = (int8_t)code;
+            }
+        }
+    }
+    return 0;
+}
+
+static float f16_at(const uint8_t* p) { return orc_f32_from_fp16((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* get_scale_min_k4 as amd-nv-cpu's slice helper reads it (build.rs:817). */
+static void q4k_scale_min(const uint8_t* blk, int g, int* sc, int* m) {
+    const uint8_t* s = blk + 4;
+    if (g < 4) {
+        *sc = s[g] & 63;
+        *m = s[g + 4] & 63;
+    } else {
+        *sc = (s[g + 4] & 15) | ((s[g - 4] >> 6) << 4);
+        *m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+    }
+}
+
+/* Slice l (0..15) of a Q4_K block: codes of sub-block l/2, values 16*(l&1)..+16.
+ * rc: the block's 256 codes; ints only (build.rs:817-845). */
+static void q4k_slice_ints(const uint8_t* blk, const int8_t* rc, int l, int32_t* dot, int32_t* sum) {
+    const int g = l >> 1, h = l & 1, shift = (g & 1) * 4;
+    const uint8_t* q = blk + 16 + (g >> 1) * 32 + h * 16;
+    const int8_t* c = rc + g * 32 + h * 16;
+    int32_t dt = 0, sm = 0;
+    for (int i = 0; i < 16; ++i) {
+        dt += ((q[i] >> shift) & 15) * c[i];
+        sm += c[i];
+    }
+    *dot = dt;
+    *sum = sm;
+}
+
+/* build.rs:845-848: the fp32 tail of a Q4_K slice. rd: the block's 8 record steps. */
+static float q4k_slice(const uint8_t* blk, const float* rd, const int8_t* rc, int l) {
+    int32_t dot, sum;
+    int sc, m;
+    q4k_slice_ints(blk, rc, l, &dot, &sum);
+    q4k_scale_min(blk, l >> 1, &sc, &m);
+    const float group_d = f16_at(blk) * (float)sc;
+    const float group_dmin = f16_at(blk + 2) * (float)m;
+    const float dot_scaled = group_d * (float)dot;
+    const float minimum_scaled = group_dmin * (float)sum;
+    const float value = dot_scaled - minimum_scaled;
+    return rd[l >> 1] * value;
+}
+
+/* Q6_K code n (0..255) of a block (build.rs:893-899 field positions). */
+static int q6k_code(const uint8_t* blk, int n) {
+    const int chunk = n / 128, local = (n % 128) / 32, within = n % 32;
+    const int lo = (blk[chunk * 64 + (local & 1) * 32 + within] >> ((local >> 1) * 4)) & 15;
+    const int hi = (blk[128 + chunk * 32 + within] >> (local * 2)) & 3;
+    return lo | (hi << 4);
+}
+
+/* build.rs:886-915: a Q6_K slice; the scale index is the slice index. */
+static float q6k_slice(const uint8_t* blk, const float* rd, const int8_t* rc, int l) {
+    int32_t dot = 0, sum = 0;
+    for (int i = 0; i < 16; ++i) {
+        dot += q6k_code(blk, l * 16 + i) * rc[l * 16 + i];
+        sum += rc[l * 16 + i];
+    }
+    const int32_t dot_signed = dot - sum * 32;
+    const float scaled = (float)(int8_t)blk[192 + l] * (float)dot_signed;
+    const float value = rd[l >> 1] * scaled;
+    return f16_at(blk + 208) * value;
+}
+
+/* build.rs:776-804: slice h (0, 1) of a Q8_0 or Q4_0 block against its record
+ * (rd: the record's step, rc: its 32 codes). Q4_0 takes the low nibbles for
+ * slice 0 and the high ones for slice 1 and subtracts 8 times the code sum;
+ * the minimum term is zero for both formats. */
+static float b32_slice(int format, const uint8_t* blk, float rd, const int8_t* rc, int h) {
+    int32_t dot = 0, sum = 0;
+    for (int i = 0; i < 16; ++i) {
+        const int c = rc[h * 16 + i];
+        const int w = format == 8 ? (int)(int8_t)blk[2 + h * 16 + i] : (blk[2 + i] >> (4 * h)) & 15;
+        dot += w * c;
+        sum += c;
+    }
+    if (format == 2) dot -= sum * 8;
+    const float d = f16_at(blk);
+    const float minimum = 0.0f;
+    const float dot_scaled = d * (float)dot;
+    const float minimum_scaled = minimum * (float)sum;
+    const float value = dot_scaled + minimum_scaled;
+    return rd * value;
+}
+
+/* amd-nv-cpu.ll:2156-2170: the lanes' butterfly, offsets 16..1; lane 0's value. */
+static float lanes_reduce(float* lane) {
+    float next[ORC_LANES];
+    for (int off = ORC_LANES / 2; off > 0; off >>= 1) {
+        for (int v = 0; v < ORC_LANES; ++v) next[v] = lane[v] + lane[v ^ off];
+        memcpy(lane, next, sizeof next);
+    }
+    return lane[0];
+}
+
+/* One row of 16-value slices: lane l adds slices l, l+32, ... in order
+ * (amd-nv-cpu.ll:1804-1836 Q4_K, 2011-2031 Q6_K, 2055-2090 Q8_0 / Q4_0). */
+static float row_slices(int format, const uint8_t* row, int64_t cols, const float* rd, const int8_t* rc) {
+    float lane[ORC_LANES];
+    for (int v = 0; v < ORC_LANES; ++v) lane[v] = 0.0f;
+    const int64_t slices = cols / 16;
+    for (int64_t s = 0; s < slices; ++s) {
+        float value;
+        if (format == 12) {
+            const int64_t b = s / 16;
+            value = q4k_slice(row + b * 144, rd + b * 8, rc + b * 256, (int)(s % 16));
+        } else if (format == 14) {
+            const int64_t b = s / 16;
+            value = q6k_slice(row + b * 210, rd + b * 8, rc + b * 256, (int)(s % 16));
+        } else {
+            const int64_t b = s / 2;
+            value = b32_slice(format, row + b * orc_block_bytes(format), rd[b], rc + b * 32, (int)(s % 2));
+        }
+        lane[s % ORC_LANES] = lane[s % ORC_LANES] + value;
+    }
+    return lanes_reduce(lane);
+}
+
+/* amd-nv-cpu.ll:1545-1733: Q4_K under a 256 step. Each slice's ints are the
+ * group scale times its dot and the group minimum times its code sum
+ * (build.rs:861-866); the four quarters' ints (four slices each) are exact.
+ * whole: one fma per block with the block's int; otherwise one per quarter. */
+static float row_q4k_256(const uint8_t* row, int64_t cols, const float* rd, const int8_t* rc, int whole) {
+    float acc = 0.0f, accmin = 0.0f;
+    for (int64_t b = 0; b < cols / 256; ++b) {
+        const uint8_t* blk = row + b * 144;
+        int32_t dq[4] = {0, 0, 0, 0}, mq[4] = {0, 0, 0, 0};
+        for (int l = 0; l < 16; ++l) {
+            int32_t dot, sum;
+            int sc, m;
+            q4k_slice_ints(blk, rc + b * 256, l, &dot, &sum);
+            q4k_scale_min(blk, l >> 1, &sc, &m);
+            dq[l >> 2] += sc * dot;
+            mq[l >> 2] += m * sum;
+        }
+        const float d8 = rd[b * 8];
+        const float scale = f16_at(blk) * d8;
+        const float dscale = f16_at(blk + 2) * d8;
+        if (whole) {
+            const int32_t dot_all = (dq[0] + dq[1]) + (dq[2] + dq[3]);
+            const int32_t min_all = (mq[0] + mq[1]) + (mq[2] + mq[3]);
+            acc = fmaf((float)dot_all, scale, acc);
+            accmin = fmaf((float)min_all, dscale, accmin);
+        } else {
+            for (int q = 0; q < 4; ++q) {
+                acc = fmaf((float)dq[q], scale, acc);
+                accmin = fmaf((float)mq[q], dscale, accmin);
+            }
+        }
+    }
+    return acc - accmin;
+}
+
+/* amd-nv-cpu.ll:1836-2031 with build.rs:871-884: Q6_K under a 256 step. Chain
+ * l (0..7) takes, from every 32-value group, the scaled dot of its four-value
+ * word l (slice 2k + l/4, word l%4), less 32 times the scaled code sums of
+ * group l; each chain meets its own fma once per block; a fixed tree adds the
+ * eight chains. */
+static float row_q6k_256(const uint8_t* row, int64_t cols, const float* rd, const int8_t* rc) {
+    float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t b = 0; b < cols / 256; ++b) {
+        const uint8_t* blk = row + b * 210;
+        const int8_t* c = rc + b * 256;
+        int32_t ints[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int s = 0; s < 16; ++s) {
+            const int scale = (int8_t)blk[192 + s];
+            for (int w = 0; w < 4; ++w) {
+                int32_t dot = 0, sum = 0;
+                for (int i = 0; i < 4; ++i) {
+                    const int n = s * 16 + w * 4 + i;
+                    dot += q6k_code(blk, n) * c[n];
+                    sum += c[n];
+                }
+                ints[(s & 1) * 4 + w] += scale * dot;
+                ints[s >> 1] += -32 * (scale * sum);
+            }
+        }
+        const float scale = rd[b * 8] * f16_at(blk + 208);
+        for (int l = 0; l < 8; ++l) f[l] = fmaf(scale, (float)ints[l], f[l]);
+    }
+    const float t0 = f[0] + f[4], t1 = f[1] + f[5], t2 = f[2] + f[6], t3 = f[3] + f[7];
+    const float u0 = t0 + t2, u1 = t1 + t3;
+    return u0 + u1;
+}
+
+int orc_int8_matvec(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const float* x, int m_count,
+                    int step, int tail, float* y) {
+    if (format != 2 && format != 8 && format != 12 && format != 14) return -1;
+    if (!shape_ok(format, rows, cols) || m_count < 1 || (step != 32 && step != 256)) return -1;
+    const int64_t rbytes = row_bytes_of(format, cols);
+    float* rd = (float*)malloc((size_t)(cols / 32) * sizeof(float));
+    int8_t* rc = (int8_t*)malloc((size_t)cols);
+    if (!rd || !rc) {
+        free(rd);
+        free(rc);
+        return -2;
+    }
+    for (int m = 0; m < m_count; ++m) {
+        orc_q8_records(x + (int64_t)m * cols, cols, step, rd, rc);
+        const int whole = m >= m_count - m_count % 4 || (tail && m == m_count - 1);
+        for (int64_t n = 0; n < rows; ++n) {
+            const uint8_t* row = bytes + n * rbytes;
+            float v;
+            if (step == 256 && format == 12)
+                v = row_q4k_256(row, cols, rd, rc, whole);
+            else if (step == 256 && format == 14)
+                v = row_q6k_256(row, cols, rd, rc);
+            else
+                v = row_slices(format, row, cols, rd, rc);
+            y[(int64_t)m * rows + n] = v;
+        }
+    }
+    free(rd);
+    free(rc);
+    return 0;
+}

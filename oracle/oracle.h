@@ -84,6 +84,32 @@ int orc_q4k_q81_reference(const uint8_t* w, int64_t rows, int64_t cols, const fl
  * rows of 16 superblocks (4096 columns). */
 void orc_q4k_xorshift_rows(uint32_t seed, int64_t rows, uint16_t scale_bits, uint8_t* out);
 
+/* recipe's int(8) sum (the default profile's `sum = "int8"`, Cargo.toml:143-162,
+ * and the llama.cpp profile's, Cargo.toml:182-201). recipe's GPU backends run
+ * it with 32 lanes per output (a wave of 32, NVIDIA's warp or gfx11/gfx12's
+ * wave32); this restatement keeps those 32 lanes as an array.
+ *
+ * Activation records (amd-nv-cpu.ll:1304-1500): per `step` inputs (32 or 256)
+ * one fp32 step d and a signed 8-bit code per input. The step's extreme is the
+ * input of largest magnitude (lane scans keep the first, the 32-lane butterfly
+ * prefers the larger signed value on equal magnitudes); inverse = -127/extreme,
+ * d = 1/inverse, code = clamp(roundeven(x*inverse), -128, 127); an all-zero
+ * step has d = 0 and zero codes. d is stored once per 32 inputs. */
+int orc_q8_records(const float* x, int64_t k, int step, float* d, int8_t* codes);
+
+/* The int(8) product of GGUF block rows against Q8 records, per position m:
+ * y[m*rows + n] in fp32. Slices of 16 values (Q4_K, Q6_K at a 32 step; Q8_0 and
+ * Q4_0 at either step: build.rs:776-866, 886-915) have their ints made with
+ * dot4 and their fp32 tail in the helper's order; lane l adds slices l, l+32,
+ * ... in order and the lanes meet in a butterfly of offsets 16..1
+ * (amd-nv-cpu.ll:1804-1836, 2031-2090, 2156-2170). At a 256 step Q4_K folds
+ * whole blocks with fma in block order (amd-nv-cpu.ll:1545-1733; four
+ * quarter fmas for positions m < M - M%4 unless `tail` makes the last
+ * position whole) and Q6_K keeps eight fma chains (amd-nv-cpu.ll:1836-2031).
+ * Inputs must be finite. */
+int orc_int8_matvec(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const float* x, int m_count,
+                    int step, int tail, float* y);
+
 #ifdef __cplusplus
 }
 #endif
