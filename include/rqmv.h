@@ -226,6 +226,28 @@ typedef struct {
 int rqmv_matvec_fused(const rqmv_weight* weight, const float* x_dev, float* y_dev, const rqmv_fusion* fusion,
                       void* stream);
 
+/* recipe's int(8) sum: the product recipe computes when a precision profile
+ * declares `sum = "int8"` (the default profile, step 32, and the llama.cpp
+ * profile, step 256; Cargo.toml:143-201) on a backend with int8 dots
+ * (contraction_forward_gemv_wave_body, amd-nv-cpu.ll:1231-2241). Each of the
+ * m fp32 activation rows (row i at x + i*ldx) is rounded to Q8 records (one
+ * fp32 step per `step` inputs, a signed byte per input); the block dots run
+ * on v_dot4_i32_i8 and the fp32 tail in recipe's order, so y[i*ldy + n] has
+ * the bits recipe's 32-lane GPU backends produce. Formats Q4_K, Q6_K, Q8_0,
+ * Q4_0 (an expert bank counts as experts x rows rows). At step 256 a Q4_K
+ * position before the last m % 4 folds each block in four quarters, as
+ * llama.cpp's batched kernel does; flags RQMV_INT8_TAIL folds the last
+ * position whole (recipe's model tail, amd-nv-cpu.ll:1716-1722). x must be
+ * finite; cols + cols/8 bytes of LDS hold the records. */
+enum { RQMV_INT8_TAIL = 1 };
+int rqmv_matvec_int8(const rqmv_weight* weight, const float* x_dev, int m, int64_t ldx, float* y_dev, int64_t ldy,
+                     int step, int flags, void* stream);
+
+/* The Q8 records of one activation row of k inputs (k a multiple of 32) that
+ * rqmv_matvec_int8 forms in LDS (amd-nv-cpu.ll:1408-1500): d_dev[k/32] steps
+ * (one value per `step` inputs, repeated per 32) and codes_dev[k] bytes. */
+int rqmv_q8_records(const float* x_dev, int64_t k, int step, float* d_dev, int8_t* codes_dev, void* stream);
+
 /* *pos += 1 on the device (the last launch of a captured decode step). */
 int rqmv_advance(int* pos, void* stream);
 

@@ -72,4 +72,12 @@ hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, int 
                               hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 size_t mfma_lds_bytes(int fmt, int xtype, int M, int64_t rows, int cus);
 
+// recipe's int(8) sum (int8.hip): Q8 activation records of `step` (32 or 256)
+// inputs, v_dot4_i32_i8 block dots, recipe's fp32 order. y[m*ldy + n] for
+// n < rows, m < M; tail: the last position folds 256-step Q4_K blocks whole.
+size_t int8_lds_bytes(int64_t cols);
+hipError_t launch_matvec_int8(int fmt, const Planes& P, int64_t rows, int K, const float* x, int M, int64_t ldx,
+                              float* y, int64_t ldy, int step, int tail, hipStream_t stream);
+hipError_t launch_q8_records(const float* x, int K, int step, float* d, int8_t* codes, hipStream_t stream);
+
 }  // namespace rq

@@ -565,6 +565,34 @@ int rqmv_argmax_workspace_size(size_t* bytes) {
     return RQMV_OK;
 }
 
+int rqmv_matvec_int8(const rqmv_weight* w, const float* x_dev, int m, int64_t ldx, float* y_dev, int64_t ldy,
+                     int step, int flags, void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(w, &info);
+    if (rc != RQMV_OK) return rc;
+    if (!x_dev || !y_dev) return fail(RQMV_EINVAL, "int8: x or y is NULL");
+    if (w->fmt != rq::Q4_K && w->fmt != rq::Q6_K && w->fmt != rq::Q8_0 && w->fmt != rq::Q4_0)
+        return fail(RQMV_EINVAL, "int8: a Q4_K, Q6_K, Q8_0 or Q4_0 weight is required");
+    if (step != 32 && step != 256) return fail(RQMV_EINVAL, "int8: step must be 32 or 256");
+    if (flags & ~RQMV_INT8_TAIL) return fail(RQMV_EINVAL, "int8: unknown flags");
+    if (m <= 0 || m > 65535) return fail(RQMV_EINVAL, "int8: m must be in 1..65535");
+    const int64_t rows = w->rows * w->experts;
+    if (ldx < w->cols || ldy < rows) return fail(RQMV_EINVAL, "int8: ldx < cols or ldy < rows");
+    if (reinterpret_cast<uintptr_t>(x_dev) % 4 != 0) return fail(RQMV_EINVAL, "int8: x must be 4-byte aligned");
+    if (rq::int8_lds_bytes(w->cols) > info.lds_limit) return fail(RQMV_EINVAL, "int8: cols too large for the LDS records");
+    hipError_t e = rq::launch_matvec_int8(w->fmt, planes_of(w, 0), rows, (int)w->cols, x_dev, m, ldx, y_dev, ldy, step,
+                                          (flags & RQMV_INT8_TAIL) ? 1 : 0, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "int8 launch");
+}
+
+int rqmv_q8_records(const float* x_dev, int64_t k, int step, float* d_dev, int8_t* codes_dev, void* stream) {
+    if (!x_dev || !d_dev || !codes_dev) return fail(RQMV_EINVAL, "q8_records: NULL argument");
+    if (k <= 0 || k % 32 != 0 || k > (1 << 24)) return fail(RQMV_EINVAL, "q8_records: k must be a positive multiple of 32");
+    if (step != 32 && step != 256) return fail(RQMV_EINVAL, "q8_records: step must be 32 or 256");
+    hipError_t e = rq::launch_q8_records(x_dev, (int)k, step, d_dev, codes_dev, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? RQMV_OK : hip_fail(e, "q8_records launch");
+}
+
 int rqmv_argmax(const float* values, int n, int* out, void* workspace, size_t workspace_bytes, void* stream) {
     if (!values || !out || !workspace || n <= 0) return fail(RQMV_EINVAL, "argmax: bad arguments");
     if (workspace_bytes < rq::argmax_workspace_bytes()) return fail(RQMV_EINVAL, "argmax: workspace too small");

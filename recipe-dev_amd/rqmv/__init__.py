@@ -66,6 +66,8 @@ class _Lib:
         L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_void_p]
         L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
+        L.rqmv_matvec_int8.argtypes = [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_int, c_int, c_void_p]
+        L.rqmv_q8_records.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p]
         L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
         L.rqmv_gguf_open.argtypes = [c_char_p, c_void_p]
         L.rqmv_gguf_close.argtypes = [c_void_p]
@@ -360,6 +362,41 @@ def expert(bank: Weight, index: int, x: np.ndarray) -> np.ndarray:
     synchronize()
     y = yb.download(np.float32).reshape(m, -1)
     return y[0] if x.ndim == 1 else y
+
+
+INT8_TAIL = 1
+
+
+def matvec_int8(weight: Weight, x: DeviceBuffer, m: int, ldx: int, y: DeviceBuffer, ldy: int, step: int = 32,
+                tail: bool = False, stream: Stream | None = None):
+    """recipe's int(8) sum (rqmv_matvec_int8): fp32 activation rows, Q8 records
+    of `step` inputs, recipe's fp32 order."""
+    _check(lib().lib.rqmv_matvec_int8(weight.handle, x.ptr, m, ldx, y.ptr, ldy, step, INT8_TAIL if tail else 0,
+                                      _sh(stream)), "rqmv_matvec_int8")
+
+
+def contract_int8(weight: Weight, x: np.ndarray, step: int = 32, tail: bool = False) -> np.ndarray:
+    """contract() under recipe's int(8) sum: x (K,) or (M, K) float32 -> fp32 (M, N)."""
+    x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    m, k = x2.shape
+    xb = DeviceBuffer.from_array(x2)
+    n = weight.rows * weight.experts
+    yb = DeviceBuffer(4 * m * n)
+    matvec_int8(weight, xb, m, k, yb, n, step, tail)
+    synchronize()
+    y = yb.download(np.float32).reshape(m, n)
+    return y[0] if x.ndim == 1 else y
+
+
+def q8_records(x: np.ndarray, step: int = 32):
+    """The Q8 records rqmv_matvec_int8 forms for one fp32 row: (d (K/32,), codes int8 (K,))."""
+    xs = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    xb = DeviceBuffer.from_array(xs)
+    db = DeviceBuffer(4 * (xs.size // 32))
+    cb = DeviceBuffer(xs.size)
+    _check(lib().lib.rqmv_q8_records(xb.ptr, xs.size, step, db.ptr, cb.ptr, None), "rqmv_q8_records")
+    synchronize()
+    return db.download(np.float32), cb.download(np.int8)
 
 
 class MoeParams(ctypes.Structure):
