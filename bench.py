@@ -322,6 +322,94 @@ def decode_bench(args):
     graph.close()
 
 
+def int8_bench(args):
+    """recipe's int(8) sum (rqmv_matvec_int8) on a workload's weight, fp32
+    activations: the same whole-job graph timing; kernel durations from events
+    recorded around each launch; parity bit for bit against the oracle."""
+    import rqmv
+    from rqmv import synth
+
+    fmt, rows, cols, _, desc = WORKLOADS[args.workload]
+    m, step = args.m, args.int8
+    desc = f"{desc}, recipe int(8) sum step {step}"
+    log(f"bench: {args.workload} int8 step {step} M={m} steps={args.steps} warmup={args.warmup}")
+    rqmv.init(0)
+    w = synth.weights(fmt, rows, cols)
+    x32 = synth.activations_f32(m * cols).reshape(m, cols)
+    alg_bytes = w.nbytes + m * cols * 4 + m * rows * 4
+    copies = args.copies or max(2, -(-2 * MALL_BYTES // w.nbytes) + 1)
+    Ws = [rqmv.Weight(fmt, rows, cols, w) for _ in range(copies)]
+    xb = rqmv.DeviceBuffer.from_array(x32)
+    yb = rqmv.DeviceBuffer(4 * m * rows)
+    stream = rqmv.Stream()
+    exact = None
+    if not args.no_check:
+        import oracle
+
+        rqmv.matvec_int8(Ws[0], xb, m, cols, yb, rows, step, stream=stream)
+        stream.synchronize()
+        y = yb.download(np.float32).reshape(m, rows)
+        ref = oracle.int8_matvec(fmt, w, rows, cols, x32, step)
+        exact = bool(np.array_equal(y.view(np.uint32), ref.view(np.uint32)))
+        log(f"bench: int8 parity bit-exact {exact}")
+        if not exact:
+            sys.exit(1)
+
+    def enqueue_steps(count):
+        for i in range(count):
+            rqmv.matvec_int8(Ws[i % copies], xb, m, cols, yb, rows, step, stream=stream)
+
+    graph = rqmv.Graph(stream, lambda: enqueue_steps(args.steps))
+    graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = rqmv.Event(), rqmv.Event()
+    e0.record(stream)
+    graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    ms_per_step = e0.elapsed_ms(e1) / args.steps
+    starts = [rqmv.Event() for _ in range(args.steps)]
+    stops = [rqmv.Event() for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record(stream)
+        rqmv.matvec_int8(Ws[i % copies], xb, m, cols, yb, rows, step, stream=stream)
+        stops[i].record(stream)
+    stream.synchronize()
+    ker_ms = float(np.mean([starts[i].elapsed_ms(stops[i]) for i in range(args.steps)]))
+    log(f"bench: int8 graph {ms_per_step * 1e3:.2f} us/step, event-bracketed kernel {ker_ms * 1e3:.2f} us")
+    achieved = alg_bytes / (ker_ms * 1e-3) / 1e9
+    out = {
+        "metric": "recipe int(8) sum matvec effective HBM GB/s at batch 1",
+        "value": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": desc, "format": fmt.upper(), "rows": rows, "cols": cols, "m": m, "step": step,
+                   "activations": "f32", "weight_copies": copies, "bytes_per_step": alg_bytes,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "kernel_us": round(ker_ms * 1e3, 3),
+        "parity_bit_exact": exact,
+    }
+    if not args.no_cpu:
+        import oracle
+
+        runs, t0 = 0, time.perf_counter()
+        while True:
+            oracle.int8_matvec(fmt, w, rows, cols, x32, step)
+            runs += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds:
+                break
+        per = el / runs
+        out["cpu_baseline"] = {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                               "sample": f"{runs} full int(8) matvecs in {el:.1f} s, {per * 1e3:.2f} ms each, "
+                                         f"oracle restatement, one thread"}
+    print(json.dumps(out), flush=True)
+    graph.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -333,6 +421,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--int8", type=int, default=0, choices=[0, 32, 256],
+                    help="run recipe's int(8) sum with this step instead (fp32 activations)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device copy of this many MB per step (counter calibration)")
     args = ap.parse_args()
@@ -350,6 +440,10 @@ def main():
         return
     if args.workload == "decode_c5":
         decode_bench(args)
+        return
+
+    if args.int8:
+        int8_bench(args)
         return
 
     import rqmv
