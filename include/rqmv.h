@@ -238,13 +238,14 @@ int rqmv_matvec_fused(const rqmv_weight* weight, const float* x_dev, float* y_de
  * position before the last m % 4 folds each block in four quarters, as
  * llama.cpp's batched kernel does; flags RQMV_INT8_TAIL folds the last
  * position whole (recipe's model tail, amd-nv-cpu.ll:1716-1722). x must be
- * finite; cols + cols/8 bytes of LDS hold the records. */
+ * finite, 16-byte aligned, ldx a multiple of 4; about cols * 1.14 bytes of
+ * LDS hold the records. */
 enum { RQMV_INT8_TAIL = 1 };
 int rqmv_matvec_int8(const rqmv_weight* weight, const float* x_dev, int m, int64_t ldx, float* y_dev, int64_t ldy,
                      int step, int flags, void* stream);
 
-/* The Q8 records of one activation row of k inputs (k a multiple of 32) that
- * rqmv_matvec_int8 forms in LDS (amd-nv-cpu.ll:1408-1500): d_dev[k/32] steps
+/* The Q8 records of one activation row of k inputs (k a multiple of 32, x
+ * 16-byte aligned) that rqmv_matvec_int8 forms in LDS (amd-nv-cpu.ll:1408-1500): d_dev[k/32] steps
  * (one value per `step` inputs, repeated per 32) and codes_dev[k] bytes. */
 int rqmv_q8_records(const float* x_dev, int64_t k, int step, float* d_dev, int8_t* codes_dev, void* stream);
 

@@ -37,47 +37,106 @@ namespace rq {
 
 namespace {
 
-constexpr int kI8Threads = 256;                    // four waves, eight 32-lane halves
-constexpr int kI8Halves = kI8Threads / 32;
-constexpr int kI8RowsPerHalf = 2;                  // outputs each half takes per workgroup
-constexpr int kI8Rows = kI8Halves * kI8RowsPerHalf;  // outputs per workgroup
+constexpr int kI8Threads = 512;                  // eight waves
+constexpr int kI8Rows = 2 * (kI8Threads / 64);   // outputs per workgroup: two per wave
 
-// The Q8 records of one activation column of K inputs: d[K/32] and codes[K].
-// Half-wave h takes steps h, h+halves, ...; lane v scans input v of each of
-// the step's 32-value blocks, keeping the first extreme, and the halves'
-// butterfly prefers the larger signed value between equal magnitudes
-// (amd-nv-cpu.ll:1408-1470). inverse = -127 / extreme, d = 1 / inverse,
-// code = clamp(round-half-even(x * inverse), -128, 127); an all-zero step
-// has d = 0 and zero codes (amd-nv-cpu.ll:1447-1500).
-__device__ __forceinline__ void q8_records(const float* __restrict__ x, int K, int step, float* d, int8_t* codes,
-                                           int tid, int nthreads) {
-    const int half = tid >> 5, lane = tid & 31, halves = nthreads >> 5;
-    const int blocks = K >> 5, span = step >> 5;
-    const int groups = (blocks + span - 1) / span;
-    for (int g = half; g < groups; g += halves) {
-        const int b0 = g * span, b1 = min(b0 + span, blocks);
-        float e = 0.f;
-        for (int b = b0; b < b1; ++b) {
-            const float v = x[b * 32 + lane];
-            if (fabsf(v) > fabsf(e)) e = v;
-        }
+// Extreme selection of recipe's Q8 records (amd-nv-cpu.ll:1422-1470): the
+// partner replaces the running extreme when its magnitude is larger, or equal
+// with a larger signed value. Scanning values in any order from +0 with this
+// rule yields the value recipe's 32-lane butterfly leaves: the maximum under
+// (magnitude, signed value), zeros and NaNs never replacing +0.
+__device__ __forceinline__ bool extreme_wins(float p, float e) {
+    const float ap = fabsf(p), ae = fabsf(e);
+    return ap > ae || (ap == ae && p > e);
+}
+
+// inverse = -127 / extreme and d = 1 / inverse, both correctly rounded; an
+// all-zero step has inverse 0 and d 0 (amd-nv-cpu.ll:1447-1456).
+__device__ __forceinline__ void step_of(float e, float& inverse, float& d) {
+    const bool nonzero = fabsf(e) > 0.f;
+    const float inverse_raw = -127.f / (nonzero ? e : 1.f);
+    const float d_raw = 1.f / inverse_raw;
+    inverse = nonzero ? inverse_raw : 0.f;
+    d = nonzero ? d_raw : 0.f;
+}
+
+// The 32 codes of record r: clamp(round-half-even(x * inverse), -128, 127)
+// (amd-nv-cpu.ll:1484-1490), from a 16-byte aligned row, into LDS.
+__device__ __forceinline__ void record_codes(const float* __restrict__ xr, float inverse, int8_t* out) {
+    uint32_t w[8];
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) {
-            const float p = __shfl_xor(e, off, 32);
-            const float ap = fabsf(p), ae = fabsf(e);
-            if (ap > ae || (ap == ae && p > e)) e = p;
+    for (int q = 0; q < 8; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float r = __builtin_rintf(f[k] * inverse);
+            word |= ((uint32_t)(int)fminf(fmaxf(r, -128.f), 127.f) & 0xffu) << (8 * k);
         }
-        const bool nonzero = fabsf(e) > 0.f;
-        const float inverse_raw = -127.f / (nonzero ? e : 1.f);
-        const float d_raw = 1.f / inverse_raw;
-        const float inverse = nonzero ? inverse_raw : 0.f;
-        const float dd = nonzero ? d_raw : 0.f;
-        for (int b = b0; b < b1; ++b) {
-            const float r = __builtin_rintf(x[b * 32 + lane] * inverse);
-            codes[b * 32 + lane] = (int8_t)(int)fminf(fmaxf(r, -128.f), 127.f);
-            if (lane == 0) d[b] = dd;
-        }
+        w[q] = word;
     }
+    reinterpret_cast<uint4*>(out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// The Q8 records of one activation row of K inputs (16-byte aligned) into
+// LDS: codes[K], d[K/32], and ginv[ceil(K/256)] scratch for a 256 step.
+// Step 32: one thread per record scans its 32 inputs. Step 256: recipe's lane
+// v keeps the first largest magnitude among input v of the step's 32-value
+// blocks (amd-nv-cpu.ll:1408-1440), computed here by one thread per (step,
+// lane) into `codes` (free until the codes are written); one thread per step
+// then takes the extreme over its 32 lanes. Ends with a barrier.
+__device__ __forceinline__ void q8_records(const float* __restrict__ x, int K, int step, float* d, int8_t* codes,
+                                           float* ginv, int tid, int nthreads) {
+    const int blocks = K >> 5;
+    if (step == 32) {
+        for (int r = tid; r < blocks; r += nthreads) {
+            const float* xr = x + r * 32;
+            float e = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+                if (extreme_wins(v.x, e)) e = v.x;
+                if (extreme_wins(v.y, e)) e = v.y;
+                if (extreme_wins(v.z, e)) e = v.z;
+                if (extreme_wins(v.w, e)) e = v.w;
+            }
+            float inverse, dd;
+            step_of(e, inverse, dd);
+            record_codes(xr, inverse, codes + r * 32);
+            d[r] = dd;
+        }
+        __syncthreads();
+        return;
+    }
+    const int groups = (blocks + 7) >> 3;
+    float* lane_best = reinterpret_cast<float*>(codes);  // groups * 32 floats <= K bytes
+    for (int i = tid; i < groups * 32; i += nthreads) {
+        const int g = i >> 5, v = i & 31;
+        const int b1 = min(g * 8 + 8, blocks);
+        float e = 0.f;
+        for (int b = g * 8; b < b1; ++b) {
+            const float xv = x[b * 32 + v];
+            if (fabsf(xv) > fabsf(e)) e = xv;
+        }
+        lane_best[i] = e;
+    }
+    __syncthreads();
+    for (int g = tid; g < groups; g += nthreads) {
+        float e = 0.f;
+        for (int v = 0; v < 32; ++v) {
+            const float p = lane_best[g * 32 + v];
+            if (extreme_wins(p, e)) e = p;
+        }
+        float inverse, dd;
+        step_of(e, inverse, dd);
+        ginv[g] = inverse;
+        for (int b = g * 8; b < min(g * 8 + 8, blocks); ++b) d[b] = dd;
+    }
+    __syncthreads();
+    for (int r = tid; r < blocks; r += nthreads) record_codes(x + r * 32, ginv[r >> 3], codes + r * 32);
+    __syncthreads();
 }
 
 // Four consecutive 4-bit fields of word n (its low half, or its high half when
@@ -93,12 +152,6 @@ __device__ __forceinline__ float f16_at(const uint8_t* p) {
     return (float)*reinterpret_cast<const _Float16*>(p);
 }
 
-// The int parts of one 16-value slice: dot = sum q*c over the slice (q the
-// weight codes, c the record bytes), sum = sum c.
-struct SliceInts {
-    int dot, sum;
-};
-
 __device__ __forceinline__ int code_sum(const uint4& c) {
     int s = sdot4(0x01010101u, c.x, 0);
     s = sdot4(0x01010101u, c.y, s);
@@ -113,18 +166,6 @@ __device__ __forceinline__ int dot4w(uint32_t q0, uint32_t q1, uint32_t q2, uint
     return sdot4(q3, c.w, s);
 }
 
-// Q4_K slice s of a row (block s/16, sub-block g = (s%16)/2, values 16*(s&1)..):
-// its ints and the superblock's 16 meta bytes (d, dmin, packed scales).
-__device__ __forceinline__ SliceInts q4k_slice(const uint8_t* rowp, int nch, int s, const uint4& c, uint4& meta) {
-    const int b = s >> 4, l = s & 15, g = l >> 1;
-    const ChunkPlace cp = chunk_place(Q4_K, b * 4 + (g >> 1), nch);
-    const uint8_t* gs = rowp + cp.group_start;
-    const uint2 n = *reinterpret_cast<const uint2*>(gs + ((g & 1) * cp.nb + cp.within) * 16 + (l & 1) * 8);
-    meta = *reinterpret_cast<const uint4*>(gs + 2 * cp.nb * 16 + (cp.within >> 2) * 16);
-    return SliceInts{dot4w(nib_codes(n.x, false), nib_codes(n.x, true), nib_codes(n.y, false), nib_codes(n.y, true), c),
-                     code_sum(c)};
-}
-
 // get_scale_min_k4 of sub-block g from the superblock's meta words.
 __device__ __forceinline__ void q4k_scale_min(const uint4& meta, int g, int& sc, int& m) {
     if (g < 4) {
@@ -137,88 +178,100 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& meta, int g, int& sc,
     }
 }
 
-// Q6_K slice s (block s/16, scale group l = s%16): its ints, scale and d.
-__device__ __forceinline__ SliceInts q6k_slice(const uint8_t* rowp, int nch, int s, const uint4& c, int& sc, float& d,
-                                               int* words = nullptr) {
-    const int b = s >> 4, l = s & 15, g4 = l & 3;
-    const ChunkPlace cp = chunk_place(Q6_K, b * 4 + (l >> 2), nch);
-    const uint8_t* gs = rowp + cp.group_start;
-    const uint2 n = *reinterpret_cast<const uint2*>(gs + ((g4 >> 1) * cp.nb + cp.within) * 16 + (g4 & 1) * 8);
-    const uint32_t H = *reinterpret_cast<const uint32_t*>(gs + (2 * cp.nb + cp.within) * 16 + g4 * 4);
-    const uint8_t* meta = gs + 3 * cp.nb * 16;
-    sc = (int)*reinterpret_cast<const int8_t*>(meta + (cp.within >> 2) * 16 + l);
-    d = f16_at(meta + (cp.nb >> 2) * 16 + (cp.within >> 2) * 2);
-    const uint32_t h0 = H & 0x33333333u, h1 = (H >> 2) & 0x33333333u;
-    const uint32_t q0 = nib_codes(n.x, false) | (spread(h0, false) << 4);
-    const uint32_t q1 = nib_codes(n.x, true) | (spread(h0, true) << 4);
-    const uint32_t q2 = nib_codes(n.y, false) | (spread(h1, false) << 4);
-    const uint32_t q3 = nib_codes(n.y, true) | (spread(h1, true) << 4);
-    if (words) {
-        words[0] = sdot4(q0, c.x, 0);
-        words[1] = sdot4(q1, c.y, 0);
-        words[2] = sdot4(q2, c.z, 0);
-        words[3] = sdot4(q3, c.w, 0);
-        return SliceInts{0, 0};
-    }
-    return SliceInts{dot4w(q0, q1, q2, q3, c), code_sum(c)};
+// The dot of 16 stored nibbles (two words, XOR 8) with a slice's record bytes.
+__device__ __forceinline__ int q4_dot(uint32_t n0, uint32_t n1, const uint4& c) {
+    return dot4w(nib_codes(n0, false), nib_codes(n0, true), nib_codes(n1, false), nib_codes(n1, true), c);
 }
 
-// The fp32 value of slice s (build.rs:776-804, 845-848, 909-912).
+// Q6_K slice t (0..3) of a chunk: codes q = l | h << 4, four per word.
+__device__ __forceinline__ void q6_words(const ChunkData<Q6_K>& D, int t, uint32_t q[4]) {
+    const uint4& lo = D.q[t >> 1];
+    const uint32_t n0 = (t & 1) ? lo.z : lo.x, n1 = (t & 1) ? lo.w : lo.y;
+    const uint32_t H = word(D.q[2], t);
+    const uint32_t h0 = H & 0x33333333u, h1 = (H >> 2) & 0x33333333u;
+    q[0] = nib_codes(n0, false) | (spread(h0, false) << 4);
+    q[1] = nib_codes(n0, true) | (spread(h0, true) << 4);
+    q[2] = nib_codes(n1, false) | (spread(h1, false) << 4);
+    q[3] = nib_codes(n1, true) | (spread(h1, true) << 4);
+}
+
+__device__ __forceinline__ uint4 record_bytes(const int8_t* xc, int s) {
+    return *reinterpret_cast<const uint4*>(xc + s * 16);
+}
+
+// Slices per chunk: a chunk is 64 weights (four 16-value slices) except
+// Q8_0's 32 (two).
 template <int FMT>
-__device__ __forceinline__ float slice_value(const uint8_t* rowp, int nch, int s, const int8_t* xc, const float* xd) {
-    const uint4 c = *reinterpret_cast<const uint4*>(xc + s * 16);
+constexpr int chunk_slices() {
+    return FMT == Q8_0 ? 2 : 4;
+}
+
+// The fp32 values of chunk c's slices (build.rs:776-804, 845-848, 909-912),
+// slice t of the chunk being slice c * chunk_slices + t of the row.
+template <int FMT>
+__device__ __forceinline__ void chunk_values(const ChunkData<FMT>& D, int c, const int8_t* xc, const float* xd,
+                                             float v[chunk_slices<FMT>()]) {
     if constexpr (FMT == Q4_K) {
-        uint4 meta;
-        const SliceInts t = q4k_slice(rowp, nch, s, c, meta);
-        int sc, m;
-        const int g = (s & 15) >> 1;
-        q4k_scale_min(meta, g, sc, m);
-        const float group_d = half_lo(meta.x) * (float)sc;
-        const float group_dmin = half_hi(meta.x) * (float)m;
-        const float dot_scaled = group_d * (float)t.dot;
-        const float minimum_scaled = group_dmin * (float)t.sum;
-        const float value = dot_scaled - minimum_scaled;
-        return xd[(s >> 4) * 8 + g] * value;
-    } else if constexpr (FMT == Q6_K) {
-        int sc;
-        float d;
-        const SliceInts t = q6k_slice(rowp, nch, s, c, sc, d);
-        const int dot_signed = t.dot - t.sum * 32;
-        const float scaled = (float)sc * (float)dot_signed;
-        const float value = xd[s >> 1] * scaled;  // record (s/16)*8 + (s%16)/2
-        return d * value;
-    } else {
-        const int blk = s >> 1, h = s & 1;
-        int dot;
-        float d;
-        if constexpr (FMT == Q8_0) {
-            const ChunkPlace cp = chunk_place(Q8_0, blk, nch);
-            const uint8_t* gs = rowp + cp.group_start;
-            const uint4 w = *reinterpret_cast<const uint4*>(gs + (h * cp.nb + cp.within) * 16);
-            d = f16_at(gs + 2 * cp.nb * 16 + cp.within * 2);
-            dot = dot4w(w.x, w.y, w.z, w.w, c);
-        } else {
-            const ChunkPlace cp = chunk_place(Q4_0, blk >> 1, nch);
-            const uint8_t* gs = rowp + cp.group_start;
-            const int part = blk & 1;
-            const uint2 n = *reinterpret_cast<const uint2*>(gs + (part * cp.nb + cp.within) * 16 + h * 8);
-            d = f16_at(gs + 2 * cp.nb * 16 + cp.within * 4 + part * 2);
-            dot = dot4w(nib_codes(n.x, false), nib_codes(n.x, true), nib_codes(n.y, false), nib_codes(n.y, true), c);
+        const float d = half_lo(D.meta.x), dmin = half_hi(D.meta.x);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int s = 4 * c + t, j = t >> 1, h = t & 1;
+            const int g = 2 * (c & 3) + j;
+            const uint4 x = record_bytes(xc, s);
+            int sc, m;
+            q4k_scale_min(D.meta, g, sc, m);
+            const float group_d = d * (float)sc;
+            const float group_dmin = dmin * (float)m;
+            const float dot_scaled = group_d * (float)q4_dot(word(D.q[j], 2 * h), word(D.q[j], 2 * h + 1), x);
+            const float minimum_scaled = group_dmin * (float)code_sum(x);
+            const float value = dot_scaled - minimum_scaled;
+            v[t] = xd[(c >> 2) * 8 + g] * value;
         }
-        const int sum = code_sum(c);
-        if constexpr (FMT == Q4_0) dot -= sum * 8;
-        const float minimum = 0.f;
-        const float dot_scaled = d * (float)dot;
-        const float minimum_scaled = minimum * (float)sum;
-        const float value = dot_scaled + minimum_scaled;
-        return xd[blk] * value;
+    } else if constexpr (FMT == Q6_K) {
+        const float d = half_lo(D.meta.y);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int s = 4 * c + t;
+            const uint4 x = record_bytes(xc, s);
+            uint32_t q[4];
+            q6_words(D, t, q);
+            const int dot_signed = dot4w(q[0], q[1], q[2], q[3], x) - code_sum(x) * 32;
+            const float scaled = (float)sbfe(D.meta.x, 8 * t, 8) * (float)dot_signed;
+            const float value = xd[s >> 1] * scaled;
+            v[t] = d * value;
+        }
+    } else if constexpr (FMT == Q8_0) {
+        const float d = half_lo(D.meta.x);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint4 x = record_bytes(xc, 2 * c + t);
+            const uint4& w = D.q[t];
+            const int sum = code_sum(x);
+            const float minimum = 0.f;
+            const float dot_scaled = d * (float)dot4w(w.x, w.y, w.z, w.w, x);
+            const float minimum_scaled = minimum * (float)sum;
+            const float value = dot_scaled + minimum_scaled;
+            v[t] = xd[c] * value;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int s = 4 * c + t, j = t >> 1, h = t & 1;
+            const uint4 x = record_bytes(xc, s);
+            const float d = j ? half_hi(D.meta.x) : half_lo(D.meta.x);
+            const int sum = code_sum(x);
+            const int dot = q4_dot(word(D.q[j], 2 * h), word(D.q[j], 2 * h + 1), x) - sum * 8;
+            const float minimum = 0.f;
+            const float dot_scaled = d * (float)dot;
+            const float minimum_scaled = minimum * (float)sum;
+            const float value = dot_scaled + minimum_scaled;
+            v[t] = xd[2 * c + j] * value;
+        }
     }
 }
 
 struct I8Launch {
-    const uint8_t* w;
-    int64_t row_bytes;
-    int nch;
+    Planes P;
     int64_t rows;
     int K;
     const float* x;
@@ -230,167 +283,256 @@ struct I8Launch {
     int tail;
 };
 
-__device__ __forceinline__ void stage_records(const I8Launch& p, int step, int8_t*& xc, float*& xd) {
+// LDS: the records' codes (K bytes), steps (K/32 floats) and per-step
+// inverses (ceil(K/256) floats), then per wave two rows of 256 slice values.
+__device__ __forceinline__ void stage_records(const I8Launch& p, int step, int8_t*& xc, float*& xd, float*& rowbuf) {
     extern __shared__ __align__(16) uint8_t i8_lds[];
     xc = reinterpret_cast<int8_t*>(i8_lds);
     xd = reinterpret_cast<float*>(i8_lds + p.K);
-    q8_records(p.x + (int64_t)blockIdx.y * p.ldx, p.K, step, xd, xc, (int)threadIdx.x, kI8Threads);
-    __syncthreads();
+    const int tail_floats = (p.K >> 5) + ((p.K + 255) >> 8);
+    rowbuf = xd + ((tail_floats + 3) & ~3) + ((int)threadIdx.x >> 6) * 512;
+    q8_records(p.x + (int64_t)blockIdx.y * p.ldx, p.K, step, xd, xc, xd + (p.K >> 5), (int)threadIdx.x, kI8Threads);
 }
 
-// 16-value slices: lane l adds slices l, l+32, ...; the half's butterfly.
+// Exact int sums over the four lanes of a quad (one 256-value block).
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);  // lane ^ 1
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);  // lane ^ 2
+}
+__device__ __forceinline__ int lane_int(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ float lane_float(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// 16-value slices. Each wave takes two rows at a time, lane i decoding chunk
+// i of each 64-chunk pass; the pass's slice values go to the wave's LDS rows,
+// where recipe's lane l (lanes 0-31 for the first row, 32-63 for the second)
+// adds slices l, l+32, ... in order; the halves' butterflies end each row.
 template <int FMT>
 __global__ __launch_bounds__(kI8Threads) void int8_slices_kernel(I8Launch p) {
+    constexpr int CS = chunk_slices<FMT>();
     int8_t* xc;
     float* xd;
-    stage_records(p, p.step, xc, xd);
-    const int half = (int)threadIdx.x >> 5, lane = (int)threadIdx.x & 31;
-    const int slices = p.K >> 4;
-    for (int i = 0; i < kI8RowsPerHalf; ++i) {
-        const int64_t row = (int64_t)blockIdx.x * kI8Rows + i * kI8Halves + half;
-        if (row >= p.rows) break;
-        const uint8_t* rowp = p.w + row * p.row_bytes;
-        float acc = 0.f;
-        for (int s = lane; s < slices; s += 32) acc = acc + slice_value<FMT>(rowp, p.nch, s, xc, xd);
+    float* rowbuf;
+    stage_records(p, p.step, xc, xd, rowbuf);
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int64_t row0 = (int64_t)blockIdx.x * kI8Rows + 2 * wave;
+    if (row0 >= p.rows) return;
+    const bool two = row0 + 1 < p.rows;
+    const int slices = p.K >> 4, nch = p.P.nch;
+    const int mine = lane >> 5;  // which of the two rows this lane sums
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int c = c0 + lane;
+        ChunkData<FMT> A, B;
+        if (c < nch) {
+            load_chunk<FMT>(p.P, row0, c, A);
+            if (two) load_chunk<FMT>(p.P, row0 + 1, c, B);
+        }
+        if (c < nch) {
+            float va[CS], vb[CS] = {};
+            chunk_values<FMT>(A, c, xc, xd, va);
+            if (two) chunk_values<FMT>(B, c, xc, xd, vb);
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 32);
-        if (lane == 0) p.y[(int64_t)blockIdx.y * p.ldy + row] = acc;
+            for (int t = 0; t < CS; ++t) {
+                rowbuf[lane * CS + t] = va[t];
+                rowbuf[256 + lane * CS + t] = vb[t];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int base = c0 * CS;  // first slice of the pass
+        const float* mybuf = rowbuf + 256 * mine;
+        const int l = lane & 31;
+#pragma unroll
+        for (int j = 0; j < 2 * CS; ++j) {
+            const int s = base + l + 32 * j;
+            if (s < slices) acc = acc + mybuf[l + 32 * j];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 32);
+    if ((lane & 31) == 0 && (mine == 0 || two)) p.y[(int64_t)blockIdx.y * p.ldy + row0 + mine] = acc;
+}
+
+// Q4_K at a 256 step (amd-nv-cpu.ll:1545-1733). Lane i decodes chunk i of a
+// pass: quarter i%4 of block i/4, whose two sub-blocks give the quarter's
+// exact ints (scale times dot, minimum times code sum). Each pass leaves, per
+// row and block, the four quarters' ints and the block's two scales in the
+// wave's LDS row (ten words per block); lanes 0 and 1 (first row) and 32 and
+// 33 (second row) then run the acc and accmin fma chains in block order.
+__device__ __forceinline__ void q4k256_ints(const ChunkData<Q4_K>& D, int c, const int8_t* xc, const float* xd,
+                                            float* out) {
+    int dq = 0, mq = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int g = 2 * (c & 3) + j;
+        int sc, m;
+        q4k_scale_min(D.meta, g, sc, m);
+        const uint4 x0 = record_bytes(xc, 4 * c + 2 * j), x1 = record_bytes(xc, 4 * c + 2 * j + 1);
+        dq += sc * (q4_dot(word(D.q[j], 0), word(D.q[j], 1), x0) + q4_dot(word(D.q[j], 2), word(D.q[j], 3), x1));
+        mq += m * (code_sum(x0) + code_sum(x1));
+    }
+    float* blk = out + (c & 63) / 4 * 10;
+    blk[2 * (c & 3)] = __builtin_bit_cast(float, dq);
+    blk[2 * (c & 3) + 1] = __builtin_bit_cast(float, mq);
+    if ((c & 3) == 0) {
+        const float d8 = xd[(c >> 2) * 8];
+        blk[8] = half_lo(D.meta.x) * d8;
+        blk[9] = half_hi(D.meta.x) * d8;
     }
 }
 
-// Q4_K at a 256 step (amd-nv-cpu.ll:1545-1733): lanes 0-15 of a half take the
-// sixteen slices of one block and lanes 16-31 those of the next.
 __global__ __launch_bounds__(kI8Threads) void int8_q4k256_kernel(I8Launch p) {
     int8_t* xc;
     float* xd;
-    stage_records(p, 256, xc, xd);
-    const int half = (int)threadIdx.x >> 5, lane = (int)threadIdx.x & 31, l = lane & 15, side = lane >> 4;
+    float* rowbuf;
+    stage_records(p, 256, xc, xd, rowbuf);
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int64_t row0 = (int64_t)blockIdx.x * kI8Rows + 2 * wave;
+    if (row0 >= p.rows) return;
+    const bool two = row0 + 1 < p.rows;
     const int m = (int)blockIdx.y;
     const bool whole = m >= p.M - (p.M & 3) || (p.tail && m == p.M - 1);
-    const int nblk = p.K >> 8;
-    for (int i = 0; i < kI8RowsPerHalf; ++i) {
-        const int64_t row = (int64_t)blockIdx.x * kI8Rows + i * kI8Halves + half;
-        if (row >= p.rows) break;
-        const uint8_t* rowp = p.w + row * p.row_bytes;
-        float acc = 0.f, accmin = 0.f;
-        for (int b0 = 0; b0 < nblk; b0 += 2) {
-            const int b = b0 + side;
-            int di = 0, mi = 0;
-            float scale = 0.f, dscale = 0.f;
-            if (b < nblk) {
-                const int s = b * 16 + l;
-                uint4 meta;
-                const SliceInts t = q4k_slice(rowp, p.nch, s, *reinterpret_cast<const uint4*>(xc + s * 16), meta);
-                int sc, mn;
-                q4k_scale_min(meta, l >> 1, sc, mn);
-                di = sc * t.dot;
-                mi = mn * t.sum;
-                const float d8 = xd[b * 8];
-                scale = half_lo(meta.x) * d8;
-                dscale = half_hi(meta.x) * d8;
-            }
-            // Quarter sums (four slices each, exact) at lanes 4q of each side.
-            di += __shfl_xor(di, 1, 32);
-            mi += __shfl_xor(mi, 1, 32);
-            di += __shfl_xor(di, 2, 32);
-            mi += __shfl_xor(mi, 2, 32);
-            const float s0 = __shfl(scale, 0, 32), ds0 = __shfl(dscale, 0, 32);
-            const float s1 = __shfl(scale, 16, 32), ds1 = __shfl(dscale, 16, 32);
-            if (whole) {
-                di += __shfl_xor(di, 4, 32);
-                mi += __shfl_xor(mi, 4, 32);
-                di += __shfl_xor(di, 8, 32);
-                mi += __shfl_xor(mi, 8, 32);
-                acc = fmaf((float)__shfl(di, 0, 32), s0, acc);
-                accmin = fmaf((float)__shfl(mi, 0, 32), ds0, accmin);
-                if (b0 + 1 < nblk) {
-                    acc = fmaf((float)__shfl(di, 16, 32), s1, acc);
-                    accmin = fmaf((float)__shfl(mi, 16, 32), ds1, accmin);
-                }
-            } else {
+    const int nch = p.P.nch;
+    const int chain = lane & 1;                        // 0: acc, 1: accmin
+    const float* mine = rowbuf + 256 * (lane >> 5);  // the row this lane's chain belongs to
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int c = c0 + lane;
+        ChunkData<Q4_K> A, B;
+        if (c < nch) {
+            load_chunk<Q4_K>(p.P, row0, c, A);
+            if (two) load_chunk<Q4_K>(p.P, row0 + 1, c, B);
+            q4k256_ints(A, c, xc, xd, rowbuf);
+            if (two) q4k256_ints(B, c, xc, xd, rowbuf + 256);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if ((lane & 31) < 2) {
+            const int blocks = min(16, (nch - c0) >> 2);
+            for (int b = 0; b < blocks; ++b) {
+                const float* blk = mine + b * 10;
+                const float s = blk[8 + chain];
+                if (whole) {
+                    const int w = (__builtin_bit_cast(int, blk[chain]) + __builtin_bit_cast(int, blk[2 + chain])) +
+                                  (__builtin_bit_cast(int, blk[4 + chain]) + __builtin_bit_cast(int, blk[6 + chain]));
+                    acc = fmaf((float)w, s, acc);
+                } else {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    acc = fmaf((float)__shfl(di, 4 * q, 32), s0, acc);
-                    accmin = fmaf((float)__shfl(mi, 4 * q, 32), ds0, accmin);
-                }
-                if (b0 + 1 < nblk) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        acc = fmaf((float)__shfl(di, 16 + 4 * q, 32), s1, acc);
-                        accmin = fmaf((float)__shfl(mi, 16 + 4 * q, 32), ds1, accmin);
-                    }
+                    for (int q = 0; q < 4; ++q) acc = fmaf((float)__builtin_bit_cast(int, blk[2 * q + chain]), s, acc);
                 }
             }
         }
-        if (lane == 0) p.y[(int64_t)m * p.ldy + row] = acc - accmin;
+        __builtin_amdgcn_wave_barrier();
+    }
+    const float other = __shfl_xor(acc, 1);
+    if (lane == 0) p.y[(int64_t)m * p.ldy + row0] = acc - other;
+    if (lane == 32 && two) p.y[(int64_t)m * p.ldy + row0 + 1] = acc - other;
+}
+
+// Q6_K at a 256 step (amd-nv-cpu.ll:1836-2031, build.rs:871-884). Lane i
+// decodes chunk i of a pass: quarter i%4 of block i/4, slices 4(i%4)+t. Chain
+// k takes word k%4 of the slices with parity k/4 (the four-value words at 4k
+// of every 32-value group) and -32 times the scaled code sums of group k. The
+// quads' exact sums give each block's eight chain ints, left with the block's
+// scale in the wave's LDS row (nine words per block); lanes 0-7 (first row)
+// and 32-39 (second row) each run one chain's fmas in block order.
+__device__ __forceinline__ void q6k256_ints(const ChunkData<Q6_K>& D, int c, const int8_t* xc, const float* xd,
+                                            float* out) {
+    const int qq = c & 3;
+    int I[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int G0 = 0, G1 = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint4 x = record_bytes(xc, 4 * c + t);
+        const int sc = sbfe(D.meta.x, 8 * t, 8);
+        uint32_t q[4];
+        q6_words(D, t, q);
+        I[(t & 1) * 4 + 0] += sc * sdot4(q[0], x.x, 0);
+        I[(t & 1) * 4 + 1] += sc * sdot4(q[1], x.y, 0);
+        I[(t & 1) * 4 + 2] += sc * sdot4(q[2], x.z, 0);
+        I[(t & 1) * 4 + 3] += sc * sdot4(q[3], x.w, 0);
+        const int g = -32 * (sc * code_sum(x));
+        if (t < 2)
+            G0 += g;
+        else
+            G1 += g;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        I[k] += (k == 2 * qq ? G0 : 0) + (k == 2 * qq + 1 ? G1 : 0);
+        I[k] = quad_sum(I[k]);
+    }
+    if (qq == 0) {
+        float* blk = out + (c & 63) / 4 * 9;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) blk[k] = __builtin_bit_cast(float, I[k]);
+        blk[8] = xd[(c >> 2) * 8] * half_lo(D.meta.y);
     }
 }
 
-// Q6_K at a 256 step (amd-nv-cpu.ll:1836-2031, build.rs:871-884): lanes 0-15
-// of a half take the slices of one block, 16-31 the next. Chain c takes word
-// c%4 of the slices with parity c/4 (the four-value words at 4c of every
-// 32-value group) and -32 times the scaled code sums of group c.
 __global__ __launch_bounds__(kI8Threads) void int8_q6k256_kernel(I8Launch p) {
     int8_t* xc;
     float* xd;
-    stage_records(p, 256, xc, xd);
-    const int half = (int)threadIdx.x >> 5, lane = (int)threadIdx.x & 31, l = lane & 15, side = lane >> 4;
-    const int chain = l & 7;
-    const int nblk = p.K >> 8;
-    for (int i = 0; i < kI8RowsPerHalf; ++i) {
-        const int64_t row = (int64_t)blockIdx.x * kI8Rows + i * kI8Halves + half;
-        if (row >= p.rows) break;
-        const uint8_t* rowp = p.w + row * p.row_bytes;
-        float f = 0.f;  // chain `chain`
-        for (int b0 = 0; b0 < nblk; b0 += 2) {
-            const int b = b0 + side;
-            int W[4] = {0, 0, 0, 0}, G = 0;
-            float scale = 0.f;
-            if (b < nblk) {
-                const int s = b * 16 + l;
-                const uint4 c = *reinterpret_cast<const uint4*>(xc + s * 16);
-                int sc, words[4];
-                float d;
-                q6k_slice(rowp, p.nch, s, c, sc, d, words);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) W[k] = sc * words[k];
-                G = -32 * (sc * code_sum(c));
-                scale = xd[b * 8] * d;
-            }
-#pragma unroll
-            for (int off = 2; off < 16; off <<= 1)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) W[k] += __shfl_xor(W[k], off, 32);
-            G += __shfl_xor(G, 1, 32);
-            const int srcw = (lane & 16) + (chain >> 2);
-            const int w0 = __shfl(W[0], srcw, 32), w1 = __shfl(W[1], srcw, 32);
-            const int w2 = __shfl(W[2], srcw, 32), w3 = __shfl(W[3], srcw, 32);
-            const int k = chain & 3;
-            const int wpart = k == 0 ? w0 : (k == 1 ? w1 : (k == 2 ? w2 : w3));
-            const int ic = wpart + __shfl(G, (lane & 16) + 2 * chain, 32);
-            const int i0 = __shfl(ic, chain, 32), i1 = __shfl(ic, 16 + chain, 32);
-            f = fmaf(__shfl(scale, 0, 32), (float)i0, f);
-            if (b0 + 1 < nblk) f = fmaf(__shfl(scale, 16, 32), (float)i1, f);
+    float* rowbuf;
+    stage_records(p, 256, xc, xd, rowbuf);
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int64_t row0 = (int64_t)blockIdx.x * kI8Rows + 2 * wave;
+    if (row0 >= p.rows) return;
+    const bool two = row0 + 1 < p.rows;
+    const int nch = p.P.nch;
+    const int chain = lane & 7;
+    const float* mine = rowbuf + 256 * (lane >> 5);
+    float f = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int c = c0 + lane;
+        ChunkData<Q6_K> A, B;
+        if (c < nch) {  // whole quads: nch is a multiple of four
+            load_chunk<Q6_K>(p.P, row0, c, A);
+            if (two) load_chunk<Q6_K>(p.P, row0 + 1, c, B);
+            q6k256_ints(A, c, xc, xd, rowbuf);
+            if (two) q6k256_ints(B, c, xc, xd, rowbuf + 256);
         }
-        const float t = f + __shfl_xor(f, 4, 32);
-        const float u = t + __shfl_xor(t, 2, 32);
-        const float total = u + __shfl_xor(u, 1, 32);
-        if (lane == 0) p.y[(int64_t)blockIdx.y * p.ldy + row] = total;
+        __builtin_amdgcn_wave_barrier();
+        if ((lane & 31) < 8) {
+            const int blocks = min(16, (nch - c0) >> 2);
+            for (int b = 0; b < blocks; ++b) {
+                const float* blk = mine + b * 9;
+                f = fmaf(blk[8], (float)__builtin_bit_cast(int, blk[chain]), f);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
     }
+    const float t = f + __shfl_xor(f, 4);
+    const float u = t + __shfl_xor(t, 2);
+    const float total = u + __shfl_xor(u, 1);
+    if (lane == 0) p.y[(int64_t)blockIdx.y * p.ldy + row0] = total;
+    if (lane == 32 && two) p.y[(int64_t)blockIdx.y * p.ldy + row0 + 1] = total;
 }
 
+// The records of one row, staged as the products stage them, then copied out.
 __global__ __launch_bounds__(kI8Threads) void q8_records_kernel(const float* x, int K, int step, float* d,
                                                                 int8_t* codes) {
-    q8_records(x, K, step, d, codes, (int)threadIdx.x, kI8Threads);
+    extern __shared__ __align__(16) uint8_t i8_lds[];
+    int8_t* xc = reinterpret_cast<int8_t*>(i8_lds);
+    float* xd = reinterpret_cast<float*>(i8_lds + K);
+    q8_records(x, K, step, xd, xc, xd + (K >> 5), (int)threadIdx.x, kI8Threads);
+    for (int i = (int)threadIdx.x; i < K; i += kI8Threads) codes[i] = xc[i];
+    for (int i = (int)threadIdx.x; i < (K >> 5); i += kI8Threads) d[i] = xd[i];
 }
 
 }  // namespace
 
-size_t int8_lds_bytes(int64_t cols) { return (size_t)cols + (size_t)(cols / 32) * 4; }
+// codes, steps, per-step inverses (rounded up to 16 bytes), then 2 KiB of
+// slice values per wave.
+size_t int8_lds_bytes(int64_t cols) {
+    const size_t tail = (size_t)(cols / 32) + (size_t)((cols + 255) / 256);
+    return (size_t)cols + ((tail + 3) & ~size_t(3)) * 4 + (size_t)(kI8Threads / 64) * 2048;
+}
 
 hipError_t launch_matvec_int8(int fmt, const Planes& P, int64_t rows, int K, const float* x, int M, int64_t ldx,
                               float* y, int64_t ldy, int step, int tail, hipStream_t stream) {
-    I8Launch p{P.base, P.row_bytes, P.nch, rows, K, x, ldx, y, ldy, M, step, tail};
+    I8Launch p{P, rows, K, x, ldx, y, ldy, M, step, tail};
     const dim3 grid((unsigned)((rows + kI8Rows - 1) / kI8Rows), (unsigned)M);
     const size_t lds = int8_lds_bytes(K);
     const bool blocks256 = step == 256 && (fmt == Q4_K || fmt == Q6_K);
@@ -412,7 +554,7 @@ hipError_t launch_matvec_int8(int fmt, const Planes& P, int64_t rows, int K, con
 }
 
 hipError_t launch_q8_records(const float* x, int K, int step, float* d, int8_t* codes, hipStream_t stream) {
-    hipLaunchKernelGGL(q8_records_kernel, dim3(1), dim3(kI8Threads), 0, stream, x, K, step, d, codes);
+    hipLaunchKernelGGL(q8_records_kernel, dim3(1), dim3(kI8Threads), int8_lds_bytes(K), stream, x, K, step, d, codes);
     return hipGetLastError();
 }
 

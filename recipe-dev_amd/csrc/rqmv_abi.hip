@@ -578,7 +578,8 @@ int rqmv_matvec_int8(const rqmv_weight* w, const float* x_dev, int m, int64_t ld
     if (m <= 0 || m > 65535) return fail(RQMV_EINVAL, "int8: m must be in 1..65535");
     const int64_t rows = w->rows * w->experts;
     if (ldx < w->cols || ldy < rows) return fail(RQMV_EINVAL, "int8: ldx < cols or ldy < rows");
-    if (reinterpret_cast<uintptr_t>(x_dev) % 4 != 0) return fail(RQMV_EINVAL, "int8: x must be 4-byte aligned");
+    if (reinterpret_cast<uintptr_t>(x_dev) % 16 != 0 || ldx % 4 != 0)
+        return fail(RQMV_EINVAL, "int8: x must be 16-byte aligned and ldx a multiple of 4");
     if (rq::int8_lds_bytes(w->cols) > info.lds_limit) return fail(RQMV_EINVAL, "int8: cols too large for the LDS records");
     hipError_t e = rq::launch_matvec_int8(w->fmt, planes_of(w, 0), rows, (int)w->cols, x_dev, m, ldx, y_dev, ldy, step,
                                           (flags & RQMV_INT8_TAIL) ? 1 : 0, static_cast<hipStream_t>(stream));
@@ -588,6 +589,11 @@ int rqmv_matvec_int8(const rqmv_weight* w, const float* x_dev, int m, int64_t ld
 int rqmv_q8_records(const float* x_dev, int64_t k, int step, float* d_dev, int8_t* codes_dev, void* stream) {
     if (!x_dev || !d_dev || !codes_dev) return fail(RQMV_EINVAL, "q8_records: NULL argument");
     if (k <= 0 || k % 32 != 0 || k > (1 << 24)) return fail(RQMV_EINVAL, "q8_records: k must be a positive multiple of 32");
+    if (reinterpret_cast<uintptr_t>(x_dev) % 16 != 0) return fail(RQMV_EINVAL, "q8_records: x must be 16-byte aligned");
+    DeviceInfo info;
+    const int dev = current_device(&info);
+    if (dev < 0) return dev;
+    if (rq::int8_lds_bytes(k) > info.lds_limit) return fail(RQMV_EINVAL, "q8_records: k too large for the LDS records");
     if (step != 32 && step != 256) return fail(RQMV_EINVAL, "q8_records: step must be 32 or 256");
     hipError_t e = rq::launch_q8_records(x_dev, (int)k, step, d_dev, codes_dev, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? RQMV_OK : hip_fail(e, "q8_records launch");
