@@ -131,6 +131,55 @@ __device__ __forceinline__ float sum_lanes(float v) {
     return v;
 }
 
+// v combined with the value of lane ^ 16 and of lane ^ 32 through gfx950's
+// VALU lane swaps (no LDS crossbar): v_permlane16_swap_b32 / 32 exchange odd
+// 16-lane rows (upper 32 lanes) of the first register with even rows (lower
+// 32 lanes) of the second; applied to two copies of v they leave, in every
+// lane, the lower lane's value in the first and the upper lane's in the
+// second. Written as inline assembly: this compiler's builtin loses the second
+// result. The s_nop gives the wait states a VALU write needs before the swap
+// reads it.
+struct LanePair {
+    float lo, hi;
+};
+__device__ __forceinline__ LanePair swap16(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return LanePair{a, b};
+}
+__device__ __forceinline__ LanePair swap32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return LanePair{a, b};
+}
+__device__ __forceinline__ float swap16_sum(float v) {
+    const LanePair p = swap16(v);
+    return p.lo + p.hi;
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+    const LanePair p = swap32(v);
+    return p.lo + p.hi;
+}
+__device__ __forceinline__ float swap16_max(float v) {
+    const LanePair p = swap16(v);
+    return fmaxf(p.lo, p.hi);
+}
+__device__ __forceinline__ float swap32_max(float v) {
+    const LanePair p = swap32(v);
+    return fmaxf(p.lo, p.hi);
+}
+
+// Maximum and sum over the 64 lanes of a wave, every lane getting the result:
+// DPP within rows of 16, then the two lane swaps.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false)));
+    return swap32_max(swap16_max(v));
+}
+__device__ __forceinline__ float wave_sum(float v) { return swap32_sum(swap16_sum(sum_lanes<16>(v))); }
+
 struct AttnWork {
     float* ml;  // [nq][nchunks][2]
     float* o;   // [nq][nchunks][hd]
@@ -272,12 +321,10 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     // pass 2: per query head, the chunk's maximum, weights and their sum (one position per lane)
     for (int g = wave; g < group; g += kAttnWaves) {
         const float s = sc[g][lane];
-        float m = s;
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float m = wave_max(s);
         const float e = s == -INFINITY ? 0.f : __expf(s - m);
         sc[g][lane] = e;
-        float l = e;
-        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+        const float l = wave_sum(e);
         if (lane == 0) {
             ml[g][0] = m;
             ml[g][1] = l;
@@ -310,8 +357,11 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 #pragma unroll
     for (int g = 0; g < MAXG; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            for (int off = LPP; off < 64; off <<= 1) o[g][e] += __shfl_xor(o[g][e], off);
+        for (int e = 0; e < 8; ++e) {
+            if constexpr (LPP <= 8) o[g][e] += __shfl_xor(o[g][e], 8);
+            if constexpr (LPP <= 16) o[g][e] = swap16_sum(o[g][e]);
+            o[g][e] = swap32_sum(o[g][e]);
+        }
     if (lane < LPP) {
 #pragma unroll
         for (int g = 0; g < MAXG; ++g)
