@@ -244,6 +244,21 @@ enum { RQMV_INT8_TAIL = 1 };
 int rqmv_matvec_int8(const rqmv_weight* weight, const float* x_dev, int m, int64_t ldx, float* y_dev, int64_t ldy,
                      int step, int flags, void* stream);
 
+/* A weight in the storage recipe's int(8) profile gives it (finish_int_sums
+ * and requantize_bound, recipe.rs:22327-22437): Q4_K and Q8_0 are kept as they
+ * are; F16, Q4_0 and Q6_K are re-encoded to Q8_0 as recipe's load kernel does
+ * (the device Q8_0 quantizer, recipe.rs:8016-8080: per 32 values scale =
+ * |first largest| / 127, code = trunc(v / scale +- 0.5) clamped, d = fp16
+ * of the scale), here on the host, once. rqmv_weight_info reports the stored
+ * format. experts = 1 for a plain weight. */
+int rqmv_weight_create_int8(int format, int64_t experts, int64_t rows, int64_t cols, const void* gguf_bytes,
+                            size_t nbytes, rqmv_weight** out);
+
+/* That re-encoding alone, host to host: rows x cols GGUF weights of `format`
+ * (F16, Q8_0, Q4_0 or Q6_K) -> rows * cols / 32 Q8_0 blocks (34 bytes each). */
+int rqmv_requantize_q8_0_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, size_t nbytes,
+                              void* out);
+
 /* The Q8 records of one activation row of k inputs (k a multiple of 32, x
  * 16-byte aligned) that rqmv_matvec_int8 forms in LDS (amd-nv-cpu.ll:1408-1500): d_dev[k/32] steps
  * (one value per `step` inputs, repeated per 32) and codes_dev[k] bytes. */

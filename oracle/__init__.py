@@ -51,6 +51,9 @@ def lib():
         L.orc_q4k_xorshift_rows.argtypes = [c_uint32, c_int64, c_uint16, c_void_p]
         L.orc_q8_records.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_void_p]
         L.orc_int8_matvec.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int, c_int, c_void_p]
+        L.orc_fp16_rne.argtypes = [c_float]
+        L.orc_fp16_rne.restype = c_uint16
+        L.orc_requantize_q8_0.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p]
         _lib = L
     return _lib
 
@@ -173,3 +176,12 @@ def int8_matvec(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray, step
                                1 if tail else 0, y.ctypes.data)
     assert rc == 0, rc
     return y
+
+
+def requantize_q8_0(fmt, gguf: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """recipe's int(8) storage for a non-Q4_K weight: the Q8_0 blocks (uint8)."""
+    g = _as_bytes(gguf)
+    out = np.empty(rows * (cols // 32) * 34, np.uint8)
+    rc = lib().orc_requantize_q8_0(_fmt(fmt), g.ctypes.data, rows, cols, out.ctypes.data)
+    assert rc == 0, rc
+    return out

@@ -749,3 +749,65 @@ int orc_int8_matvec(int format, const uint8_t* bytes, int64_t rows, int64_t cols
     free(rc);
     return 0;
 }
+
+/* IEEE binary16 encode with round half to even, subnormals and overflow to
+ * infinity (what LLVM's fptrunc float -> half does on recipe's device). */
+uint16_t orc_fp16_rne(float value) {
+    uint32_t x;
+    memcpy(&x, &value, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t a = x & 0x7fffffffu;
+    if (a >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0u));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 */
+    if (a < 0x38800000u) {                                   /* below 2^-14 */
+        const int e = (int)(a >> 23);
+        if (e < 102) return sign;
+        const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        const int shift = 126 - e;
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = (a >> 13) - (112u << 10);
+    const uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+}
+
+/* recipe.rs:8016-8080 (emit_requantize, DeviceQuantizer::Q8_0) over the
+ * decoded weight, 32 values at a time. */
+int orc_requantize_q8_0(int format, const uint8_t* bytes, int64_t rows, int64_t cols, uint8_t* out) {
+    if (format != 1 && format != 2 && format != 8 && format != 14) return -1;
+    if (!shape_ok(format, rows, cols) || cols % 32 != 0) return -1;
+    const int bv = orc_block_values(format), bb = orc_block_bytes(format);
+    const int64_t rbytes = row_bytes_of(format, cols);
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint8_t* row = bytes + r * rbytes;
+        for (int64_t b = 0; b < cols / 32; ++b) {
+            float v[32];
+            for (int i = 0; i < 32; ++i) {
+                const int64_t k = b * 32 + i;
+                v[i] = (float)orc_dequant_value(format, row + (k / bv) * bb, (int)(k % bv));
+            }
+            float e = 0.0f;
+            for (int i = 0; i < 32; ++i)
+                if (fabsf(v[i]) > fabsf(e)) e = v[i];
+            const float scale = fabsf(e) / 127.0f;
+            const float inverse = scale == 0.0f ? 0.0f : 1.0f / scale;
+            uint8_t* blk = out + (r * (cols / 32) + b) * 34;
+            const uint16_t d = orc_fp16_rne(scale);
+            blk[0] = (uint8_t)(d & 0xff);
+            blk[1] = (uint8_t)(d >> 8);
+            for (int i = 0; i < 32; ++i) {
+                const float q = v[i] * inverse;
+                const float rounded = q >= 0.0f ? q + 0.5f : q + -0.5f;
+                int c = (int)rounded; /* toward zero */
+                if (c < -128) c = -128;
+                if (c > 127) c = 127;
+                blk[2 + i] = (uint8_t)(int8_t)c;
+            }
+        }
+    }
+    return 0;
+}

@@ -110,6 +110,19 @@ int orc_q8_records(const float* x, int64_t k, int step, float* d, int8_t* codes)
 int orc_int8_matvec(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const float* x, int m_count,
                     int step, int tail, float* y);
 
+/* IEEE binary16 encode, round half to even (LLVM's fptrunc float -> half). */
+uint16_t orc_fp16_rne(float value);
+
+/* The storage recipe's int(8) profile gives a bound weight that is not Q4_K or
+ * Q8_0 (finish_int_sums + requantize_bound, recipe.rs:22327-22437): each
+ * 32-value block of the decoded weight re-encoded as Q8_0 by the device
+ * quantizer (recipe.rs:8016-8080): extreme = first value of largest magnitude,
+ * scale = |extreme| / 127, inverse = 1 / scale (0 for a zero scale), code =
+ * clamp(trunc(v * inverse + (v * inverse >= 0 ? 0.5 : -0.5)), -128, 127),
+ * d = fp16(scale) rounded half to even. Sources Q4_0, Q6_K, F16 and Q8_0
+ * (whose values decode exactly in fp32). out: rows * cols / 32 * 34 bytes. */
+int orc_requantize_q8_0(int format, const uint8_t* bytes, int64_t rows, int64_t cols, uint8_t* out);
+
 #ifdef __cplusplus
 }
 #endif

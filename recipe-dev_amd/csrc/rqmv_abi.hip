@@ -13,6 +13,7 @@
 #include "gguf.h"
 #include "moe.h"
 #include "repack.h"
+#include "requant.h"
 
 struct rqmv_weight {
     int fmt;
@@ -226,6 +227,35 @@ int rqmv_weight_create(int format, int64_t rows, int64_t cols, const void* gguf_
 int rqmv_expert_bank_create(int format, int64_t experts, int64_t rows, int64_t cols, const void* gguf_bytes,
                             size_t nbytes, rqmv_weight** out) {
     return create(format, experts, rows, cols, gguf_bytes, nbytes, out);
+}
+
+int rqmv_requantize_q8_0_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, size_t nbytes,
+                              void* out) {
+    if (!gguf_bytes || !out) return fail(RQMV_EINVAL, "requantize: NULL argument");
+    if (!rq::requantizable_to_q8_0(format)) return fail(RQMV_EINVAL, "requantize: the source must be F16, Q8_0, Q4_0 or Q6_K");
+    const int64_t want = rq::gguf_bytes(format, rows, cols);
+    if (want < 0 || cols % 32 != 0) return fail(RQMV_EINVAL, "requantize: cols is not a whole number of blocks");
+    if ((size_t)want != nbytes)
+        return fail(RQMV_EINVAL, "requantize: expected " + std::to_string(want) + " GGUF bytes, got " + std::to_string(nbytes));
+    if (rq::requantize_q8_0(format, rows, cols, static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(out)) != 0)
+        return fail(RQMV_EINVAL, "requantize failed");
+    return RQMV_OK;
+}
+
+int rqmv_weight_create_int8(int format, int64_t experts, int64_t rows, int64_t cols, const void* gguf_bytes,
+                            size_t nbytes, rqmv_weight** out) {
+    if (!out) return fail(RQMV_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (format == rq::Q4_K || format == rq::Q8_0) return create(format, experts, rows, cols, gguf_bytes, nbytes, out);
+    if (experts <= 0 || rows <= 0) return fail(RQMV_EINVAL, "shape must be positive");
+    const int64_t total = experts * rows;
+    std::vector<uint8_t> q8;
+    const int64_t q8_bytes = rq::gguf_bytes(rq::Q8_0, total, cols);
+    if (q8_bytes < 0) return fail(RQMV_EINVAL, "cols is not a whole number of Q8_0 blocks");
+    q8.resize((size_t)q8_bytes);
+    const int rc = rqmv_requantize_q8_0_host(format, total, cols, gguf_bytes, nbytes, q8.data());
+    if (rc != RQMV_OK) return rc;
+    return create(rq::Q8_0, experts, rows, cols, q8.data(), q8.size(), out);
 }
 
 int rqmv_glu_weight_create(int format, int64_t rows, int64_t cols, const void* gate_gguf, const void* up_gguf,

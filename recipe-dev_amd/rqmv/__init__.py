@@ -66,6 +66,8 @@ class _Lib:
         L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_void_p]
         L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
+        L.rqmv_weight_create_int8.argtypes = [c_int, c_int64, c_int64, c_int64, c_void_p, c_size_t, POINTER(c_void_p)]
+        L.rqmv_requantize_q8_0_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_size_t, c_void_p]
         L.rqmv_matvec_int8.argtypes = [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_int, c_int, c_void_p]
         L.rqmv_q8_records.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p]
         L.rqmv_embed_row.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]
@@ -373,6 +375,31 @@ def matvec_int8(weight: Weight, x: DeviceBuffer, m: int, ldx: int, y: DeviceBuff
     of `step` inputs, recipe's fp32 order."""
     _check(lib().lib.rqmv_matvec_int8(weight.handle, x.ptr, m, ldx, y.ptr, ldy, step, INT8_TAIL if tail else 0,
                                       _sh(stream)), "rqmv_matvec_int8")
+
+
+def int8_weight(fmt, rows: int, cols: int, gguf: np.ndarray, experts: int | None = None) -> Weight:
+    """A weight stored as recipe's int(8) profile stores it (rqmv_weight_create_int8):
+    Q4_K and Q8_0 as they are, F16/Q4_0/Q6_K re-encoded to Q8_0."""
+    gguf = np.ascontiguousarray(gguf).view(np.uint8).reshape(-1)
+    h = c_void_p()
+    _check(lib().lib.rqmv_weight_create_int8(_fmt(fmt), experts or 1, rows, cols, gguf.ctypes.data, gguf.nbytes,
+                                             byref(h)), "rqmv_weight_create_int8")
+    w = Weight.__new__(Weight)
+    w.handle = h.value
+    w.rows, w.cols, w.experts = rows, cols, experts or 1
+    w.fmt = w.info()["format"]
+    w.gguf_nbytes = rows * (experts or 1) * cols // 32 * 34 if w.fmt == FORMATS["q8_0"] else gguf.nbytes
+    w.glu = False
+    return w
+
+
+def requantize_q8_0_host(fmt, rows: int, cols: int, gguf: np.ndarray) -> np.ndarray:
+    """rqmv_requantize_q8_0_host: the Q8_0 blocks recipe's int(8) profile stores."""
+    gguf = np.ascontiguousarray(gguf).view(np.uint8).reshape(-1)
+    out = np.empty(rows * (cols // 32) * 34, np.uint8)
+    _check(lib().lib.rqmv_requantize_q8_0_host(_fmt(fmt), rows, cols, gguf.ctypes.data, gguf.nbytes, out.ctypes.data),
+           "rqmv_requantize_q8_0_host")
+    return out
 
 
 def contract_int8(weight: Weight, x: np.ndarray, step: int = 32, tail: bool = False) -> np.ndarray:

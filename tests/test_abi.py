@@ -131,3 +131,43 @@ def test_last_error_names_the_failure():
     h = ctypes.c_void_p()
     rc = L.rqmv_weight_create(12, 4, 256, None, 0, ctypes.byref(h))
     assert rc == -1 and h.value is None
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "q8_0", "f16"])
+def test_host_requantize_q8_0_matches_oracle(fmt):
+    """The library's int(8) storage re-encoding (rqmv_requantize_q8_0_host)
+    against the oracle's restatement of recipe's device Q8_0 quantizer."""
+    import oracle
+
+    shapes = [(1, 256), (7, 512), (33, 4096)] if fmt in ("q6_k",) else [(1, 64), (9, 128), (33, 4096)]
+    for rows, cols in shapes:
+        if fmt == "f16":
+            w = synth.f16_weights(rows, cols, 0.02, seed=rows + cols)
+        else:
+            w = synth.weights(fmt, rows, cols, seed=rows + cols)
+        got = rqmv.requantize_q8_0_host(fmt, rows, cols, w)
+        assert np.array_equal(got, oracle.requantize_q8_0(fmt, w, rows, cols)), (fmt, rows, cols)
+
+
+def test_host_requantize_extremes():
+    import oracle
+
+    # zero blocks, ties of magnitude, tiny and large fp16 values through an F16 source
+    v = np.zeros((4, 64), np.float32)
+    v[1, :32] = 3.0
+    v[1, 5] = -3.0
+    v[2, :] = np.float32(6.1e-5)
+    v[2, 7] = np.float32(-65504.0)
+    v[3, :] = np.linspace(-1, 1, 64, dtype=np.float32) * np.float32(1e-3)
+    w = v.astype(np.float16).view(np.uint8).reshape(-1)
+    got = rqmv.requantize_q8_0_host("f16", 4, 64, w)
+    assert np.array_equal(got, oracle.requantize_q8_0("f16", w, 4, 64))
+    assert not got[:68].any()  # the zero row: d = 0 and zero codes
+
+
+def test_host_requantize_rejects_bad_arguments():
+    w = synth.q4_k(1, 256, seed=1)
+    with pytest.raises(rqmv.RqmvError, match="F16, Q8_0, Q4_0 or Q6_K"):
+        rqmv.requantize_q8_0_host("q4_k", 1, 256, w)
+    with pytest.raises(rqmv.RqmvError, match="expected"):
+        rqmv.requantize_q8_0_host("q4_0", 2, 64, synth.q4_0(1, 64, seed=1))

@@ -139,3 +139,21 @@ def test_argument_errors(gpu):
     F = gpu.Weight("f16", 4, 64, synth.f16_weights(4, 64, 0.02, seed=2))
     with pytest.raises(gpu.RqmvError, match="Q4_K, Q6_K, Q8_0 or Q4_0"):
         gpu.matvec_int8(F, xb, 1, 64, yb, 4, 32)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "f16", "q8_0", "q4_k"])
+@pytest.mark.parametrize("step", [32, 256])
+def test_int8_profile_storage(gpu, fmt, step):
+    """recipe's int(8) profile end to end: the weight in the storage the profile
+    gives it (Q4_K and Q8_0 kept, F16/Q4_0/Q6_K re-encoded to Q8_0), then the
+    int(8) product, bit for bit against the oracle's composition."""
+    rows, cols = 96, 1024
+    w = synth.f16_weights(rows, cols, 0.02, seed=6) if fmt == "f16" else synth.weights(fmt, rows, cols, seed=6)
+    W = gpu.int8_weight(fmt, rows, cols, w)
+    kept = fmt in ("q4_k", "q8_0")
+    assert W.info()["format"] == (gpu.FORMATS[fmt] if kept else gpu.FORMATS["q8_0"])
+    stored = w if kept else oracle.requantize_q8_0(fmt, w, rows, cols)
+    sfmt = fmt if kept else "q8_0"
+    x = np.stack([synth.activations_f32(cols, seed=20 + i) for i in range(2)])
+    assert _bits_equal(gpu.contract_int8(W, x, step), oracle.int8_matvec(sfmt, stored, rows, cols, x, step))
+    assert np.array_equal(W.unpack(), stored)

@@ -279,3 +279,70 @@ def test_256_step_blocks_meet_their_accumulator_with_fma(fmt):
     terms = np.abs(oracle.dequant_rows(fmt, one.reshape(-1), rows, 256).astype(np.float64)) @ np.abs(used)
     assert np.count_nonzero(got) >= rows - 1
     assert np.all(np.abs(got) <= terms * 2.0 ** -21)
+
+
+# ------------------------------------------- Q8_0 storage under int(8) ----
+
+def test_fp16_rne_matches_ieee():
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    edge = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, 2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0000001,
+                     2.0 ** -14, 2.0 ** -14 * (1 - 2.0 ** -12), 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 3.0e-8],
+                    np.float32)
+    for v in np.concatenate([vals, edge, -edge]):
+        want = np.array([v], np.float32).astype(np.float16).view(np.uint16)[0]
+        assert oracle.lib().orc_fp16_rne(float(v)) == want, v
+
+
+def _q8_block(d, codes):
+    return np.concatenate([np.array([np.float16(d)]).view(np.uint8), np.asarray(codes, np.int8).view(np.uint8)])
+
+
+def test_requantize_rounds_half_away_through_fp32():
+    # An F16 row holding 127 (scale 1, inverse 1) and halves: 2.5 -> 3, -2.5 -> -3,
+    # 1.5 -> 2, -0.5 -> -1 (round half away from zero, recipe.rs:8023, 8072-8078).
+    v = np.zeros(32, np.float32)
+    v[:6] = [127.0, 2.5, -2.5, 1.5, -0.5, -127.0]
+    out = oracle.requantize_q8_0("f16", v.astype(np.float16).view(np.uint8), 1, 32)
+    assert out[:2].view(np.float16)[0] == 1.0
+    assert list(out[2:8].view(np.int8)) == [127, 3, -3, 2, -1, -127]
+    # A Q8_0 source holding 127 and -128 (d = 1): the extreme is -128, the scale
+    # 128/127; 127 * (1/scale) = 126.0078 -> 126, -128 -> -127; d = fp16(128/127).
+    out = oracle.requantize_q8_0("q8_0", _q8_block(1.0, [127, -128] + [0] * 30), 1, 32)
+    assert out[:2].view(np.float16)[0] == np.float16(np.float32(128.0) / np.float32(127.0))
+    assert list(out[2:4].view(np.int8)) == [126, -127]
+
+
+def test_requantize_q8_0_is_idempotent_on_full_range_blocks():
+    rng = np.random.default_rng(9)
+    blocks = []
+    for _ in range(64):
+        codes = rng.integers(-127, 128, 32)
+        codes[rng.integers(0, 32)] = rng.choice([-127, 127])
+        d = np.float16(np.abs(rng.standard_normal()) * 0.01 + 1e-3)
+        blocks.append(_q8_block(d, codes))
+    w = np.concatenate(blocks)
+    assert np.array_equal(oracle.requantize_q8_0("q8_0", w, 8, 256), w)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "f16"])
+def test_requantize_error_bound(fmt):
+    rows, cols = 12, 512
+    w = synth.f16_weights(rows, cols, 0.02, seed=3) if fmt == "f16" else synth.weights(fmt, rows, cols, seed=3)
+    out = oracle.requantize_q8_0(fmt, w, rows, cols)
+    src = (synth.fp16_to_f32(w.view(np.uint16)).reshape(rows, cols) if fmt == "f16"
+           else oracle.dequant_rows(fmt, w, rows, cols)).astype(np.float64)
+    back = oracle.dequant_rows("q8_0", out, rows, cols).astype(np.float64)
+    blk = out.reshape(-1, 34)
+    d16 = blk[:, :2].copy().view(np.float16).astype(np.float64).reshape(rows, cols // 32)
+    scale = np.abs(src.reshape(rows, cols // 32, 32)).max(axis=2) / 127.0
+    codes = blk[:, 2:].view(np.int8).astype(np.float64).reshape(rows, cols // 32, 32)
+    # the codes are the scaled values rounded to within half a step (the step before its fp16 rounding) ...
+    assert np.all(np.abs(codes * scale[..., None] - src.reshape(rows, cols // 32, 32)) <= scale[..., None] * (0.5 + 1e-5))
+    # ... and the block's largest value takes code +-127
+    assert np.all(np.abs(codes).max(axis=2) == 127)
+    # the stored step is the fp16 rounding of the scale
+    assert np.array_equal(d16, scale.astype(np.float32).astype(np.float16).astype(np.float64))
+    assert np.allclose(back, src, atol=np.abs(src).max() / 127 * 0.51)
