@@ -244,6 +244,14 @@ enum { RQMV_INT8_TAIL = 1 };
 int rqmv_matvec_int8(const rqmv_weight* weight, const float* x_dev, int m, int64_t ldx, float* y_dev, int64_t ldy,
                      int step, int flags, void* stream);
 
+/* The gfx950 row of recipe's capability table (FormatCapability rows and
+ * resolve_capability, recipe.rs:2646-2745): for a compute format named as
+ * recipe names it ("int4", "int8", "int16", "int32", "fp8", "fp16", "fp32",
+ * "fp64", "bf16", "tf32"), the vector and matrix instructions this library
+ * uses (static strings; NULL where there is none). A format with neither is
+ * an error whose message lists the formats that have each, as recipe's. */
+int rqmv_capability(const char* format, const char** vector, const char** matrix);
+
 /* A weight in the storage recipe's int(8) profile gives it (finish_int_sums
  * and requantize_bound, recipe.rs:22327-22437): Q4_K and Q8_0 are kept as they
  * are; F16, Q4_0 and Q6_K are re-encoded to Q8_0 as recipe's load kernel does

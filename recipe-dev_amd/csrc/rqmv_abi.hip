@@ -229,6 +229,54 @@ int rqmv_expert_bank_create(int format, int64_t experts, int64_t rows, int64_t c
     return create(format, experts, rows, cols, gguf_bytes, nbytes, out);
 }
 
+// The gfx950 row of recipe's capability table (recipe.rs:2646-2738): per
+// compute format, the vector and matrix instructions this library runs it on.
+namespace {
+struct Capability {
+    const char* format;
+    const char* vector;
+    const char* matrix;
+};
+const Capability kGfx950[] = {
+    {"int4", nullptr, nullptr},
+    {"int8", "v_dot4_i32_i8 on Q8 activation records (rqmv_matvec_int8)", nullptr},
+    {"int16", nullptr, nullptr},
+    {"int32", nullptr, nullptr},
+    {"fp8", nullptr, nullptr},
+    {"fp16",
+     "v_dot8_i32_i4 / v_dot4_i32_i8 on exactly encoded activations, v_dot2_f32_f16 for F16 weights (rqmv_matvec)",
+     "v_mfma_f32_16x16x32_f16 on exact fp16 weight codes (rqmv_matvec, M >= 3)"},
+    {"fp32", "v_dot8_i32_i4 / v_dot4_i32_i8 on exactly encoded activations, fp32 fma for F16 weights (rqmv_matvec)",
+     "v_mfma_f32_16x16x32_f16 on exact fp16 weight codes, activations as fp16 high and low parts (rqmv_matvec, M >= 3)"},
+    {"fp64", nullptr, nullptr},
+    {"bf16", nullptr, nullptr},
+    {"tf32", nullptr, nullptr},
+};
+}  // namespace
+
+int rqmv_capability(const char* format, const char** vector, const char** matrix) {
+    if (!format || !vector || !matrix) return fail(RQMV_EINVAL, "capability: NULL argument");
+    *vector = nullptr;
+    *matrix = nullptr;
+    for (const Capability& c : kGfx950) {
+        if (std::strcmp(c.format, format) != 0) continue;
+        if (!c.vector && !c.matrix) {
+            std::string vectors, matrices;
+            for (const Capability& e : kGfx950) {
+                if (e.vector) vectors += std::string(vectors.empty() ? "" : " ") + e.format;
+                if (e.matrix) matrices += std::string(matrices.empty() ? "" : " ") + e.format;
+            }
+            return fail(RQMV_EINVAL, std::string("gfx950 has no ") + format + " instruction. Vector: " +
+                                         (vectors.empty() ? "none" : vectors) + ". Matrix: " +
+                                         (matrices.empty() ? "none" : matrices) + ".");
+        }
+        *vector = c.vector;
+        *matrix = c.matrix;
+        return RQMV_OK;
+    }
+    return fail(RQMV_EINVAL, std::string("gfx950 has no ") + format + " capability entry");
+}
+
 int rqmv_requantize_q8_0_host(int format, int64_t rows, int64_t cols, const void* gguf_bytes, size_t nbytes,
                               void* out) {
     if (!gguf_bytes || !out) return fail(RQMV_EINVAL, "requantize: NULL argument");

@@ -66,6 +66,7 @@ class _Lib:
         L.rqmv_argmax.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_void_p]
         L.rqmv_argmax_workspace_size.argtypes = [POINTER(c_size_t)]
         L.rqmv_advance.argtypes = [c_void_p, c_void_p]
+        L.rqmv_capability.argtypes = [ctypes.c_char_p, POINTER(ctypes.c_char_p), POINTER(ctypes.c_char_p)]
         L.rqmv_weight_create_int8.argtypes = [c_int, c_int64, c_int64, c_int64, c_void_p, c_size_t, POINTER(c_void_p)]
         L.rqmv_requantize_q8_0_host.argtypes = [c_int, c_int64, c_int64, c_void_p, c_size_t, c_void_p]
         L.rqmv_matvec_int8.argtypes = [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_int, c_int, c_void_p]
@@ -375,6 +376,14 @@ def matvec_int8(weight: Weight, x: DeviceBuffer, m: int, ldx: int, y: DeviceBuff
     of `step` inputs, recipe's fp32 order."""
     _check(lib().lib.rqmv_matvec_int8(weight.handle, x.ptr, m, ldx, y.ptr, ldy, step, INT8_TAIL if tail else 0,
                                       _sh(stream)), "rqmv_matvec_int8")
+
+
+def capability(fmt: str):
+    """(vector, matrix) instruction descriptions for a compute format on gfx950
+    (rqmv_capability); raises RqmvError where there is neither."""
+    v, m = ctypes.c_char_p(), ctypes.c_char_p()
+    _check(lib().lib.rqmv_capability(fmt.encode(), byref(v), byref(m)), "rqmv_capability")
+    return (v.value.decode() if v.value else None, m.value.decode() if m.value else None)
 
 
 def int8_weight(fmt, rows: int, cols: int, gguf: np.ndarray, experts: int | None = None) -> Weight:

@@ -171,3 +171,14 @@ def test_host_requantize_rejects_bad_arguments():
         rqmv.requantize_q8_0_host("q4_k", 1, 256, w)
     with pytest.raises(rqmv.RqmvError, match="expected"):
         rqmv.requantize_q8_0_host("q4_0", 2, 64, synth.q4_0(1, 64, seed=1))
+
+
+def test_capability_row_for_gfx950():
+    v, m = rqmv.capability("int8")
+    assert "v_dot4_i32_i8" in v and m is None
+    v, m = rqmv.capability("fp16")
+    assert "v_dot8_i32_i4" in v and "v_mfma_f32_16x16x32_f16" in m
+    with pytest.raises(rqmv.RqmvError, match=r"gfx950 has no fp8 instruction. Vector: int8 fp16 fp32. Matrix: fp16 fp32."):
+        rqmv.capability("fp8")
+    with pytest.raises(rqmv.RqmvError, match="no int7 capability entry"):
+        rqmv.capability("int7")
