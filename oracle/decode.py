@@ -87,20 +87,35 @@ class DecoderReference:
 
     def __init__(self, shape, embed, out_norm, head, layers, caches, max_ctx: int):
         s = self.shape = shape
-        self.embed = np.asarray(embed, dtype=np.float64)
+        if isinstance(embed, tuple):  # (format, blocks) of a quantized token_embd
+            self.embed = dequant_rows(embed[0], embed[1], s.vocab, s.d).reshape(s.vocab, s.d).astype(np.float64)
+        else:
+            self.embed = np.asarray(embed, dtype=np.float64)
         self.out_norm = np.asarray(out_norm, dtype=np.float64)
         self.head = dequant_rows(s.head_fmt, head, s.vocab, s.d).reshape(s.vocab, s.d).astype(np.float64)
         qkv_rows = (s.q_heads + 2 * s.kv_heads) * s.head_dim
         self.layers = []
+
+        def deq(fmt, blocks, rows, cols):
+            return dequant_rows(fmt, blocks, rows, cols).reshape(rows, cols).astype(np.float64)
+
         for t in layers:
+            # per-tensor formats (a Q4_K_M file) where the layer names them
+            fmts = getattr(t, "fmts", None) or {}
+            f = lambda name: fmts.get(name, s.proj_fmt)  # noqa: E731
+            parts = getattr(t, "qkv_parts", None)
+            if parts:
+                qkv = np.vstack([deq(fmt, blocks, rows, s.d) for fmt, rows, blocks in parts])
+            else:
+                qkv = deq(f("qkv"), t.qkv, qkv_rows, s.d)
             self.layers.append({
                 "attn_norm": np.asarray(t.attn_norm, dtype=np.float64),
-                "qkv": dequant_rows(s.proj_fmt, t.qkv, qkv_rows, s.d).reshape(qkv_rows, s.d).astype(np.float64),
-                "o": dequant_rows(s.proj_fmt, t.o, s.d, s.d).reshape(s.d, s.d).astype(np.float64),
+                "qkv": qkv,
+                "o": deq(f("o"), t.o, s.d, s.d),
                 "ffn_norm": np.asarray(t.ffn_norm, dtype=np.float64),
-                "gate": dequant_rows(s.proj_fmt, t.gate, s.ffn, s.d).reshape(s.ffn, s.d).astype(np.float64),
-                "up": dequant_rows(s.proj_fmt, t.up, s.ffn, s.d).reshape(s.ffn, s.d).astype(np.float64),
-                "down": dequant_rows(s.proj_fmt, t.down, s.d, s.ffn).reshape(s.d, s.ffn).astype(np.float64),
+                "gate": deq(f("gate"), t.gate, s.ffn, s.d),
+                "up": deq(f("up"), t.up, s.ffn, s.d),
+                "down": deq(f("down"), t.down, s.d, s.ffn),
             })
         self.k, self.v = [], []
         for kc, vc in caches:

@@ -190,6 +190,12 @@ class DeviceBuffer:
     def fill_zero(self):
         _hip(lib().hip.hipMemset(self.ptr, 0, self.nbytes), "hipMemset")
 
+    def view(self, offset: int, nbytes: int) -> "BufferView":
+        """A non-owning window [offset, offset + nbytes) of this allocation."""
+        if offset < 0 or nbytes < 0 or offset + nbytes > self.nbytes:
+            raise ValueError("view outside the buffer")
+        return BufferView(self, self.ptr + offset, nbytes)
+
     def close(self):
         if self.ptr:
             lib().hip.hipFree(self.ptr)
@@ -200,6 +206,14 @@ class DeviceBuffer:
             self.close()
         except Exception:
             pass
+
+
+class BufferView:
+    """Part of a DeviceBuffer, usable wherever a kernel takes a device pointer;
+    it keeps its parent alive and frees nothing itself."""
+
+    def __init__(self, parent: DeviceBuffer, ptr: int, nbytes: int):
+        self.parent, self.ptr, self.nbytes = parent, ptr, nbytes
 
 
 class Stream:

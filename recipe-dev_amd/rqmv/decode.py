@@ -66,28 +66,61 @@ class DecoderShape:
 class LayerTensors:
     """One layer's tensors as the file stores them: fp32 norm scales and GGUF
     blocks (rows of W_q, W_k, W_v stacked as one QKV projection; W_gate and
-    W_up as ffn_gate and ffn_up)."""
+    W_up as ffn_gate and ffn_up). Every projection is in the shape's proj_fmt
+    unless `fmts` names its own ("qkv", "o", "gate", "up", "down"). A QKV
+    projection whose parts differ in format (a Q4_K_M file's Q6_K attn_v) comes
+    as `qkv_parts`: (format, rows, blocks) for Q, K and V in order; consecutive
+    parts of one format run as one product."""
     attn_norm: np.ndarray
-    qkv: np.ndarray
+    qkv: np.ndarray | None
     o: np.ndarray
     ffn_norm: np.ndarray
     gate: np.ndarray
     up: np.ndarray
     down: np.ndarray
+    fmts: dict | None = None
+    qkv_parts: list | None = None
+
+    def fmt(self, name: str, default: str) -> str:
+        return (self.fmts or {}).get(name, default)
+
+    def qkv_runs(self, default: str, q_rows: int, kv_rows: int) -> list:
+        """[(format, rows, blocks)] for the QKV projection, runs of one format merged."""
+        parts = self.qkv_parts
+        if parts is None:
+            return [(self.fmt("qkv", default), q_rows + 2 * kv_rows, self.qkv)]
+        runs = []
+        for fmt, rows, blocks in parts:
+            blocks = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+            if runs and runs[-1][0] == fmt:
+                runs[-1] = (fmt, runs[-1][1] + rows, np.concatenate([runs[-1][2], blocks]))
+            else:
+                runs.append((fmt, rows, blocks))
+        if sum(r for _, r, _ in runs) != q_rows + 2 * kv_rows:
+            raise ValueError("qkv_parts must hold the Q, K and V rows")
+        return runs
 
 
 class DecodeModel:
     """The device state of one decoder: weights, caches and step buffers."""
 
-    def __init__(self, shape: DecoderShape, max_ctx: int, embed: np.ndarray, out_norm: np.ndarray,
-                 head: np.ndarray):
+    def __init__(self, shape: DecoderShape, max_ctx: int, embed, out_norm: np.ndarray, head: np.ndarray):
+        """embed: the fp32 table [vocab, d], or (format, GGUF blocks) of a
+        quantized token_embd, decoded once to fp32 on the device."""
         shape.validate()
         self.shape, self.max_ctx = shape, int(max_ctx)
         s = shape
-        embed = np.ascontiguousarray(embed, dtype=np.float32)
-        if embed.shape != (s.vocab, s.d):
-            raise ValueError(f"embedding table must be {(s.vocab, s.d)}, got {embed.shape}")
-        self.embed = DeviceBuffer.from_array(embed)
+        if isinstance(embed, tuple):
+            fmt, blocks = embed
+            table = Weight(fmt, s.vocab, s.d, blocks)
+            self.embed = DeviceBuffer(4 * s.vocab * s.d)
+            table.dequantize(self.embed)
+            table.close()
+        else:
+            embed = np.ascontiguousarray(embed, dtype=np.float32)
+            if embed.shape != (s.vocab, s.d):
+                raise ValueError(f"embedding table must be {(s.vocab, s.d)}, got {embed.shape}")
+            self.embed = DeviceBuffer.from_array(embed)
         self.out_norm = DeviceBuffer.from_array(np.ascontiguousarray(out_norm, dtype=np.float32))
         self.head = Weight(s.head_fmt, s.vocab, s.d, head)
         self.layers: list[dict | None] = [None] * s.layers
@@ -111,13 +144,20 @@ class DecodeModel:
     # ---------------------------------------------------------------- setup
     def set_layer(self, index: int, t: LayerTensors):
         s = self.shape
+        gate_fmt, up_fmt = t.fmt("gate", s.proj_fmt), t.fmt("up", s.proj_fmt)
+        if gate_fmt != up_fmt:
+            raise ValueError("ffn_gate and ffn_up must share a format (they run as one pair weight)")
+        runs, at = [], 0
+        for fmt, rows, blocks in t.qkv_runs(s.proj_fmt, s.q_heads * s.head_dim, s.kv_heads * s.head_dim):
+            runs.append((Weight(fmt, rows, s.d, blocks), self.qkv.view(4 * at, 4 * rows)))
+            at += rows
         self.layers[index] = {
             "attn_norm": DeviceBuffer.from_array(np.ascontiguousarray(t.attn_norm, dtype=np.float32)),
-            "qkv": Weight(s.proj_fmt, s.qkv_rows, s.d, t.qkv),
-            "o": Weight(s.proj_fmt, s.d, s.d, t.o),
+            "qkv": runs,
+            "o": Weight(t.fmt("o", s.proj_fmt), s.d, s.d, t.o),
             "ffn_norm": DeviceBuffer.from_array(np.ascontiguousarray(t.ffn_norm, dtype=np.float32)),
-            "gate_up": glu_weight(s.proj_fmt, s.ffn, s.d, t.gate, t.up),
-            "down": Weight(s.proj_fmt, s.d, s.ffn, t.down),
+            "gate_up": glu_weight(gate_fmt, s.ffn, s.d, t.gate, t.up),
+            "down": Weight(t.fmt("down", s.proj_fmt), s.d, s.ffn, t.down),
         }
 
     def set_cache(self, index: int, k: np.ndarray, v: np.ndarray):
@@ -148,12 +188,14 @@ class DecodeModel:
         embed_row(self.embed, s.vocab, s.d, self.token, xs[0], stream)
         cur, pending = 0, None  # pending: the down projection not yet added to the stream
         for i, L in enumerate(self.layers):
+            (w0, y0), rest = L["qkv"][0], L["qkv"][1:]
             if pending is None:
-                matvec_fused(L["qkv"], xs[cur], self.qkv, EPI_PLAIN, L["attn_norm"], s.eps, stream=stream)
+                matvec_fused(w0, xs[cur], y0, EPI_PLAIN, L["attn_norm"], s.eps, stream=stream)
             else:
-                matvec_fused(L["qkv"], xs[cur], self.qkv, EPI_PLAIN, L["attn_norm"], s.eps, pending, xs[1 - cur],
-                             stream=stream)
+                matvec_fused(w0, xs[cur], y0, EPI_PLAIN, L["attn_norm"], s.eps, pending, xs[1 - cur], stream=stream)
                 cur = 1 - cur
+            for w, y in rest:  # further format runs of Q, K, V read the updated stream
+                matvec_fused(w, xs[cur], y, EPI_PLAIN, L["attn_norm"], s.eps, stream=stream)
             attention_rope(self.qkv, self.rope, self.k_cache[i], self.v_cache[i], self.pos, s.q_heads, s.kv_heads,
                            s.head_dim, self.max_ctx, self.workspace, self.attn, stream)
             matvec_fused(L["o"], self.attn, self.y_o, EPI_PLAIN, stream=stream)
@@ -184,7 +226,7 @@ class DecodeModel:
         """GGUF bytes of every projection and the head (what one step streams)."""
         total = self.head.gguf_nbytes
         for L in self.layers:
-            total += sum(L[k].gguf_nbytes for k in ("qkv", "o", "gate_up", "down"))
+            total += sum(L[k].gguf_nbytes for k in ("o", "gate_up", "down")) + sum(w.gguf_nbytes for w, _ in L["qkv"])
         return total
 
 
@@ -213,8 +255,12 @@ def from_gguf(path: str, max_ctx: int) -> DecodeModel:
     (<arch>.block_count, embedding_length, attention.head_count(_kv),
     feed_forward_length, rope.freq_base (default 10000),
     attention.layer_norm_rms_epsilon (default 1e-5); recipe.rs:17806-17936).
-    Separate Q, K and V projections are stacked into one QKV weight, gate and
-    up become one pair weight; blocks are uploaded from the mapped file."""
+    Separate Q, K and V projections of one format are stacked into one QKV
+    weight (of different formats, as in a Q4_K_M file's Q6_K attn_v, they run
+    as consecutive products into the QKV vector); gate and up become one pair
+    weight; every projection keeps its own format; a quantized token_embd is
+    decoded to fp32 once on the device; blocks are uploaded from the mapped
+    file."""
     from . import Gguf
 
     g = Gguf(path)
@@ -255,18 +301,40 @@ def from_gguf(path: str, max_ctx: int) -> DecodeModel:
         embed = g.data("token_embd.weight").view(np.float32).reshape(vocab, d)
     elif embed_info.ggml_type == 1:
         embed = g.data("token_embd.weight").view(np.float16).astype(np.float32).reshape(vocab, d)
+    elif embed_info.ggml_type in _GGML_FORMAT:  # decoded to fp32 once, on the device
+        embed = (_GGML_FORMAT[embed_info.ggml_type], g.data("token_embd.weight"))
     else:
-        raise ValueError("token_embd.weight must be F32 or F16")
+        raise ValueError("token_embd.weight must be F32, F16, Q4_0, Q8_0, Q4_K or Q6_K")
     model = DecodeModel(shape, max_ctx, embed, _f32_vector(g, "output_norm.weight"), g.data("output.weight"))
+    hd = d // nq
     for i in range(layers):
         p = f"blk.{i}."
+
+        def fmt_of(name):
+            t = g.tensor(p + name)
+            if t is None:
+                raise ValueError(f"{p + name} is absent")
+            if t.ggml_type not in _GGML_FORMAT:
+                raise ValueError(f"{p + name} must be Q4_0, Q8_0, Q4_K or Q6_K")
+            return _GGML_FORMAT[t.ggml_type]
+
+        fmts = {k: fmt_of(f"{n}.weight") for k, n in (("o", "attn_output"), ("gate", "ffn_gate"), ("up", "ffn_up"),
+                                                      ("down", "ffn_down"))}
+        qkv, parts = None, None
         if g.tensor(p + "attn_qkv.weight") is not None:
+            fmts["qkv"] = fmt_of("attn_qkv.weight")
             qkv = g.data(p + "attn_qkv.weight")
         else:
-            qkv = np.concatenate([g.data(p + "attn_q.weight"), g.data(p + "attn_k.weight"), g.data(p + "attn_v.weight")])
+            f3 = [fmt_of(f"attn_{n}.weight") for n in "qkv"]
+            data = [g.data(p + f"attn_{n}.weight") for n in "qkv"]
+            if f3[0] == f3[1] == f3[2]:
+                fmts["qkv"] = f3[0]
+                qkv = np.concatenate(data)
+            else:  # a Q4_K_M file: attn_v in Q6_K beside Q4_K attn_q / attn_k
+                parts = [(f3[0], nq * hd, data[0]), (f3[1], nkv * hd, data[1]), (f3[2], nkv * hd, data[2])]
         model.set_layer(i, LayerTensors(attn_norm=_f32_vector(g, p + "attn_norm.weight"), qkv=qkv,
                                         o=g.data(p + "attn_output.weight"), ffn_norm=_f32_vector(g, p + "ffn_norm.weight"),
                                         gate=g.data(p + "ffn_gate.weight"), up=g.data(p + "ffn_up.weight"),
-                                        down=g.data(p + "ffn_down.weight")))
+                                        down=g.data(p + "ffn_down.weight"), fmts=fmts, qkv_parts=parts))
     g.close()
     return model

@@ -411,3 +411,78 @@ def test_gguf_weight_matches_bytes(gpu, tmp_path):
     assert rel_err(gpu.contract(W, x), oracle.matvec_f64("q6_k", w, 48, 1024, x)[0]) < 1e-3
     with pytest.raises(gpu.RqmvError):
         g.weight("absent")
+
+
+def _scaled_q6_k(rows, cols, seed, factor=0.25):
+    """Q6_K blocks whose fp16 d is scaled, so their values stay near the Q4_K ones."""
+    w = synth.q6_k(rows, cols, seed=seed).reshape(-1, 210)
+    d = w[:, 208:210].copy().view(np.float16).astype(np.float32) * factor
+    w[:, 208:210] = d.astype(np.float16).view(np.uint8)
+    return w.reshape(-1)
+
+
+def test_decode_from_q4_k_m_style_gguf(gpu, tmp_path):
+    """A file laid out as llama.cpp's Q4_K_M mixes formats: Q4_K token_embd and
+    attn_q / attn_k, Q6_K attn_v and (in some layers) ffn_down, a Q6_K output.
+    Every projection keeps its own format; Q, K and V of two formats run as two
+    products into one QKV vector; token_embd is decoded on the device."""
+    import gguf_writer as gw
+    from rqmv.decode import from_gguf
+    shape = DecoderShape(layers=2, d=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=384,
+                         head_fmt="q6_k")
+    D = synth.DecoderSynth(shape, seed=12, norm_std=0.1)
+    s = shape
+    nq, nk = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
+    embed = synth.q4_k(s.vocab, s.d, seed=31)
+    head = _scaled_q6_k(s.vocab, s.d, seed=32)
+    meta = [("general.architecture", gw.STRING, "llama"), ("llama.block_count", gw.U32, s.layers),
+            ("llama.embedding_length", gw.U32, s.d), ("llama.attention.head_count", gw.U32, s.q_heads),
+            ("llama.attention.head_count_kv", gw.U32, s.kv_heads), ("llama.feed_forward_length", gw.U32, s.ffn),
+            ("llama.rope.freq_base", gw.F32, s.rope_base), ("llama.attention.layer_norm_rms_epsilon", gw.F32, s.eps)]
+    tensors = [("token_embd.weight", [s.d, s.vocab], 12, embed.tobytes())]
+    layers = []
+    for i in range(s.layers):
+        t = D.layer(i)
+        rb = t.qkv.nbytes // s.qkv_rows
+        q, k = t.qkv[:nq * rb], t.qkv[nq * rb:(nq + nk) * rb]
+        v = _scaled_q6_k(nk, s.d, seed=40 + i)
+        down_fmt = "q6_k" if i == 0 else "q4_k"
+        down = _scaled_q6_k(s.d, s.ffn, seed=50 + i) if i == 0 else t.down
+        p = f"blk.{i}."
+        tensors += [(p + "attn_norm.weight", [s.d], 0, t.attn_norm.astype(np.float32).tobytes()),
+                    (p + "attn_q.weight", [s.d, nq], 12, q.tobytes()), (p + "attn_k.weight", [s.d, nk], 12, k.tobytes()),
+                    (p + "attn_v.weight", [s.d, nk], 14, v.tobytes()),
+                    (p + "attn_output.weight", [s.d, s.d], 12, t.o.tobytes()),
+                    (p + "ffn_norm.weight", [s.d], 0, t.ffn_norm.astype(np.float32).tobytes()),
+                    (p + "ffn_gate.weight", [s.d, s.ffn], 12, t.gate.tobytes()),
+                    (p + "ffn_up.weight", [s.d, s.ffn], 12, t.up.tobytes()),
+                    (p + "ffn_down.weight", [s.ffn, s.d], 14 if i == 0 else 12, down.tobytes())]
+        layers.append(type(t)(attn_norm=t.attn_norm, qkv=None, o=t.o, ffn_norm=t.ffn_norm, gate=t.gate, up=t.up,
+                              down=down, fmts={"down": down_fmt},
+                              qkv_parts=[("q4_k", nq, q), ("q4_k", nk, k), ("q6_k", nk, v)]))
+    tensors += [("output_norm.weight", [s.d], 0, D.out_norm().astype(np.float32).tobytes()),
+                ("output.weight", [s.d, s.vocab], 14, head.tobytes())]
+    path = str(tmp_path / "q4km.gguf")
+    gw.write(path, meta, tensors)
+    max_ctx = 8
+    model = from_gguf(path, max_ctx)
+    assert model.shape.head_fmt == "q6_k" and len(model.layers[0]["qkv"]) == 2
+    R = ref.DecoderReference(shape, ("q4_k", embed), D.out_norm(), head, layers,
+                             [(np.zeros((2, 0, 64), np.uint16), np.zeros((2, 0, 64), np.uint16))] * 2, max_ctx)
+    stream = gpu.Stream()
+    token, pos = 7, 0
+    model.set_position(token, pos)
+    for _ in range(3):
+        model.enqueue_step(stream)
+        stream.synchronize()
+        logits = model.read_logits()
+        want = R.step(token, pos)
+        assert np.isfinite(want).all() and rel_err(logits, want) < 1e-3, pos
+        token, pos = model.read_token(), pos + 1
+    # and captured: a graph replay continues the sequence
+    g = model.capture(stream)
+    g.launch(stream)
+    stream.synchronize()
+    assert rel_err(model.read_logits(), R.step(token, pos)) < 1e-3
+    g.close()
+    stream.close()
