@@ -139,6 +139,14 @@ int rqmv_moe_workspace_size(const rqmv_moe_params* params, size_t* bytes);
 int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,
              void* workspace, size_t workspace_bytes, void* stream);
 
+/* m positions at once (a prefill batch; recipe runs gguf_moe over every
+ * position of a step, each routed on its own): position p reads x_dev + p*ldx
+ * elements and writes y_dev + p*ldy; its routing weights go to route_dev +
+ * p*experts when route_dev is not NULL. The workspace holds m times
+ * rqmv_moe_workspace_size bytes. Still three launches for the whole batch. */
+int rqmv_moe_batch(const rqmv_moe_params* params, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev,
+                   int64_t ldy, float* route_dev, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Decode-step helpers. They have no counterpart at the matrix-vector
  * boundary: they run the rest of a decoder layer on the device between the
  * projections, for the end-to-end single-token decode, with the semantics of

@@ -1,4 +1,4 @@
-// gguf_moe decode-step kernels (one position).
+// gguf_moe kernels: one position, or a batch of positions along the launch's y dimension.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -31,16 +31,25 @@ struct MoeWorkspace {
 size_t moe_workspace_bytes(const MoeDims& d);
 MoeWorkspace moe_workspace(void* base, const MoeDims& d);
 
+// Positions of a batch: launch dimension y picks position p, whose activations
+// start p * x_stride bytes after x, workspace p * ws_stride bytes after the
+// first position's, output p * y_stride floats after y and routing plane
+// p * route_stride floats after route_dense.
+struct MoeBatch {
+    int64_t x_stride = 0, ws_stride = 0, y_stride = 0, route_stride = 0;
+    int m = 1;
+};
+
 // Routes the position (ws.ids, ws.weights and route_dense when not null,
 // topk_forward_wave_body semantics, amd-nv-cpu.ll:4489-4652) and computes
 // h[slot][f] = silu(gate_slot[f] . x) * (up_slot[f] . x) for every routed slot
 // and the shared expert.
 hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
                           const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws,
-                          float* route_dense, int cus, hipStream_t stream);
+                          float* route_dense, const MoeBatch& b, int cus, hipStream_t stream);
 
 // y[n] = sum_slot w_slot * (down_slot[n] . h_slot), routed slots in ascending expert id, then the shared expert.
 hipError_t launch_moe_down(int fmt, const MoeDims& d, const MoeBank& down, const MoeBank& down_sh, MoeWorkspace ws,
-                           float* y, int cus, hipStream_t stream);
+                           float* y, const MoeBatch& b, int cus, hipStream_t stream);
 
 }  // namespace rq

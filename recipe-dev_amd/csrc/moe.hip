@@ -1,4 +1,5 @@
-// gguf_moe decode step (one position) on gfx950.
+// gguf_moe block on gfx950: one position, or a batch of positions (prefill)
+// along the launches' y dimension, each with its own routing.
 //
 // Reference: lower_gguf_moe (recipe.rs:23415-23459) emits router Contraction ->
 // TopK -> ExpertIn(gate), ExpertIn(up) -> silu(gate)*up -> ExpertOut(down), and a
@@ -45,6 +46,16 @@ MoeWorkspace moe_workspace(void* base, const MoeDims& d) {
 }
 
 __device__ __forceinline__ float sigmoidf_dev(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// The workspace of position p of a batch.
+__device__ __forceinline__ MoeWorkspace position_ws(MoeWorkspace ws, int64_t stride_bytes, int p) {
+    const int64_t o = stride_bytes * p;
+    ws.logits = reinterpret_cast<float*>(reinterpret_cast<char*>(ws.logits) + o);
+    ws.ids = reinterpret_cast<int*>(reinterpret_cast<char*>(ws.ids) + o);
+    ws.weights = reinterpret_cast<float*>(reinterpret_cast<char*>(ws.weights) + o);
+    ws.h = reinterpret_cast<float*>(reinterpret_cast<char*>(ws.h) + o);
+    return ws;
+}
 
 // (value, index) pair of the better expert: the higher score, the lower id on a tie.
 __device__ __forceinline__ void better_of(float& v, int& i, float pv, int pi) {
@@ -190,8 +201,12 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
 template <int FMT, bool XF32, int S>
 __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
                                                        MoeBank up_sh, const void* x, MoeWorkspace ws, float* route_dense,
-                                                       int G) {
+                                                       int G, MoeBatch batch) {
     constexpr int XP = Traits<FMT>::XP;
+    // position blockIdx.y of the batch
+    x = static_cast<const char*>(x) + batch.x_stride * blockIdx.y;
+    ws = position_ws(ws, batch.ws_stride, (int)blockIdx.y);
+    if (route_dense) route_dense += batch.route_stride * blockIdx.y;
     extern __shared__ uint4 smem[];
     __shared__ int slot_ids_all[4][64];
     const int nch = gate.P.nch;
@@ -253,8 +268,10 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
 
 template <int FMT>
 __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
-                                                        float* y, int G) {
+                                                        float* y, int G, MoeBatch batch) {
     constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
+    ws = position_ws(ws, batch.ws_stride, (int)blockIdx.y);
+    y += batch.y_stride * blockIdx.y;
     extern __shared__ uint4 smem[];
     const int K = d.top * d.hidden + d.hidden_shared;
     const int nch = K / CW;            // chunks of all slots back to back
@@ -320,8 +337,8 @@ static int lanes_for(int64_t nch) {
 
 template <int FMT, bool XF32, int S>
 static hipError_t glu_launch(const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
-                             const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense, int cus,
-                             hipStream_t stream) {
+                             const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense,
+                             const MoeBatch& b, int cus, hipStream_t stream) {
     const int nch = gate.P.nch;
     const int G = lanes_for(nch);
     const int total_rows = d.top * d.hidden + d.hidden_shared;
@@ -335,17 +352,17 @@ static hipError_t glu_launch(const MoeDims& d, const MoeBank& gate, const MoeBan
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMoeThreads), lds, stream, d, gate, up, gate_sh, up_sh, x, ws,
-                       route_dense, G);
+    hipLaunchKernelGGL(kernel, dim3(grid, b.m), dim3(kMoeThreads), lds, stream, d, gate, up, gate_sh, up_sh, x, ws,
+                       route_dense, G, b);
     return hipGetLastError();
 }
 
 template <int FMT, bool XF32>
 static hipError_t glu_slots(const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
-                            const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense, int cus,
-                            hipStream_t stream) {
+                            const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense,
+                            const MoeBatch& b, int cus, hipStream_t stream) {
     const int slots = (d.experts + 63) / 64;
-#define RQ_GLU(S) glu_launch<FMT, XF32, S>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream)
+#define RQ_GLU(S) glu_launch<FMT, XF32, S>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream)
     if (slots <= 1) return RQ_GLU(1);
     if (slots <= 2) return RQ_GLU(2);
     if (slots <= 4) return RQ_GLU(4);
@@ -357,28 +374,28 @@ static hipError_t glu_slots(const MoeDims& d, const MoeBank& gate, const MoeBank
 
 template <int FMT>
 static hipError_t glu_fmt(int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up, const MoeBank& gate_sh,
-                          const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense, int cus,
-                          hipStream_t stream) {
+                          const MoeBank& up_sh, const void* x, MoeWorkspace ws, float* route_dense,
+                          const MoeBatch& b, int cus, hipStream_t stream) {
     if (d.experts > kTopkMaxExperts || d.top > 64 || d.top < 1) return hipErrorInvalidValue;
-    if (xtype == 0) return glu_slots<FMT, true>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
-    return glu_slots<FMT, false>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+    if (xtype == 0) return glu_slots<FMT, true>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream);
+    return glu_slots<FMT, false>(d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream);
 }
 
 hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
                           const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws,
-                          float* route_dense, int cus, hipStream_t stream) {
+                          float* route_dense, const MoeBatch& b, int cus, hipStream_t stream) {
     switch (fmt) {
-        case Q4_0: return glu_fmt<Q4_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
-        case Q8_0: return glu_fmt<Q8_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
-        case Q4_K: return glu_fmt<Q4_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
-        case Q6_K: return glu_fmt<Q6_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, cus, stream);
+        case Q4_0: return glu_fmt<Q4_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream);
+        case Q8_0: return glu_fmt<Q8_0>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream);
+        case Q4_K: return glu_fmt<Q4_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream);
+        case Q6_K: return glu_fmt<Q6_K>(xtype, d, gate, up, gate_sh, up_sh, x, ws, route_dense, b, cus, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int FMT>
 static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank& down_sh, MoeWorkspace ws, float* y,
-                           int cus, hipStream_t stream) {
+                           const MoeBatch& b, int cus, hipStream_t stream) {
     constexpr int CW = Traits<FMT>::CW;
     const int nch = (d.top * d.hidden + d.hidden_shared) / CW;
     const int G = lanes_for(nch);
@@ -391,17 +408,18 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(moe_down_kernel<FMT>, dim3(grid), dim3(kMoeThreads), lds, stream, d, down, down_sh, ws, y, G);
+    hipLaunchKernelGGL(moe_down_kernel<FMT>, dim3(grid, b.m), dim3(kMoeThreads), lds, stream, d, down, down_sh, ws, y, G,
+                       b);
     return hipGetLastError();
 }
 
 hipError_t launch_moe_down(int fmt, const MoeDims& d, const MoeBank& down, const MoeBank& down_sh, MoeWorkspace ws,
-                           float* y, int cus, hipStream_t stream) {
+                           float* y, const MoeBatch& b, int cus, hipStream_t stream) {
     switch (fmt) {
-        case Q4_0: return down_fmt<Q4_0>(d, down, down_sh, ws, y, cus, stream);
-        case Q8_0: return down_fmt<Q8_0>(d, down, down_sh, ws, y, cus, stream);
-        case Q4_K: return down_fmt<Q4_K>(d, down, down_sh, ws, y, cus, stream);
-        case Q6_K: return down_fmt<Q6_K>(d, down, down_sh, ws, y, cus, stream);
+        case Q4_0: return down_fmt<Q4_0>(d, down, down_sh, ws, y, b, cus, stream);
+        case Q8_0: return down_fmt<Q8_0>(d, down, down_sh, ws, y, b, cus, stream);
+        case Q4_K: return down_fmt<Q4_K>(d, down, down_sh, ws, y, b, cus, stream);
+        case Q6_K: return down_fmt<Q6_K>(d, down, down_sh, ws, y, b, cus, stream);
         default: return hipErrorInvalidValue;
     }
 }

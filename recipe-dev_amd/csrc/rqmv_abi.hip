@@ -139,7 +139,6 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     if (!x || !y) return fail(RQMV_EINVAL, "x or y is NULL");
     if (xtype != RQMV_DTYPE_F16 && xtype != RQMV_DTYPE_F32) return fail(RQMV_EINVAL, "x_dtype must be F16 or F32");
     if (m <= 0) return fail(RQMV_EINVAL, "m must be positive");
-    if (m > 1 && (ldx < w->cols || ldy < rows)) return fail(RQMV_EINVAL, "ldx < cols or ldy < rows");
     const size_t esize = xtype == RQMV_DTYPE_F16 ? 2 : 4;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || (m > 1 && ((size_t)ldx * esize) % 16 != 0))
         return fail(RQMV_EINVAL, "x rows must start 16-byte aligned (x and ldx * element size)");
@@ -148,11 +147,12 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     p.P2 = p.P;
     p.split = rows;
     if (extra_row) {  // one more output row from a second F16 weight of the same width
-        if (w->fmt != rq::F16 || extra_row->fmt != rq::F16 || extra_row->cols != w->cols || m != 1)
-            return fail(RQMV_EINVAL, "an extra row needs two F16 weights of one width and one activation row");
+        if (w->fmt != rq::F16 || extra_row->fmt != rq::F16 || extra_row->cols != w->cols)
+            return fail(RQMV_EINVAL, "an extra row needs two F16 weights of one width");
         p.P2 = planes_of(extra_row, 0);
         rows += 1;
     }
+    if (m > 1 && (ldx < w->cols || ldy < rows)) return fail(RQMV_EINVAL, "ldx < cols or ldy < rows");
     p.rows = rows;
     p.K = (int)w->cols;
     p.ldx = ldx;
@@ -527,8 +527,8 @@ int rqmv_moe_workspace_size(const rqmv_moe_params* params, size_t* bytes) {
     return RQMV_OK;
 }
 
-int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,
-             void* workspace, size_t workspace_bytes, void* stream) {
+int rqmv_moe_batch(const rqmv_moe_params* params, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev,
+                   int64_t ldy, float* route_dev, void* workspace, size_t workspace_bytes, void* stream) {
     DeviceInfo info;
     int rc = check_launch(params ? params->router : nullptr, &info);
     if (rc != RQMV_OK) return rc;
@@ -537,27 +537,46 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
     if (rc != RQMV_OK) return rc;
     if (!x_dev || !y_dev || !workspace) return fail(RQMV_EINVAL, "x, y and workspace are required");
     if (x_dtype != RQMV_DTYPE_F16 && x_dtype != RQMV_DTYPE_F32) return fail(RQMV_EINVAL, "x_dtype must be F16 or F32");
-    if (workspace_bytes < rq::moe_workspace_bytes(d)) return fail(RQMV_EINVAL, "workspace too small");
-    if (reinterpret_cast<uintptr_t>(x_dev) % 16 != 0 || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
-        return fail(RQMV_EINVAL, "x must be 16-byte and workspace 256-byte aligned");
+    if (m < 1 || m > 65535) return fail(RQMV_EINVAL, "moe: m must be in 1..65535");
+    if (ldx < d.d_model || ldy < d.d_model) return fail(RQMV_EINVAL, "moe: ldx and ldy must be at least d_model");
+    const size_t per = rq::moe_workspace_bytes(d);
+    if (workspace_bytes / (size_t)m < per) return fail(RQMV_EINVAL, "workspace too small");
+    const int xb = x_dtype == RQMV_DTYPE_F16 ? 2 : 4;
+    if (reinterpret_cast<uintptr_t>(x_dev) % 16 != 0 || (ldx * xb) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(RQMV_EINVAL, "x rows must be 16-byte and workspace 256-byte aligned");
     for (const rqmv_weight* w : {params->gate_exps, params->up_exps, params->down_exps, params->shared_gate_inp,
                                  params->gate_shexp, params->up_shexp, params->down_shexp})
         if (w && w->device != params->router->device) return fail(RQMV_ESTATE, "moe weights live on different devices");
     hipStream_t s = static_cast<hipStream_t>(stream);
     rq::MoeWorkspace ws = rq::moe_workspace(workspace, d);
-    // router logits and the shared expert's gate logit: one F16 launch over
-    // both weights (experts + 1 rows)
-    rc = matvec_rows(params->router, 0, d.experts, x_dev, x_dtype, 1, d.d_model, ws.logits, d.experts, s, info,
-                     nullptr, nullptr, params->shared_gate_inp);
+    rq::MoeBatch b;
+    b.m = m;
+    b.x_stride = ldx * xb;
+    b.ws_stride = (int64_t)per;
+    b.y_stride = ldy;
+    b.route_stride = d.experts;
+    // router logits and the shared expert's gate logit of every position: one
+    // F16 product over both weights (experts + 1 rows), position p's into its
+    // own workspace
+    rc = matvec_rows(params->router, 0, d.experts, x_dev, x_dtype, m, ldx, ws.logits, (int64_t)(per / sizeof(float)), s,
+                     info, nullptr, nullptr, params->shared_gate_inp);
     if (rc != RQMV_OK) return rc;
     const int fmt = params->gate_exps->fmt;
     hipError_t e = rq::launch_moe_glu(fmt, x_dtype, d, bank_of(params->gate_exps), bank_of(params->up_exps),
-                                      bank_of(params->gate_shexp), bank_of(params->up_shexp), x_dev, ws, route_dev,
+                                      bank_of(params->gate_shexp), bank_of(params->up_shexp), x_dev, ws, route_dev, b,
                                       info.cus, s);
     if (e != hipSuccess) return hip_fail(e, "moe routing and gate/up launch");
-    e = rq::launch_moe_down(fmt, d, bank_of(params->down_exps), bank_of(params->down_shexp), ws, y_dev, info.cus, s);
+    e = rq::launch_moe_down(fmt, d, bank_of(params->down_exps), bank_of(params->down_shexp), ws, y_dev, b, info.cus, s);
     if (e != hipSuccess) return hip_fail(e, "moe down launch");
     return RQMV_OK;
+}
+
+int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,
+             void* workspace, size_t workspace_bytes, void* stream) {
+    const int64_t d_model = params && params->router ? params->router->cols : 0;
+    return rqmv_moe_batch(params, x_dev, x_dtype, 1, d_model, y_dev, d_model, route_dev, workspace, workspace_bytes,
+                          stream);
 }
 
 int rqmv_add_rmsnorm(float* x, const float* delta, const float* weight, int n, float eps, float* out, void* stream) {

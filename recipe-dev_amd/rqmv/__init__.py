@@ -56,6 +56,8 @@ class _Lib:
         L.rqmv_expert_matvec.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p]
         L.rqmv_moe_workspace_size.argtypes = [c_void_p, POINTER(c_size_t)]
         L.rqmv_moe.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        L.rqmv_moe_batch.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                     c_size_t, c_void_p]
         L.rqmv_add_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]
         L.rqmv_rope_kv.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, ctypes.c_double, c_void_p, c_void_p, c_int,
                                    c_void_p]
@@ -478,15 +480,35 @@ class Moe:
                                   self.workspace.ptr, self.workspace.nbytes, stream.handle if stream else None),
                "rqmv_moe")
 
+    def run_batch(self, x: DeviceBuffer, x_dtype: int, m: int, ldx: int, y: DeviceBuffer, ldy: int,
+                  route: DeviceBuffer | None = None, workspace: DeviceBuffer | None = None,
+                  stream: Stream | None = None):
+        """m positions (rqmv_moe_batch); the workspace holds m per-position workspaces."""
+        if workspace is None:
+            workspace = self.batch_workspace(m)
+        _check(lib().lib.rqmv_moe_batch(byref(self.params), x.ptr, x_dtype, m, ldx, y.ptr, ldy,
+                                        route.ptr if route else None, workspace.ptr, workspace.nbytes,
+                                        stream.handle if stream else None), "rqmv_moe_batch")
+
+    def batch_workspace(self, m: int) -> DeviceBuffer:
+        return DeviceBuffer(self.workspace.nbytes * m)
+
     def __call__(self, x: np.ndarray):
-        """Host convenience: returns (y fp32 (d_model,), routing weights fp32 (experts,))."""
-        xh, dt = _x_host(np.ascontiguousarray(x))
+        """Host convenience: x (d_model,) or (m, d_model) -> (y fp32, routing weights fp32),
+        shaped (d_model,) / (experts,) or (m, d_model) / (m, experts)."""
+        x2 = np.atleast_2d(np.ascontiguousarray(x))
+        xh, dt = _x_host(x2)
+        m = xh.shape[0]
         xb = DeviceBuffer.from_array(xh)
-        yb = DeviceBuffer(4 * self.d_model)
-        rb = DeviceBuffer(4 * self.experts)
-        self.run(xb, dt, yb, rb)
+        yb = DeviceBuffer(4 * self.d_model * m)
+        rb = DeviceBuffer(4 * self.experts * m)
+        if m == 1:
+            self.run(xb, dt, yb, rb)
+        else:
+            self.run_batch(xb, dt, m, self.d_model, yb, self.d_model, rb)
         synchronize()
-        return yb.download(np.float32), rb.download(np.float32)
+        y, r = yb.download(np.float32).reshape(m, -1), rb.download(np.float32).reshape(m, -1)
+        return (y[0], r[0]) if x.ndim == 1 else (y, r)
 
 
 def layout_bytes(fmt, rows: int, cols: int) -> int:

@@ -329,3 +329,29 @@ def test_bad_arguments_return_errors(gpu):
     Wr = gpu.Weight("f16", 8, cols, synth.f16_weights(8, cols, 0.02, seed=3))
     with pytest.raises(gpu.RqmvError):
         gpu.Moe(Wr, W, W, W, 2)  # banks are not 8-expert banks
+
+
+@pytest.mark.parametrize("m,xdt", [(2, "f16"), (5, "f32"), (8, "f16")])
+def test_moe_batch_parity(gpu, m, xdt):
+    """A prefill batch of positions through rqmv_moe_batch: each position routed
+    on its own, against the oracle position by position, and equal to the
+    one-position call bit for bit."""
+    fmt, d, E, top, H, HS = "q4_k", 512, 32, 4, 256, 256
+    router, gate, up, down, shared = _moe_case(fmt, d, E, top, H, HS, True, seed=77)
+    xh, dt, x32 = _x(m, d, xdt, seed=78)
+    sg, gs, us, ds = shared
+    moe = gpu.Moe(gpu.Weight("f16", E, d, router), gpu.Weight(fmt, H, d, gate, experts=E),
+                  gpu.Weight(fmt, H, d, up, experts=E), gpu.Weight(fmt, d, H, down, experts=E), top,
+                  shared_gate_inp=gpu.Weight("f16", 1, d, sg), gate_sh=gpu.Weight(fmt, HS, d, gs),
+                  up_sh=gpu.Weight(fmt, HS, d, us), down_sh=gpu.Weight(fmt, d, HS, ds))
+    y, route = moe(xh)
+    assert y.shape == (m, d) and route.shape == (m, E)
+    for p in range(m):
+        y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
+                                       x32[p].astype(np.float64), hidden_shared=HS, shared_gate_bits=sg.view(np.uint16),
+                                       gate_sh=gs, up_sh=us, down_sh=ds)
+        assert np.array_equal(route[p] != 0, rw_ref != 0), p
+        assert np.allclose(route[p], rw_ref, rtol=1e-5, atol=1e-7)
+        assert rel_l2(y[p], y_ref) <= REL_L2, p
+        y1, r1 = moe(xh[p])
+        assert np.array_equal(y1, y[p]) and np.array_equal(r1, route[p]), p
