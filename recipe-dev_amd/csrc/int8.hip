@@ -60,24 +60,46 @@ __device__ __forceinline__ void step_of(float e, float& inverse, float& d) {
     d = nonzero ? d_raw : 0.f;
 }
 
-// The 32 codes of record r: clamp(round-half-even(x * inverse), -128, 127)
-// (amd-nv-cpu.ll:1484-1490), from a 16-byte aligned row, into LDS.
-__device__ __forceinline__ void record_codes(const float* __restrict__ xr, float inverse, int8_t* out) {
+// The 32 inputs of one record from a 16-byte aligned row.
+__device__ __forceinline__ void load_record(const float* __restrict__ xr, float4 (&xv)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xv[q] = reinterpret_cast<const float4*>(xr)[q];
+}
+
+// The 32 codes of a record in registers: clamp(round-half-even(x * inverse),
+// -128, 127) (amd-nv-cpu.ll:1484-1490), written to LDS.
+__device__ __forceinline__ void record_codes(const float4 (&xv)[8], float inverse, int8_t* out) {
     uint32_t w[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
-        const float f[4] = {v.x, v.y, v.z, v.w};
+        const float f[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
         uint32_t word = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float r = __builtin_rintf(f[k] * inverse);
-            word |= ((uint32_t)(int)fminf(fmaxf(r, -128.f), 127.f) & 0xffu) << (8 * k);
+            const float rr = __builtin_rintf(f[k] * inverse);
+            word |= ((uint32_t)(int)fminf(fmaxf(rr, -128.f), 127.f) & 0xffu) << (8 * k);
         }
         w[q] = word;
     }
     reinterpret_cast<uint4*>(out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
     reinterpret_cast<uint4*>(out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// Record r at a 32 step from its 32 inputs in registers: the extreme, the
+// step d[r] and the codes.
+__device__ __forceinline__ void record_from_registers(const float4 (&xv)[8], float* d, int8_t* codes, int r) {
+    float e = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        if (extreme_wins(xv[q].x, e)) e = xv[q].x;
+        if (extreme_wins(xv[q].y, e)) e = xv[q].y;
+        if (extreme_wins(xv[q].z, e)) e = xv[q].z;
+        if (extreme_wins(xv[q].w, e)) e = xv[q].w;
+    }
+    float inverse, dd;
+    step_of(e, inverse, dd);
+    record_codes(xv, inverse, codes + r * 32);
+    d[r] = dd;
 }
 
 // The Q8 records of one activation row of K inputs (16-byte aligned) into
@@ -92,20 +114,9 @@ __device__ __forceinline__ void q8_records(const float* __restrict__ x, int K, i
     const int blocks = K >> 5;
     if (step == 32) {
         for (int r = tid; r < blocks; r += nthreads) {
-            const float* xr = x + r * 32;
-            float e = 0.f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
-                if (extreme_wins(v.x, e)) e = v.x;
-                if (extreme_wins(v.y, e)) e = v.y;
-                if (extreme_wins(v.z, e)) e = v.z;
-                if (extreme_wins(v.w, e)) e = v.w;
-            }
-            float inverse, dd;
-            step_of(e, inverse, dd);
-            record_codes(xr, inverse, codes + r * 32);
-            d[r] = dd;
+            float4 xv[8];
+            load_record(x + r * 32, xv);
+            record_from_registers(xv, d, codes, r);
         }
         __syncthreads();
         return;
@@ -135,7 +146,11 @@ __device__ __forceinline__ void q8_records(const float* __restrict__ x, int K, i
         for (int b = g * 8; b < min(g * 8 + 8, blocks); ++b) d[b] = dd;
     }
     __syncthreads();
-    for (int r = tid; r < blocks; r += nthreads) record_codes(x + r * 32, ginv[r >> 3], codes + r * 32);
+    for (int r = tid; r < blocks; r += nthreads) {
+        float4 xv[8];
+        load_record(x + r * 32, xv);
+        record_codes(xv, ginv[r >> 3], codes + r * 32);
+    }
     __syncthreads();
 }
 
@@ -314,18 +329,44 @@ __global__ __launch_bounds__(kI8Threads) void int8_slices_kernel(I8Launch p) {
     int8_t* xc;
     float* xd;
     float* rowbuf;
-    stage_records(p, p.step, xc, xd, rowbuf);
-    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int tid = (int)threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t row0 = (int64_t)blockIdx.x * kI8Rows + 2 * wave;
-    if (row0 >= p.rows) return;
-    const bool two = row0 + 1 < p.rows;
+    const bool live = row0 < p.rows, two = row0 + 1 < p.rows;
     const int slices = p.K >> 4, nch = p.P.nch;
+    // At a 32 step with at most one record per thread, the inputs of the
+    // thread's record are loaded first and the first pass's weights after
+    // them, so that waiting for the inputs leaves the weight loads in flight
+    // (the counter of outstanding loads drains in order).
+    const int blocks = p.K >> 5;
+    const bool early = p.step == 32 && blocks <= kI8Threads;
+    ChunkData<FMT> A, B;
+    bool have = false;
+    if (early) {
+        extern __shared__ __align__(16) uint8_t i8_lds[];
+        xc = reinterpret_cast<int8_t*>(i8_lds);
+        xd = reinterpret_cast<float*>(i8_lds + p.K);
+        const int tail_floats = (p.K >> 5) + ((p.K + 255) >> 8);
+        rowbuf = xd + ((tail_floats + 3) & ~3) + wave * 512;
+        float4 xv[8];
+        if (tid < blocks) load_record(p.x + (int64_t)blockIdx.y * p.ldx + tid * 32, xv);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        if (live && lane < nch) {
+            load_chunk<FMT>(p.P, row0, lane, A);
+            if (two) load_chunk<FMT>(p.P, row0 + 1, lane, B);
+            have = true;
+        }
+        if (tid < blocks) record_from_registers(xv, xd, xc, tid);
+        __syncthreads();
+    } else {
+        stage_records(p, p.step, xc, xd, rowbuf);
+    }
+    if (!live) return;
     const int mine = lane >> 5;  // which of the two rows this lane sums
     float acc = 0.f;
     for (int c0 = 0; c0 < nch; c0 += 64) {
         const int c = c0 + lane;
-        ChunkData<FMT> A, B;
-        if (c < nch) {
+        if (c < nch && !(have && c0 == 0)) {
             load_chunk<FMT>(p.P, row0, c, A);
             if (two) load_chunk<FMT>(p.P, row0 + 1, c, B);
         }
