@@ -215,19 +215,23 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// NeoX rotation of the eight values x (dims 8b..8b+7 of a head) given their
-// partners xp (dims 8b +- HD/2) and the position's (cos, sin) row.
-template <int HD>
-__device__ __forceinline__ void rotate8(float (&x)[8], const float (&xp)[8], const float2* cs_row, int b) {
-    constexpr int HALF = HD / 2;
-    const bool upper = 8 * b >= HALF;
-    const int i0 = 8 * b - (upper ? HALF : 0);
+// NeoX rotation of the eight values x (dims 8b..8b+7 of a head, `upper` when
+// they lie in the second half) given their partners xp (dims 8b +- HD/2) and
+// the eight (cos, sin) pairs of pairs 8b mod HD/2 .. +7 at the position.
+__device__ __forceinline__ void rotate8(float (&x)[8], const float (&xp)[8], const float2 (&cs)[8], bool upper) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float2 cs = cs_row[i0 + e];
         // lower half: x_i c - x_{i+half} s; upper half: x_{i+half} c + x_i s
-        x[e] = upper ? x[e] * cs.x + xp[e] * cs.y : x[e] * cs.x - xp[e] * cs.y;
+        x[e] = upper ? x[e] * cs[e].x + xp[e] * cs[e].y : x[e] * cs[e].x - xp[e] * cs[e].y;
     }
+}
+
+// The rotation partners of a lane's eight values: in the lane holding the
+// piece HD/2 away in the same position, lane ^ (LPP / 2).
+template <int LPP>
+__device__ __forceinline__ void partners8(const float (&x)[8], float (&xp)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xp[e] = __shfl_xor(x[e], LPP / 2);
 }
 
 template <int HD, int MAXG, bool ROPE>
@@ -243,14 +247,24 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     __shared__ float ml[MAXG][2];
     __shared__ float red[kAttnWaves][MAXG * HD];
     const int kh = blockIdx.x, chunk = blockIdx.y;
-    const int pos = *pos_dev;
-    const int len = min(pos + 1, max_ctx);  // positions past the cache are not read
-    const int t0 = chunk * kAttnChunk;
-    if (t0 >= len) return;  // a chunk past the position: nothing to read (the whole workgroup leaves)
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int b = t % LPP, slot = t / LPP;
-    const int pb = (b + LPP / 2) % LPP;  // the lane piece holding the rotation partners
-    const float2* cs_row = rope + (size_t)min(pos, max_ctx - 1) * HALF;  // the table has max_ctx rows
+    const int t0 = chunk * kAttnChunk;
+    // Every load is issued before the first wait. The queries and, under ROPE,
+    // the new key and value do not depend on the position, so they go out
+    // while it is read; slots past the group read the group's last head and
+    // are zeroed below.
+    float qr[MAXG][8];
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) load8(q + (size_t)(kh * group + min(g, group - 1)) * HD + b * 8, qr[g]);
+    float kn[8], vn[8];
+    if constexpr (ROPE) {
+        load8(kv_new + (size_t)kh * HD + b * 8, kn);
+        load8(kv_new + (size_t)(nkv + kh) * HD + b * 8, vn);
+    }
+    const int pos = *pos_dev;
+    const int len = min(pos + 1, max_ctx);  // positions past the cache are not read
+    if (t0 >= len) return;  // a chunk past the position: nothing to read (the whole workgroup leaves)
 
     // keys and values of this lane's positions (clamped into the cache; masked below)
     uint4 kr[NS], vr[NS];
@@ -265,30 +279,30 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
         const int p = min(t0 + slot + j * PPS, max_ctx - 1);
         vr[j] = *reinterpret_cast<const uint4*>(vc + (head_base + p) * HD + b * 8);
     }
-    float qr[MAXG][8];
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g) {
-        if (g < group) {
-            load8(q + (size_t)(kh * group + g) * HD + b * 8, qr[g]);
-            if constexpr (ROPE) {
-                float qp[8];
-                load8(q + (size_t)(kh * group + g) * HD + pb * 8, qp);
-                rotate8<HD>(qr[g], qp, cs_row, b);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qr[g][e] = 0.f;
-        }
-    }
     if constexpr (ROPE) {
+        // the position's (cos, sin) pairs for this lane's dims (the table has max_ctx rows)
+        const bool upper = 8 * b >= HALF;
+        const float4* cs4 =
+            reinterpret_cast<const float4*>(rope + (size_t)min(pos, max_ctx - 1) * HALF + (8 * b - (upper ? HALF : 0)));
+        float2 cs[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = cs4[i];
+            cs[2 * i] = make_float2(v.x, v.y);
+            cs[2 * i + 1] = make_float2(v.z, v.w);
+        }
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) {
+            float qp[8];
+            partners8<LPP>(qr[g], qp);
+            rotate8(qr[g], qp, cs, upper);
+        }
+        float kp[8];
+        partners8<LPP>(kn, kp);
+        rotate8(kn, kp, cs, upper);
         // the new position's key and value replace the cache entry in the chunk that holds it
         const int jn = pos - t0 - slot;
         if (pos < max_ctx && jn >= 0 && jn < kAttnChunk && jn % PPS == 0) {
-            float kn[8], kp[8], vn[8];
-            load8(kv_new + (size_t)kh * HD + b * 8, kn);
-            load8(kv_new + (size_t)kh * HD + pb * 8, kp);
-            load8(kv_new + (size_t)(nkv + kh) * HD + b * 8, vn);
-            rotate8<HD>(kn, kp, cs_row, b);
             const uint4 k16 = pack8(kn), v16 = pack8(vn);
             *reinterpret_cast<uint4*>(kc + (head_base + pos) * HD + b * 8) = k16;
             *reinterpret_cast<uint4*>(vc + (head_base + pos) * HD + b * 8) = v16;
@@ -300,6 +314,10 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
                 }
         }
     }
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[g][e] = g < group ? qr[g][e] : 0.f;
 
     // pass 1: scores
 #pragma unroll
