@@ -61,6 +61,33 @@ def traffic_from_profiles(workload, m):
         return None
 
 
+def stream_copy(achieved_gbs, nbytes=1 << 30, reps=20):
+    """The device's STREAM copy rate measured in the same process: a
+    stream-ordered device-to-device copy of nbytes (the HIP runtime's copy
+    kernel), bytes read plus bytes written over the mean of `reps` copies; and
+    the workload's achieved rate as a fraction of it (the second roofline
+    fraction beside the 8 TB/s vendor peak)."""
+    import rqmv
+
+    src, dst, st = rqmv.DeviceBuffer(nbytes), rqmv.DeviceBuffer(nbytes), rqmv.Stream()
+    src.fill_zero()
+    for _ in range(3):
+        dst.copy_from(src, nbytes, st)
+    e0, e1 = rqmv.Event(), rqmv.Event()
+    e0.record(st)
+    for _ in range(reps):
+        dst.copy_from(src, nbytes, st)
+    e1.record(st)
+    e1.synchronize()
+    gbs = 2 * nbytes * reps / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    for o in (src, dst, st, e0, e1):
+        o.close()
+    log(f"bench: device copy {gbs:.0f} GB/s (read + write)")
+    return {"value": round(gbs, 1), "unit": "GB/s", "bytes_per_copy": 2 * nbytes,
+            "method": "hipMemcpyAsync device to device of 1 GiB, bytes read + written",
+            "frac": round(achieved_gbs / gbs, 4)}
+
+
 def cpu_baseline(fmt, rows, cols, x32, seconds, weights_bytes, alg_bytes):
     import oracle
 
@@ -199,6 +226,7 @@ def moe_bench(args):
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
                      "note": "whole step (three launches) from the graph replay"},
+        "stream_copy": stream_copy(value),
         "parity_rel_l2": rel,
     }
     if not args.no_cpu:
@@ -300,6 +328,7 @@ def decode_bench(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "note": "whole token (every launch of the step) from graph replays"},
+        "stream_copy": stream_copy(achieved),
     }
     if not args.no_cpu:
         import oracle
@@ -407,6 +436,7 @@ def int8_bench(args):
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "stream_copy": stream_copy(achieved),
         "kernel_us": round(ker_ms * 1e3, 3),
         "parity_bit_exact": exact,
     }
@@ -555,6 +585,7 @@ def main():
                    "bytes_per_step": alg_bytes, "flops_per_step": flops, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.workload, m)},
+        "stream_copy": stream_copy(achieved),
         "kernel_us": round(ker_ms * 1e3, 3),
         "gflops": round(flops / (ker_ms * 1e-3) / 1e9, 1),
         "parity_rel_l2": rel,

@@ -101,6 +101,7 @@ class _Lib:
         H.hipMalloc.argtypes = [POINTER(c_void_p), c_size_t]
         H.hipFree.argtypes = [c_void_p]
         H.hipMemcpy.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
+        H.hipMemcpyAsync.argtypes = [c_void_p, c_void_p, c_size_t, c_int, c_void_p]
         H.hipMemset.argtypes = [c_void_p, c_int, c_size_t]
         H.hipDeviceSynchronize.argtypes = []
         H.hipStreamCreate.argtypes = [POINTER(c_void_p)]
@@ -191,6 +192,12 @@ class DeviceBuffer:
 
     def fill_zero(self):
         _hip(lib().hip.hipMemset(self.ptr, 0, self.nbytes), "hipMemset")
+
+    def copy_from(self, src: "DeviceBuffer", nbytes: int, stream=None):
+        """Stream-ordered device-to-device copy of src's first nbytes."""
+        assert nbytes <= self.nbytes and nbytes <= src.nbytes
+        _hip(lib().hip.hipMemcpyAsync(self.ptr, src.ptr, nbytes, _D2D, stream.handle if stream else None),
+             "hipMemcpyAsync D2D")
 
     def view(self, offset: int, nbytes: int) -> "BufferView":
         """A non-owning window [offset, offset + nbytes) of this allocation."""
