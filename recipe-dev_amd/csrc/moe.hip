@@ -24,8 +24,18 @@
 namespace rq {
 
 constexpr int kMoeThreads = 256;  // workgroup size of the MoE kernels (four waves)
+constexpr int kMoeOwnRouteMax = 2;  // positions per launch up to which every wave routes on its own
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Workgroups per position of a launch: at most eight per CU over the whole
+// batch (each workgroup routes or stages its position once, so a batch of
+// many positions walks several tiles per wave rather than repeating that
+// work in more workgroups), and at least one.
+static int batch_grid_cap(int cus, int m) {
+    const int cap = cus * 8 / (m > 0 ? m : 1);
+    return cap > 1 ? cap : 1;
+}
 
 size_t moe_workspace_bytes(const MoeDims& d) {
     return al(sizeof(float) * (size_t)(d.experts + 1)) + al(sizeof(int) * (size_t)d.top) +
@@ -198,7 +208,10 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
     }
 }
 
-template <int FMT, bool XF32, int S>
+// RING (batches): two buffers of weights, the next tile's requested before
+// the current one is computed. One or two positions run one tile per wave,
+// where the single buffer holds fewer registers and measured faster.
+template <int FMT, bool XF32, int S, bool RING>
 __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
                                                        MoeBank up_sh, const void* x, MoeWorkspace ws, float* route_dense,
                                                        int G, MoeBatch batch) {
@@ -218,11 +231,16 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     const int total_rows = routed + d.hidden_shared;
     const int rows_per_wave = 64 / G;
     const int tiles = (total_rows + rows_per_wave - 1) / rows_per_wave;
-    // Every wave routes the position itself (a few microseconds of one wave,
-    // instead of a launch and a round trip through memory); the first wave of
-    // the first workgroup also writes the routing out for the down kernel.
-    int* const slot_ids = slot_ids_all[wave];
-    route_wave<S>(d, ws, route_dense, blockIdx.x == 0 && wave == 0, slot_ids);
+    // The position is routed here (a few microseconds of one wave, instead of
+    // a launch and a round trip through memory); the first wave of the first
+    // workgroup also writes the routing out for the down kernel. For one or
+    // two positions every wave routes on its own and none waits; for more,
+    // where the launch holds many workgroups per position, the first wave
+    // routes for its workgroup and the others read its slots after a barrier.
+    // (RING is chosen for exactly the launches of more than two positions.)
+    int* const slot_ids = slot_ids_all[RING ? 0 : wave];
+    if (!RING || wave == 0) route_wave<S>(d, ws, route_dense, blockIdx.x == 0 && wave == 0, slot_ids);
+    if constexpr (RING) __syncthreads();
     // Row r of the gate/up stack: hidden row f of routed slot s, or of the shared expert.
     auto fetch = [&](int r, int c, ChunkData<FMT>& dg, ChunkData<FMT>& du) {
         r = r < total_rows ? r : total_rows - 1;
@@ -238,18 +256,43 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
         }
     };
     int tile = blockIdx.x * wpb + wave;
-    // the first chunk's weights are requested before the activations are staged
-    ChunkData<FMT> dg, du;
-    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, dg, du);
+    const int stride = gridDim.x * wpb;
+    // the first tile's weights are requested before the activations are staged
+    ChunkData<FMT> dg0, du0, dg1, du1;
+    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, dg0, du0);
     stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb));
     __syncthreads();
-    bool fetched = true;
-    for (; tile < tiles; tile += gridDim.x * wpb) {
-        const int r = tile * rows_per_wave + sub;
+    if constexpr (!RING) {
+        bool fetched = true;
+        for (; tile < tiles; tile += stride) {
+            const int r = tile * rows_per_wave + sub;
+            float ag = 0.f, au = 0.f;
+            for (int c = g; c < nch; c += G) {
+                if (!fetched) fetch(r, c, dg0, du0);
+                fetched = false;
+                uint4 xv[1][XP];
+                uint4 bv[1][2];
+#pragma unroll
+                for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
+                bv[0][0] = xb[c];
+                bv[0][1] = xb[nch + c];
+                dot_int<FMT, 1>(dg0, c, xv, bv, &ag);
+                dot_int<FMT, 1>(du0, c, xv, bv, &au);
+            }
+            ag = group_sum(ag, G);
+            au = group_sum(au, G);
+            if (r < total_rows && g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
+        }
+        return;
+    }
+    // One tile from the buffers (dg, du), whose first chunk is loaded; the
+    // next tile's first chunk goes to (ng, nu) before this one is computed.
+    auto step = [&](int t, ChunkData<FMT>& dg, ChunkData<FMT>& du, ChunkData<FMT>& ng, ChunkData<FMT>& nu) {
+        const int r = t * rows_per_wave + sub;
+        if (t + stride < tiles) fetch((t + stride) * rows_per_wave + sub, g, ng, nu);
         float ag = 0.f, au = 0.f;
         for (int c = g; c < nch; c += G) {
-            if (!fetched) fetch(r, c, dg, du);
-            fetched = false;
+            if (c != g) fetch(r, c, dg, du);  // a row longer than one chunk per lane
             uint4 xv[1][XP];
             uint4 bv[1][2];
 #pragma unroll
@@ -259,14 +302,20 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
             dot_int<FMT, 1>(dg, c, xv, bv, &ag);
             dot_int<FMT, 1>(du, c, xv, bv, &au);
         }
-        fetched = false;
         ag = group_sum(ag, G);
         au = group_sum(au, G);
         if (r < total_rows && g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
+    };
+    while (tile < tiles) {
+        step(tile, dg0, du0, dg1, du1);
+        tile += stride;
+        if (tile >= tiles) break;
+        step(tile, dg1, du1, dg0, du0);
+        tile += stride;
     }
 }
 
-template <int FMT>
+template <int FMT, bool RING>
 __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
                                                         float* y, int G, MoeBatch batch) {
     constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
@@ -299,20 +348,45 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
         }
     };
     int tile = blockIdx.x * wpb + wave;
-    // the first chunk's weights are requested before the slot activations are staged
-    ChunkData<FMT> cd;
-    float w;
-    int lc;
-    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd, w, lc);
+    const int stride = gridDim.x * wpb;
+    // the first tile's weights are requested before the slot activations are staged
+    ChunkData<FMT> cd0, cd1;
+    float w0, w1;
+    int lc0, lc1;
+    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd0, w0, lc0);
     stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb));
     __syncthreads();
-    bool fetched = true;
-    for (; tile < tiles; tile += gridDim.x * wpb) {
-        const int n = tile * rows_per_wave + sub;
+    if constexpr (!RING) {
+        bool fetched = true;
+        for (; tile < tiles; tile += stride) {
+            const int n = tile * rows_per_wave + sub;
+            float acc = 0.f;
+            for (int c = g; c < nch; c += G) {
+                if (!fetched) fetch(n, c, cd0, w0, lc0);
+                fetched = false;
+                uint4 xv[1][XP];
+                uint4 bv[1][2];
+#pragma unroll
+                for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
+                bv[0][0] = xb[c];
+                bv[0][1] = xb[nch + c];
+                float part = 0.f;
+                dot_int<FMT, 1>(cd0, lc0, xv, bv, &part);
+                acc = fmaf(w0, part, acc);
+            }
+            acc = group_sum(acc, G);
+            if (n < d.d_model && g == G - 1) y[n] = acc;
+        }
+        return;
+    }
+    // One tile from (cd, w, lc), whose first chunk is loaded; the next tile's
+    // first chunk goes to (nd, nw, nlc) before this one is computed.
+    auto step = [&](int t, ChunkData<FMT>& cd, float& w, int& lc, ChunkData<FMT>& nd, float& nw, int& nlc) {
+        const int n = t * rows_per_wave + sub;
+        if (t + stride < tiles) fetch((t + stride) * rows_per_wave + sub, g, nd, nw, nlc);
         float acc = 0.f;
         for (int c = g; c < nch; c += G) {
-            if (!fetched) fetch(n, c, cd, w, lc);
-            fetched = false;
+            if (c != g) fetch(n, c, cd, w, lc);  // the lane's later chunks of the row, in turn
             uint4 xv[1][XP];
             uint4 bv[1][2];
 #pragma unroll
@@ -323,9 +397,15 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
             dot_int<FMT, 1>(cd, lc, xv, bv, &part);
             acc = fmaf(w, part, acc);
         }
-        fetched = false;
         acc = group_sum(acc, G);
         if (n < d.d_model && g == G - 1) y[n] = acc;
+    };
+    while (tile < tiles) {
+        step(tile, cd0, w0, lc0, cd1, w1, lc1);
+        tile += stride;
+        if (tile >= tiles) break;
+        step(tile, cd1, w1, lc1, cd0, w0, lc0);
+        tile += stride;
     }
 }
 
@@ -344,9 +424,10 @@ static hipError_t glu_launch(const MoeDims& d, const MoeBank& gate, const MoeBan
     const int total_rows = d.top * d.hidden + d.hidden_shared;
     const int rows_per_block = 4 * (64 / G);
     int grid = (total_rows + rows_per_block - 1) / rows_per_block;
-    if (grid > cus * 8) grid = cus * 8;
+    const int cap = batch_grid_cap(cus, b.m);
+    if (grid > cap) grid = cap;
     const size_t lds = stage_bytes_int(FMT, 1, nch);
-    auto kernel = moe_glu_kernel<FMT, XF32, S>;
+    auto kernel = b.m > kMoeOwnRouteMax ? moe_glu_kernel<FMT, XF32, S, true> : moe_glu_kernel<FMT, XF32, S, false>;
     if (lds > 60000) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -401,15 +482,16 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
     const int G = lanes_for(nch);
     const int rows_per_block = 4 * (64 / G);
     int grid = (d.d_model + rows_per_block - 1) / rows_per_block;
-    if (grid > cus * 8) grid = cus * 8;
+    const int cap = batch_grid_cap(cus, b.m);
+    if (grid > cap) grid = cap;
     const size_t lds = stage_bytes_int(FMT, 1, nch);
+    auto kernel = b.m > kMoeOwnRouteMax ? moe_down_kernel<FMT, true> : moe_down_kernel<FMT, false>;
     if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_down_kernel<FMT>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(moe_down_kernel<FMT>, dim3(grid, b.m), dim3(kMoeThreads), lds, stream, d, down, down_sh, ws, y, G,
-                       b);
+    hipLaunchKernelGGL(kernel, dim3(grid, b.m), dim3(kMoeThreads), lds, stream, d, down, down_sh, ws, y, G, b);
     return hipGetLastError();
 }
 
