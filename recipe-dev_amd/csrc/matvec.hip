@@ -273,7 +273,7 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
 #pragma unroll
                         for (int mm = 0; mm < M; ++mm)
                             acc[r][mm] += chunk_dot_f32(cur[r], reinterpret_cast<const float4*>(smem), nch, c, mm);
-            } else {
+            } else if constexpr (M <= 8) {
                 uint4 xv[M][8];
 #pragma unroll
                 for (int mm = 0; mm < M; ++mm)
@@ -282,6 +282,19 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
 #pragma unroll
                 for (int r = 0; r < R; ++r)
                     if (row0 + r < p.rows) dot_f16w<M>(cur[r], xv, acc[r]);
+            } else {
+                // one activation row's pieces at a time (all of them would not
+                // fit in registers); each sum sees the same operations in the
+                // same order as at any other M
+#pragma unroll
+                for (int mm = 0; mm < M; ++mm) {
+                    uint4 xv[1][8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xv[0][j] = smem[(mm * 8 + j) * nch + c];
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        if (row0 + r < p.rows) dot_f16w<1>(cur[r], xv, &acc[r][mm]);
+                }
             }
         }
         if (w.s == w.steps - 1) finish_tile<M, R>(p, row0, g, acc);
@@ -388,6 +401,9 @@ static hipError_t launch_fmt(int xtype, int M, const MvParams& p, const LaunchSh
         case 32 + 2: return launch_one<FMT, 2, 2>(xtype, p, s, stream, ev0, ev1);
         case 64 + 1: return launch_one<FMT, 4, 1>(xtype, p, s, stream, ev0, ev1);
         case 128 + 1: return launch_one<FMT, 8, 1>(xtype, p, s, stream, ev0, ev1);
+        case 256 + 1:  // sixteen activation rows: F16 weights only (a router over a batch)
+            if constexpr (FMT == F16) return launch_one<FMT, 16, 1>(xtype, p, s, stream, ev0, ev1);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

@@ -177,7 +177,7 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
         return RQMV_OK;
     }
     while (done < m) {
-        int mb = 8;
+        int mb = w->fmt == rq::F16 ? 16 : 8;  // F16 (routers) takes sixteen rows per launch
         while (mb > m - done) mb >>= 1;
         while (mb > 1 && rq::matvec_lds_bytes(w->fmt, xtype, mb, (int)w->cols) > info.lds_limit) mb >>= 1;
         if (rq::matvec_lds_bytes(w->fmt, xtype, mb, (int)w->cols) > info.lds_limit)

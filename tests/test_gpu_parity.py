@@ -122,6 +122,24 @@ def test_matvec_parity(gpu, fmt, xdt, m):
         assert err <= limit, (fmt, xdt, m, rows, cols, err)
 
 
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+def test_f16_sixteen_row_launches(gpu, xdt):
+    """F16 weights (routers over a batch of positions) take sixteen activation
+    rows per launch, then eight, four, ...: every row agrees with the oracle
+    and is bit-identical to its own one-row product."""
+    rows, cols = 257, 2048
+    w = _weights("f16", rows, cols, seed=21)
+    W = gpu.Weight("f16", rows, cols, w)
+    for m in (16, 19, 33):
+        xh, dt, x32 = _x(m, cols, xdt, seed=m + 40)
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        ref = oracle.matvec_recipe_f32("f16", w, rows, cols, x32, threads=THREADS)
+        assert rel_l2(y, ref) <= (1e-5 if xdt == "f32" else 2e-4), (xdt, m)
+        for i in (0, 7, 15, m - 1):
+            one = _run_matvec(gpu, W, np.ascontiguousarray(xh[i:i + 1]), dt, rows)
+            assert np.array_equal(one[0].view(np.uint32), y[i].view(np.uint32)), (xdt, m, i)
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("xdt", ["f16", "f32"])
 @pytest.mark.parametrize("m", [16, 17, 32, 33, 40])
