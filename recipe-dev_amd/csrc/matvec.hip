@@ -1,4 +1,5 @@
-// Batch-1 and small-M (M <= 8) dequant-dot matrix-vector kernels for gfx950.
+// Batch-1 and small-M (M <= 8; F16 weights M <= 16) dequant-dot matrix-vector
+// kernels for gfx950.
 //
 // Work mapping. A wave's 64 lanes are split into 64/G groups of G lanes; a
 // group owns R consecutive rows and its lanes take chunks g, g+G, g+2G, ...

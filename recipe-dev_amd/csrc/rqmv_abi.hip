@@ -132,7 +132,8 @@ int check_launch(const rqmv_weight* w, DeviceInfo* info) {
 }
 
 // Runs y = W x over rows [first_row, first_row + rows) of a weight, M rows of x
-// at a time in blocks the VALU kernels take (8, 4, 2, 1) and LDS can hold.
+// at a time in blocks the VALU kernels take (8, 4, 2, 1; 16 for F16 weights)
+// and LDS can hold.
 int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const void* x, int xtype, int m, int64_t ldx,
                 float* y, int64_t ldy, hipStream_t stream, const DeviceInfo& info, hipEvent_t ev0 = nullptr,
                 hipEvent_t ev1 = nullptr, const rqmv_weight* extra_row = nullptr) {
