@@ -4,6 +4,8 @@ layout sizes, argument checks) behave. No GPU call is made here."""
 import ctypes
 import os
 import re
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -26,6 +28,26 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(rqmv.LIB_PATH)
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def test_missing_library_raises_instead_of_falling_back():
+    """Without librqmv.so every entry fails with RqmvError; there is no CPU
+    path to fall back to (checked in a fresh interpreter)."""
+    code = (
+        "import sys; sys.path[:0] = [%r, %r]\n"
+        "import numpy as np, rqmv\n"
+        "rqmv.LIB_PATH = '/nonexistent/librqmv.so'\n"
+        "for call in (lambda: rqmv.init(0), lambda: rqmv.Weight('q4_k', 1, 256, np.zeros(144, np.uint8)),\n"
+        "             lambda: rqmv.layout_bytes('q4_k', 1, 256)):\n"
+        "    try:\n"
+        "        call()\n"
+        "    except rqmv.RqmvError as e:\n"
+        "        assert 'not built' in str(e), e\n"
+        "    else:\n"
+        "        raise SystemExit('no error')\n"
+        "print('raised')\n" % (ROOT, os.path.join(ROOT, "recipe-dev_amd")))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and "raised" in out.stdout, out.stdout + out.stderr
 
 
 def _shapes(fmt):
