@@ -32,9 +32,10 @@ namespace rq {
 // Walks this wave's (tile, step) pairs in order: step s of a tile takes chunk
 // c = g + s*G of the tile's rows, for s < ceil(nch / G) on every lane (a lane
 // whose chunk lies past the row does no work), so the whole wave reaches each
-// tile's cross-lane reduction together.
+// tile's cross-lane reduction together. Tile and row indices are 32-bit (a
+// weight has fewer than 2^31 rows, which its 4 GiB limit implies).
 struct StepWalk {
-    int64_t tile, tiles, tile_stride, rows_per_wave;
+    int tile, tiles, tile_stride, rows_per_wave;
     int s, steps, g, G, nch;
     __device__ bool valid() const { return tile < tiles; }
     __device__ int chunk() const { return g + s * G; }
@@ -49,10 +50,10 @@ struct StepWalk {
 __device__ __forceinline__ StepWalk make_walk(const MvParams& p, int R, int g) {
     StepWalk w;
     const int wpb = p.block >> 6, wave = threadIdx.x >> 6;
-    w.rows_per_wave = (int64_t)(64 / p.G) * R;
-    w.tiles = (p.rows + w.rows_per_wave - 1) / w.rows_per_wave;
-    w.tile = (int64_t)blockIdx.x * wpb + wave;
-    w.tile_stride = (int64_t)gridDim.x * wpb;
+    w.rows_per_wave = (64 / p.G) * R;
+    w.tiles = (int)((p.rows + w.rows_per_wave - 1) / w.rows_per_wave);
+    w.tile = (int)blockIdx.x * wpb + wave;
+    w.tile_stride = (int)gridDim.x * wpb;
     w.s = 0;
     w.steps = (p.P.nch + p.G - 1) / p.G;
     w.g = g;
@@ -66,12 +67,12 @@ __device__ __forceinline__ StepWalk make_walk(const MvParams& p, int R, int g) {
 // instead; their results are never added.
 template <int FMT, int R>
 __device__ __forceinline__ void load_rows(const MvParams& p, const StepWalk& w, int sub, ChunkData<FMT> (&d)[R]) {
-    const int64_t tile = w.tile < w.tiles ? w.tile : w.tiles - 1;
-    const int64_t row0 = tile * w.rows_per_wave + (int64_t)sub * R;
+    const int tile = w.tile < w.tiles ? w.tile : w.tiles - 1;
+    const int row0 = tile * w.rows_per_wave + sub * R, rows = (int)p.rows;
     const int c = w.chunk() < w.nch ? w.chunk() : w.nch - 1;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int64_t row = row0 + r < p.rows ? row0 + r : p.rows - 1;
+        const int row = row0 + r < rows ? row0 + r : rows - 1;
         if constexpr (FMT == F16) {
             const bool second = row >= p.split;
             Planes P = p.P;
@@ -87,7 +88,7 @@ __device__ __forceinline__ void load_rows(const MvParams& p, const StepWalk& w, 
 // epilogue runs with M = 1 and an even R, so that a lane group holds each
 // (gate, up) row pair). NORM: the rmsnorm factor multiplies the sums first.
 template <int M, int R, bool NORM = false>
-__device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int g, float (&acc)[R][M],
+__device__ __forceinline__ void finish_tile(const MvParams& p, int row0, int g, float (&acc)[R][M],
                                             float norm_scale = 1.f) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -100,14 +101,14 @@ __device__ __forceinline__ void finish_tile(const MvParams& p, int64_t row0, int
         if (p.epi == kEpiPlain) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows)
+                if (row0 + r < (int)p.rows)
 #pragma unroll
                     for (int mm = 0; mm < M; ++mm) p.y[(int64_t)mm * p.ldy + row0 + r] = acc[r][mm];
         } else {
             // silu(gate) * up, silu(v) = v * sigmoid(v), sigmoid = 0.5 (tanh(v / 2) + 1) (recipe.rs:22662-22668)
 #pragma unroll
             for (int r = 0; r + 1 < R; r += 2)
-                if (row0 + r + 1 < p.rows) {
+                if (row0 + r + 1 < (int)p.rows) {
                     const float gt = acc[r][0];
                     p.y[(row0 + r) / 2] = gt * (0.5f * (tanhf(0.5f * gt) + 1.0f)) * acc[r + 1][0];
                 }
@@ -126,9 +127,9 @@ template <int FMT, int R>
 __device__ __forceinline__ void load_rows_rs(const MvParams& p, __amdgpu_buffer_rsrc_t rs, const StepWalk& w, int sub,
                                              ChunkData<FMT> (&d)[R]) {
     const bool live = w.tile < w.tiles && w.chunk() < w.nch;
-    const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+    const int row0 = w.tile * w.rows_per_wave + sub * R, rows = (int)p.rows;
 #pragma unroll
-    for (int r = 0; r < R; ++r) load_chunk_rs<FMT>(rs, p.P, (uint32_t)(row0 + r), w.chunk(), live && row0 + r < p.rows, d[r]);
+    for (int r = 0; r < R; ++r) load_chunk_rs<FMT>(rs, p.P, (uint32_t)(row0 + r), w.chunk(), live && row0 + r < rows, d[r]);
 }
 
 // One step of matvec_int: the lane's chunk of its R rows against the staged
@@ -139,7 +140,7 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
     constexpr int XP = Traits<FMT>::XP;
     const int nch = p.P.nch;
     const int c = w.chunk();
-    const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+    const int row0 = w.tile * w.rows_per_wave + sub * R, rows = (int)p.rows;
     if (c < nch) {
         // one activation row's digits live at a time; the weights stay in registers
 #pragma unroll
@@ -152,7 +153,7 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
             bv[0][1] = xb[(mm * 2 + 1) * nch + c];
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < p.rows) dot_int<FMT, 1>(d[r], c, xv, bv, &acc[r][mm]);
+                if (row0 + r < rows) dot_int<FMT, 1>(d[r], c, xv, bv, &acc[r][mm]);
         }
     }
     if (w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, norm_scale);
@@ -265,12 +266,12 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
         if (!loaded) load_rows<F16, R>(p, w, sub, cur);
         loaded = false;
         const int c = w.chunk();
-        const int64_t row0 = w.tile * w.rows_per_wave + (int64_t)sub * R;
+        const int row0 = w.tile * w.rows_per_wave + sub * R, rows = (int)p.rows;
         if (c < nch) {
             if constexpr (XF32) {
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    if (row0 + r < p.rows)
+                    if (row0 + r < rows)
 #pragma unroll
                         for (int mm = 0; mm < M; ++mm)
                             acc[r][mm] += chunk_dot_f32(cur[r], reinterpret_cast<const float4*>(smem), nch, c, mm);
@@ -282,7 +283,7 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
                     for (int j = 0; j < 8; ++j) xv[mm][j] = smem[(mm * 8 + j) * nch + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    if (row0 + r < p.rows) dot_f16w<M>(cur[r], xv, acc[r]);
+                    if (row0 + r < rows) dot_f16w<M>(cur[r], xv, acc[r]);
             } else {
                 // one activation row's pieces at a time (all of them would not
                 // fit in registers); each sum sees the same operations in the
@@ -294,7 +295,7 @@ __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
                     for (int j = 0; j < 8; ++j) xv[0][j] = smem[(mm * 8 + j) * nch + c];
 #pragma unroll
                     for (int r = 0; r < R; ++r)
-                        if (row0 + r < p.rows) dot_f16w<1>(cur[r], xv, &acc[r][mm]);
+                        if (row0 + r < rows) dot_f16w<1>(cur[r], xv, &acc[r][mm]);
                 }
             }
         }
