@@ -245,7 +245,12 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     constexpr int HALF = HD / 2;
     __shared__ float sc[MAXG][kAttnChunk];
     __shared__ float ml[MAXG][2];
-    __shared__ float red[kAttnWaves][MAXG * HD];
+    // the partial outputs: with at most four query heads, one padded row per
+    // position slot of the workgroup; with more, one row per wave
+    constexpr bool kSlotRows = MAXG <= 4;
+    constexpr int kRedRows = kSlotRows ? kAttnThreads / (HD / 8) : kAttnWaves;
+    constexpr int kRedStride = MAXG * HD + (kSlotRows ? 4 : 0);
+    __shared__ float red[kRedRows * kRedStride];
     const int kh = blockIdx.x, chunk = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int b = t % LPP, slot = t / LPP;
@@ -372,25 +377,36 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
             for (int e = 0; e < 8; ++e) o[g][e] = fmaf(wgt, vv[e], o[g][e]);
         }
     }
+    if constexpr (kSlotRows) {
+        // every lane's sums go to its slot's row; each output then adds the
+        // rows in slot order (fewer instructions than lane exchanges)
+        float* row = red + slot * kRedStride + b * 8;
 #pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            if constexpr (LPP <= 8) o[g][e] += __shfl_xor(o[g][e], 8);
-            if constexpr (LPP <= 16) o[g][e] = swap16_sum(o[g][e]);
-            o[g][e] = swap32_sum(o[g][e]);
+        for (int g = 0; g < MAXG; ++g) {
+            *reinterpret_cast<float4*>(row + g * HD) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+            *reinterpret_cast<float4*>(row + g * HD + 4) = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
         }
-    if (lane < LPP) {
+    } else {
 #pragma unroll
         for (int g = 0; g < MAXG; ++g)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) red[wave][g * HD + b * 8 + e] = o[g][e];
+            for (int e = 0; e < 8; ++e) {
+                if constexpr (LPP <= 8) o[g][e] += __shfl_xor(o[g][e], 8);
+                if constexpr (LPP <= 16) o[g][e] = swap16_sum(o[g][e]);
+                o[g][e] = swap32_sum(o[g][e]);
+            }
+        if (lane < LPP) {
+#pragma unroll
+            for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) red[wave * kRedStride + g * HD + b * 8 + e] = o[g][e];
+        }
     }
     __syncthreads();
     for (int i = t; i < group * HD; i += kAttnThreads) {
         float acc = 0.f;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) acc += red[w][i];
+        for (int r = 0; r < kRedRows; ++r) acc += red[r * kRedStride + i];
         const int g = i / HD, d = i % HD;
         ws.o[((size_t)(kh * group + g) * nchunks + chunk) * HD + d] = acc;
     }
