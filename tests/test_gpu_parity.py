@@ -349,11 +349,14 @@ def test_bad_arguments_return_errors(gpu):
         gpu.Moe(Wr, W, W, W, 2)  # banks are not 8-expert banks
 
 
-@pytest.mark.parametrize("m,xdt", [(2, "f16"), (5, "f32"), (8, "f16")])
+@pytest.mark.parametrize("m,xdt", [(2, "f16"), (5, "f32"), (8, "f16"), (16, "f32"), (19, "f16"), (64, "f16")])
 def test_moe_batch_parity(gpu, m, xdt):
     """A prefill batch of positions through rqmv_moe_batch: each position routed
     on its own, against the oracle position by position, and equal to the
-    one-position call bit for bit."""
+    one-position call bit for bit. From three positions on, the launches hold
+    at most eight workgroups per CU over the batch (at 64 positions each wave
+    walks two tiles of this model's gate/up and down rows) and the router takes
+    sixteen positions per launch."""
     fmt, d, E, top, H, HS = "q4_k", 512, 32, 4, 256, 256
     router, gate, up, down, shared = _moe_case(fmt, d, E, top, H, HS, True, seed=77)
     xh, dt, x32 = _x(m, d, xdt, seed=78)
