@@ -71,7 +71,10 @@ const char* rqmv_last_error(void);
 /* Uploads rows x cols weights given as GGUF block bytes (row-major: row r is
  * cols/block consecutive blocks, recipe.rs:9875-9889), repacked into the
  * kernels' layout. Replaces StoredWeight + Buffer::fill_weights with
- * row_interleave (recipe.rs:15859-16069, 26980-27010, 3162-3212). */
+ * row_interleave (recipe.rs:15859-16069, 26980-27010, 3162-3212).
+ * cols is a whole number of blocks (32 for Q8_0/Q4_0, 256 for Q4_K/Q6_K) and
+ * a multiple of 32; F16 rows are packed in 64-value chunks, so an F16 weight
+ * (a router) needs a multiple of 64. Other widths are RQMV_EINVAL. */
 int rqmv_weight_create(int format, int64_t rows, int64_t cols, const void* gguf_bytes, size_t nbytes,
                        rqmv_weight** out);
 
@@ -129,7 +132,12 @@ typedef struct {
     float scale;        /* routed weight scale (1 = none) */
 } rqmv_moe_params;
 
-/* Device workspace bytes rqmv_moe needs for one position. */
+/* Device workspace bytes rqmv_moe needs for one position. It also checks the
+ * parameters: the banks are quantized, the hidden width and d_model are
+ * multiples of the bank format's 16-byte-part chunk (32 values for Q8_0, 64
+ * for Q4_0, a superblock's 256 for Q4_K/Q6_K), the router is F16 (d_model a
+ * multiple of 64), and top is in 1..min(64, experts) with at most 2048 experts;
+ * otherwise RQMV_EINVAL. */
 int rqmv_moe_workspace_size(const rqmv_moe_params* params, size_t* bytes);
 
 /* One position: x (d_model, f16 or f32) -> y (d_model, fp32). The routing

@@ -89,7 +89,9 @@ int create(int format, int64_t experts, int64_t rows, int64_t cols, const void* 
     if (cols > (1 << 30)) return fail(RQMV_EINVAL, "cols too large");
     const int64_t total_rows = experts * rows;
     const int64_t want = rq::gguf_bytes(format, total_rows, cols);
-    if (want < 0) return fail(RQMV_EINVAL, "cols is not a whole number of blocks for this format");
+    if (want < 0)
+        return fail(RQMV_EINVAL, "cols is not a whole number of blocks for this format (a multiple of 32, and of "
+                                 "256 for Q4_K/Q6_K and 64 for F16)");
     if (!bytes || (size_t)want != nbytes)
         return fail(RQMV_EINVAL, "expected " + std::to_string(want) + " GGUF bytes, got " + std::to_string(nbytes));
     DeviceInfo info;
