@@ -86,7 +86,7 @@ def test_rope_kv_position_outside_cache_writes_nothing(gpu):
     assert not np.any(K.download(np.uint16)) and not np.any(V.download(np.uint16))
 
 
-@pytest.mark.parametrize("nq,nkv,hd", [(4, 2, 64), (32, 8, 128), (8, 1, 128), (4, 4, 256)])
+@pytest.mark.parametrize("nq,nkv,hd", [(4, 2, 64), (32, 8, 128), (8, 1, 128), (4, 4, 256), (12, 4, 128), (24, 4, 64)])
 @pytest.mark.parametrize("length", [1, 127, 128, 129, 300])
 def test_attention(gpu, nq, nkv, hd, length):
     max_ctx = 384
@@ -285,7 +285,7 @@ def test_fused_rejects_bad_arguments(gpu):
         gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN, D, 1e-5, D, X)  # x_out over x
 
 
-@pytest.mark.parametrize("nq,nkv,hd", [(32, 8, 128), (4, 2, 64), (8, 1, 256)])
+@pytest.mark.parametrize("nq,nkv,hd", [(32, 8, 128), (4, 2, 64), (8, 1, 256), (12, 4, 128), (24, 4, 64)])
 @pytest.mark.parametrize("pos", [0, 63, 64, 300, 4099])
 def test_attention_rope_fused(gpu, nq, nkv, hd, pos):
     """Rotary, cache append and attention in one call, against the f64
