@@ -426,9 +426,11 @@ hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const Lau
     }
 }
 
-LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus) {
+LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu) {
     LaunchShape s = plan_matvec(fmt, rows, cols, 1, X_F32, cus);
-    s.R = 2;  // a lane group holds a (gate, up) row pair for kEpiGlu
+    // a lane group holds a (gate, up) row pair for kEpiGlu; otherwise Q8_0
+    // takes one row, as in plan_matvec
+    s.R = glu || fmt != Q8_0 ? 2 : 1;
     if (s.block > 512) s.block = 512;
     const int64_t rows_per_wave = (int64_t)(64 / s.G) * s.R;
     const int64_t tiles = (rows + rows_per_wave - 1) / rows_per_wave;
@@ -439,15 +441,17 @@ LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus) {
     return s;
 }
 
-template <int FMT>
+template <int FMT, int R = 2>
 static hipError_t launch_fused_fmt(const MvParams& p, const LaunchShape& s, hipStream_t stream) {
     const size_t lds = matvec_lds_bytes(FMT, X_F32, 1, p.K);
-    if (p.norm_w) return launch_kernel(matvec_int<FMT, 1, 2, true, true>, p, s, lds, stream, nullptr, nullptr);
-    return launch_kernel(matvec_int<FMT, 1, 2, true>, p, s, lds, stream, nullptr, nullptr);
+    if (p.norm_w) return launch_kernel(matvec_int<FMT, 1, R, true, true>, p, s, lds, stream, nullptr, nullptr);
+    return launch_kernel(matvec_int<FMT, 1, R, true>, p, s, lds, stream, nullptr, nullptr);
 }
 
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream) {
-    if (s.R != 2 || s.block > 512) return hipErrorInvalidValue;
+    if (s.block > 512) return hipErrorInvalidValue;
+    if (s.R == 1 && fmt == Q8_0 && p.epi != kEpiGlu) return launch_fused_fmt<Q8_0, 1>(p, s, stream);
+    if (s.R != 2) return hipErrorInvalidValue;
     switch (fmt) {
         case Q4_0: return launch_fused_fmt<Q4_0>(p, s, stream);
         case Q8_0: return launch_fused_fmt<Q8_0>(p, s, stream);

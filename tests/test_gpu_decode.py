@@ -229,7 +229,8 @@ def _mv_ref(fmt, w, rows, cols, x):
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 6144, 4096), ("q8_0", 4096, 4096), ("q6_k", 512, 1024),
-                                           ("q4_0", 300, 4096), ("q4_k", 256, 14336)])
+                                           ("q4_0", 300, 4096), ("q4_k", 256, 14336), ("q8_0", 1001, 544),
+                                           ("q8_0", 3, 32)])
 @pytest.mark.parametrize("with_delta", [False, True])
 def test_fused_norm_prologue(gpu, fmt, rows, cols, with_delta):
     w = synth.weights(fmt, rows, cols, seed=rows + cols)
@@ -271,6 +272,22 @@ def test_fused_glu_epilogue(gpu, fmt, n, cols):
     z = Z.download(np.float32)
     assert rel_err(z[0::2], _mv_ref(fmt, g, n, cols, x)) < 1e-3
     assert rel_err(z[1::2], _mv_ref(fmt, u, n, cols, x)) < 1e-3
+
+
+@pytest.mark.parametrize("fmt,rows,cols", [("q8_0", 1001, 544), ("q8_0", 4096, 4096), ("q4_0", 77, 128)])
+def test_fused_plain_without_norm(gpu, fmt, rows, cols):
+    """The fused entry point with neither prologue nor epilogue equals the plain
+    product bit for bit (one launch shape per format and row count)."""
+    w = synth.weights(fmt, rows, cols, seed=rows)
+    W = gpu.Weight(fmt, rows, cols, w)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    X, Y, Z = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * rows), gpu.DeviceBuffer(4 * rows)
+    gpu.matvec_fused(W, X, Y, gpu.EPI_PLAIN)
+    W.matvec(X, gpu.DTYPE_F32, 1, cols, Z, rows)
+    gpu.synchronize()
+    y = Y.download(np.float32)
+    assert rel_err(y, _mv_ref(fmt, w, rows, cols, x)) < 1e-3
+    assert np.array_equal(y.view(np.uint32), Z.download(np.float32).view(np.uint32))
 
 
 def test_fused_rejects_bad_arguments(gpu):
