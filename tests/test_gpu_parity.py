@@ -349,6 +349,18 @@ def test_bad_arguments_return_errors(gpu):
         gpu.Moe(Wr, W, W, W, 2)  # banks are not 8-expert banks
 
 
+def test_weight_of_4_gib_is_rejected(gpu):
+    """Kernel offsets are 32-bit: a weight or bank whose repacked bytes reach
+    4 GiB - 256 B is refused before any copy. The zero buffer is never read, so
+    its pages are never touched."""
+    cols = 4096
+    big = np.zeros(1_000_000 * (cols // 32) * 34, np.uint8)  # Q8_0, 4.35 GB
+    with pytest.raises(gpu.RqmvError, match="4 GiB"):
+        gpu.Weight("q8_0", 1_000_000, cols, big)
+    with pytest.raises(gpu.RqmvError, match="4 GiB"):
+        gpu.Weight("q8_0", 4000, cols, big, experts=250)
+
+
 @pytest.mark.parametrize("m,xdt", [(2, "f16"), (5, "f32"), (8, "f16"), (16, "f32"), (19, "f16"), (64, "f16")])
 def test_moe_batch_parity(gpu, m, xdt):
     """A prefill batch of positions through rqmv_moe_batch: each position routed
