@@ -38,6 +38,7 @@ MALL_BYTES = 256 * 2 ** 20
 WORKLOADS = {
     "q4_k_up": ("q4_k", 14336, 4096, "f16", "Q4_K matvec 4096->14336 batch 1 (FFN up/gate)"),
     "q4_k_down": ("q4_k", 4096, 14336, "f16", "Q4_K matvec 14336->4096 batch 1 (FFN down)"),
+    "q4_k_4096": ("q4_k", 4096, 4096, "f16", "Q4_K matvec 4096->4096 batch 1 (attention output)"),
     "q4_0_up": ("q4_0", 14336, 4096, "f16", "Q4_0 matvec 4096->14336 batch 1"),
     "q4_0_down": ("q4_0", 4096, 14336, "f16", "Q4_0 matvec 14336->4096 batch 1"),
     "q8_0_4096": ("q8_0", 4096, 4096, "f32", "Q8_0 matvec 4096x4096, fp32 activations"),

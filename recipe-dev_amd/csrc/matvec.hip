@@ -352,6 +352,13 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     const bool long_rows = nch > 128;
     s.block = long_rows ? 512 : 256;
     int per_cu = long_rows ? 1 : 2;
+    // Small products, whose tiles would not give every CU a workgroup, spread
+    // them over smaller workgroups of one row per lane group (the MoE router,
+    // 257 x 2048 F16: 17 -> 65 workgroups, 4.6 -> 3.8 us)
+    if (((rows + (64 / G) * s.R - 1) / ((64 / G) * s.R) + s.block / 64 - 1) / (s.block / 64) < cus) {
+        s.R = 1;
+        s.block = 128;
+    }
     s.G = env_int("RQMV_G", s.G);
     s.R = env_int("RQMV_R", s.R);
     s.block = env_int("RQMV_BLOCK", s.block);
