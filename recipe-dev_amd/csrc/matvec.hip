@@ -354,8 +354,8 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     int per_cu = long_rows ? 1 : 2;
     // Small products at one or two activation rows, whose tiles would not give
     // every CU a workgroup, spread them over smaller workgroups of one row per
-    // lane group (the MoE router, 257 x 2048 F16: 17 -> 65 workgroups, 4.6 ->
-    // 3.8 us). With 16 rows the smaller workgroups stage x twice as often and
+    // lane group (the MoE router, 257 x 2048 F16: 17 -> 65 workgroups; the MoE
+    // step 19.7 -> 18.9 us). With 16 rows the smaller workgroups stage x twice as often and
     // the batched router measured slower (MoE step at 16 positions 82.4 -> 85.0 us).
     if (M <= 2 && ((rows + (64 / G) * s.R - 1) / ((64 / G) * s.R) + s.block / 64 - 1) / (s.block / 64) < cus) {
         s.R = 1;
