@@ -281,7 +281,7 @@ def decode_bench(args):
     log(f"bench: model built in {time.perf_counter() - t0:.1f} s")
     stream = rqmv.Stream()
     model.set_position(1, ctx)
-    model.enqueue_step(stream)  # one eager step first
+    model.step(stream)  # one eager step first
     stream.synchronize()
     logits = model.read_logits()
     tok = model.read_token()
@@ -291,14 +291,12 @@ def decode_bench(args):
         log("bench: decode step check failed")
         sys.exit(1)
     graph = model.capture(stream)
-    for _ in range(args.warmup):
-        graph.launch(stream)
+    model.replay(graph, stream, args.warmup)
     stream.synchronize()
     pos0 = model.read_position()
     e0, e1 = rqmv.Event(), rqmv.Event()
     e0.record(stream)
-    for _ in range(args.steps):
-        graph.launch(stream)
+    model.replay(graph, stream, args.steps)
     e1.record(stream)
     e1.synchronize()
     total_ms = e0.elapsed_ms(e1)

@@ -24,6 +24,9 @@
  *     amd-nv-cpu.ll:1161-1165; pass the transpose). Outputs y are fp32, row m
  *     of N values at y + m*ldy. Rows of x start 16-byte aligned (x and
  *     ldx * element size multiples of 16), as device allocations are.
+ *   - A NaN or an infinity in an activation row makes that row's outputs
+ *     non-finite (NaN where recipe's fp32 sums may give +-inf), never finite;
+ *     rqmv_matvec_int8 requires finite activations.
  */
 #ifndef RQMV_H
 #define RQMV_H
@@ -49,6 +52,19 @@ typedef enum { RQMV_DTYPE_F32 = 0, RQMV_DTYPE_F16 = 1 } rqmv_dtype;
 
 /* Routing score function (recipe's Scoring: softmax = 0, sigmoid = 1). */
 typedef enum { RQMV_SCORE_SOFTMAX = 0, RQMV_SCORE_SIGMOID = 1 } rqmv_scoring;
+
+/* recipe's Activation, by its saved code (Activation::code,
+ * recipe.rs:13925-13950), with the programs of activation_program
+ * (recipe.rs:22579-22727) and recipe's default constants (Cargo.toml:117-124).
+ * RQMV_ACT_GELU_FP16 is Gelu as the llama.cpp profile's gelu table computes
+ * it. RQMV_ACT_SCALE multiplies by the factor given beside the code, and
+ * RQMV_ACT_PRELU takes that factor as its slope. */
+typedef enum {
+    RQMV_ACT_LINEAR = 0, RQMV_ACT_COS = 1, RQMV_ACT_EXP = 2, RQMV_ACT_LOG = 3, RQMV_ACT_LN = 4,
+    RQMV_ACT_HUBER = 5, RQMV_ACT_TAN = 6, RQMV_ACT_RELU = 7, RQMV_ACT_LEAK = 8, RQMV_ACT_SIGMOID = 9,
+    RQMV_ACT_TANH = 10, RQMV_ACT_SELU = 11, RQMV_ACT_GELU = 12, RQMV_ACT_SILU = 13, RQMV_ACT_ELU = 14,
+    RQMV_ACT_PRELU = 15, RQMV_ACT_SCALE = 16, RQMV_ACT_SQRT = 17, RQMV_ACT_SOFTPLUS = 18, RQMV_ACT_GELU_FP16 = 32
+} rqmv_activation;
 
 enum {
     RQMV_OK = 0,
@@ -116,7 +132,12 @@ int rqmv_expert_matvec(const rqmv_weight* bank, int64_t expert, const void* x_de
                        float* y_dev, int64_t ldy, void* stream);
 
 /* The gguf_moe block (recipe.rs:14722, lowered at 23415-23459): router,
- * top-k routing, routed SiLU-GLU experts and an optional gated shared expert. */
+ * top-k routing, routed gated experts and an optional shared expert. Every
+ * argument of gguf_moe(experts, top_k, hidden, activation, scoring,
+ * renormalize, shared, scale, selection_bias) has a field here: experts and
+ * hidden are the banks' shapes; shared is SharedExpert::None (no shared
+ * weights), ::Ungated (shared weights, shared_gate_inp NULL: weight one) or
+ * ::Gated { gate } (shared_gate_inp and shared_gate_activation = gate). */
 typedef struct {
     const rqmv_weight* router;      /* F16, experts x d_model (ffn_gate_inp) */
     const rqmv_weight* gate_exps;   /* bank: experts x hidden x d_model (ffn_gate_exps) */
@@ -130,6 +151,13 @@ typedef struct {
     int scoring;        /* rqmv_scoring */
     int renormalize;    /* divide the kept weights by their total */
     float scale;        /* routed weight scale (1 = none) */
+    int activation;     /* rqmv_activation of every expert: act(gate x) * (up x) (lower_gated,
+                           recipe.rs:23279-23286); RQMV_ACT_SILU for llama-style experts */
+    int shared_gate_activation; /* rqmv_activation of the shared gate (SharedExpert::Gated's gate) */
+    float activation_factor;    /* RQMV_ACT_SCALE's constant, RQMV_ACT_PRELU's slope (else unused) */
+    const float* selection_bias; /* device, experts fp32 values (exp_probs_b.bias) or NULL: the top-k
+                                    key becomes the expert's probability plus its bias, the weights
+                                    stay those of the unbiased scores (topk_key, amd-nv-cpu.ll:4653-4660) */
 } rqmv_moe_params;
 
 /* Device workspace bytes rqmv_moe needs for one position. It also checks the

@@ -44,9 +44,11 @@ def lib():
         L.orc_matvec_recipe_f32.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int64, c_void_p,
                                             c_int64, c_int]
         L.orc_topk.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_void_p]
-        L.orc_moe_f64.argtypes = [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_double, c_void_p, c_void_p,
-                                  c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                  c_void_p, c_void_p]
+        L.orc_topk_biased.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]
+        L.orc_activation.argtypes = [c_int, c_double, c_double, c_void_p]
+        L.orc_moe_f64.argtypes = [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_double, c_int, c_double,
+                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
         L.orc_q4k_q81_reference.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
         L.orc_q4k_xorshift_rows.argtypes = [c_uint32, c_int64, c_uint16, c_void_p]
         L.orc_q8_records.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_void_p]
@@ -114,17 +116,43 @@ def matvec_recipe_f32(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray
     return y
 
 
-def topk(scores: np.ndarray, top: int, scoring: int = 0, renormalize: bool = True) -> np.ndarray:
+# recipe's Activation::code() values (recipe.rs:13925-13950); "gelu_fp16" is
+# Gelu under the llama.cpp profile's gelu table.
+ACTIVATIONS = {"linear": 0, "cos": 1, "exp": 2, "log": 3, "ln": 4, "huber": 5, "tan": 6, "relu": 7, "leak": 8,
+               "sigmoid": 9, "tanh": 10, "selu": 11, "gelu": 12, "silu": 13, "elu": 14, "prelu": 15, "scale": 16,
+               "sqrt": 17, "softplus": 18, "gelu_fp16": 32}
+
+
+def _act(a) -> int:
+    return ACTIVATIONS[a] if isinstance(a, str) else int(a)
+
+
+def activation(act, x, factor: float = 0.0) -> np.ndarray:
+    """recipe's activation program applied elementwise in f64."""
+    xs = np.asarray(x, dtype=np.float64).reshape(-1)
+    out = np.empty_like(xs)
+    r = c_double()
+    for i, v in enumerate(xs):
+        assert lib().orc_activation(_act(act), factor, float(v), ctypes.byref(r)) == 1
+        out[i] = r.value
+    return out.reshape(np.shape(x))
+
+
+def topk(scores: np.ndarray, top: int, scoring: int = 0, renormalize: bool = True, bias=None) -> np.ndarray:
     s = np.ascontiguousarray(scores, dtype=np.float64)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float64)
     w = np.empty_like(s)
-    rc = lib().orc_topk(s.ctypes.data, s.size, top, scoring, 1 if renormalize else 0, w.ctypes.data)
+    rc = lib().orc_topk_biased(s.ctypes.data, s.size, top, scoring, 1 if renormalize else 0, _ptr(b), w.ctypes.data)
     assert rc == 0, rc
     return w
 
 
 def moe_f64(fmt, d_model, experts, top, hidden, router_bits, gate, up, down, x, scoring=0, renormalize=True,
-            scale=1.0, hidden_shared=0, shared_gate_bits=None, gate_sh=None, up_sh=None, down_sh=None):
-    """Returns (y float64 (d_model,), routing weights float64 (experts,))."""
+            scale=1.0, hidden_shared=0, shared_gate_bits=None, gate_sh=None, up_sh=None, down_sh=None,
+            activation="silu", shared_gate_activation="sigmoid", activation_factor=0.0, selection_bias=None):
+    """Returns (y float64 (d_model,), routing weights float64 (experts,)).
+    A shared expert (gate_sh, up_sh, down_sh) is weighted by
+    shared_gate_activation(shared_gate . x), or by one without shared_gate_bits."""
     r = np.ascontiguousarray(router_bits, dtype=np.uint16)
     xs = np.ascontiguousarray(x, dtype=np.float64)
     y = np.empty(d_model, np.float64)
@@ -132,9 +160,11 @@ def moe_f64(fmt, d_model, experts, top, hidden, router_bits, gate, up, down, x, 
     conv = lambda a, t: None if a is None else np.ascontiguousarray(a, dtype=t)  # noqa: E731
     sg, gs, us, ds = conv(shared_gate_bits, np.uint16), conv(gate_sh, np.uint8), conv(up_sh, np.uint8), conv(down_sh, np.uint8)
     g, u, d = conv(gate, np.uint8), conv(up, np.uint8), conv(down, np.uint8)
+    sb = conv(selection_bias, np.float64)
     rc = lib().orc_moe_f64(_fmt(fmt), d_model, experts, top, hidden, scoring, 1 if renormalize else 0, scale,
-                           r.ctypes.data, g.ctypes.data, u.ctypes.data, d.ctypes.data, hidden_shared, _ptr(sg),
-                           _ptr(gs), _ptr(us), _ptr(ds), xs.ctypes.data, y.ctypes.data, rw.ctypes.data)
+                           _act(activation), activation_factor, _ptr(sb), r.ctypes.data, g.ctypes.data, u.ctypes.data,
+                           d.ctypes.data, hidden_shared, _ptr(sg), _act(shared_gate_activation), _ptr(gs), _ptr(us),
+                           _ptr(ds), xs.ctypes.data, y.ctypes.data, rw.ctypes.data)
     assert rc == 0, rc
     return y, rw
 

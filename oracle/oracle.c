@@ -278,14 +278,25 @@ static double topk_score(double score, double maximum, int sigmoid) {
     return sigmoid ? sigmoid_ref(score) : exp(score - maximum);
 }
 
-/* @topk_forward_body (amd-nv-cpu.ll:4653-4716) without a selection bias:
- * repeated scans pick the highest unmarked score, the lower expert on a tie;
- * the maximum and total run over the kept set when renormalizing, over every
- * expert otherwise; softmax (or renormalized sigmoid) divides by the total. */
-int orc_topk(const double* scores, int experts, int top, int scoring, int renormalize, double* weights) {
+/* @topk_forward_body (amd-nv-cpu.ll:4653-4716): repeated scans pick the
+ * highest unmarked key, the lower expert on a tie (a strict greater-than over
+ * ascending ids). The key (@topk_key, amd-nv-cpu.ll:4653-4660) is the raw
+ * score without a selection bias; with one it is the expert's probability
+ * (its sigmoid, or its softmax over every expert: exp(score - max) / total,
+ * the maximum and total taken over all experts first) plus its bias. The
+ * weights come from the unbiased scores: the maximum and total run over the
+ * kept set when renormalizing, over every expert otherwise; softmax (or
+ * renormalized sigmoid) divides by the total. */
+int orc_topk_biased(const double* scores, int experts, int top, int scoring, int renormalize, const double* bias,
+                    double* weights) {
     if (experts <= 0 || top <= 0 || top > experts) return -1;
     const int sigmoid = scoring != 0, renorm = renormalize != 0;
     const int every = !renorm, divide = renorm || !sigmoid;
+    double all_max = 0.0;
+    for (int e = 0; e < experts; ++e)
+        if (e == 0 || scores[e] > all_max) all_max = scores[e];
+    double all_total = 0.0;
+    for (int e = 0; e < experts; ++e) all_total = all_total + topk_score(scores[e], all_max, sigmoid);
     for (int e = 0; e < experts; ++e) weights[e] = 0.0;
     for (int pick = 0; pick < top; ++pick) {
         int best = -1;
@@ -293,6 +304,10 @@ int orc_topk(const double* scores, int experts, int top, int scoring, int renorm
         for (int c = 0; c < experts; ++c) {
             int unmarked = weights[c] == 0.0;
             double key = scores[c];
+            if (bias) {
+                const double raw = topk_score(scores[c], all_max, sigmoid);
+                key = (sigmoid ? raw : raw / all_total) + bias[c];
+            }
             int better = best == -1 || key > best_score;
             if (unmarked && better) {
                 best = c;
@@ -323,10 +338,90 @@ int orc_topk(const double* scores, int experts, int top, int scoring, int renorm
     return 0;
 }
 
-/* SiLU and Sigmoid as recipe lowers them (recipe.rs:22662-22668):
- * sigmoid = 0.5 * (tanh(x / 2) + 1), silu = x * sigmoid. */
-static double act_sigmoid(double x) { return 0.5 * (tanh(0.5 * x) + 1.0); }
-static double act_silu(double x) { return x * act_sigmoid(x); }
+int orc_topk(const double* scores, int experts, int top, int scoring, int renormalize, double* weights) {
+    return orc_topk_biased(scores, experts, top, scoring, renormalize, NULL, weights);
+}
+
+/* fp16 rounding of an f64 value (RNE, as the Half scalar op rounds the GELU
+ * table's input and output), back to f64. */
+static double half_round(double v) { return (double)orc_f32_from_fp16(orc_fp16_rne((float)v)); }
+
+/* Activation::code() values (recipe.rs:13925-13950). */
+enum {
+    ACT_LINEAR = 0, ACT_COS = 1, ACT_EXP = 2, ACT_LOG = 3, ACT_LN = 4, ACT_HUBER = 5, ACT_TAN = 6, ACT_RELU = 7,
+    ACT_LEAK = 8, ACT_SIGMOID = 9, ACT_TANH = 10, ACT_SELU = 11, ACT_GELU = 12, ACT_SILU = 13, ACT_ELU = 14,
+    ACT_PRELU = 15, ACT_SCALE = 16, ACT_SQRT = 17, ACT_SOFTPLUS = 18, ACT_GELU_FP16 = 32
+};
+
+/* recipe's activation programs (activation_program, recipe.rs:22579-22727)
+ * in f64, with the default constants of Cargo.toml:117-124 (leak slope 0.01,
+ * ELU alpha 1, SELU alpha/scale, GELU scale sqrt(2/pi) and cubic 0.044715,
+ * Huber threshold 1). `factor` is Scale's constant and PReLU's slope.
+ * ACT_GELU_FP16 is Gelu under the llama.cpp profile's gelu table (its input
+ * and result rounded to fp16 inside (-10, 10); the input itself at 10 and
+ * above, zero at -10 and below). Returns 0 for an unknown code. */
+int orc_activation(int code, double factor, double x, double* out) {
+    const double one = 1.0, half = 0.5;
+    const int positive = x > 0.0;
+    double r;
+    switch (code) {
+        case ACT_LINEAR: r = x; break;
+        case ACT_COS: r = cos(x); break;
+        case ACT_EXP: r = exp(x); break;
+        case ACT_SQRT: r = sqrt(x); break;
+        case ACT_SOFTPLUS: r = (positive ? x : 0.0) + log(one + exp(0.0 - fabs(x))); break;
+        case ACT_LOG:
+        case ACT_LN: {
+            const double magnitude = log(one + fabs(x));
+            const double signed_ = positive ? magnitude : 0.0 - magnitude;
+            r = code == ACT_LOG ? signed_ / 2.302585092994045684 : signed_;
+            break;
+        }
+        case ACT_HUBER: {
+            const double t = 1.0, a = fabs(x);
+            r = a > t ? t * (a - half * t) : half * (x * x);
+            break;
+        }
+        case ACT_TAN: r = sin(x) / cos(x); break;
+        case ACT_RELU: r = positive ? x : 0.0; break;
+        case ACT_LEAK: r = positive ? x : 0.01 * x; break;
+        case ACT_PRELU: r = positive ? x : factor * x; break;
+        case ACT_ELU:
+        case ACT_SELU: {
+            const double alpha = code == ACT_SELU ? 1.6732632423543772 : 1.0;
+            const double masked = positive ? 0.0 : x;
+            const double negative = alpha * (exp(masked) - one);
+            r = positive ? x : negative;
+            if (code == ACT_SELU) r = 1.0507009873554805 * r;
+            break;
+        }
+        case ACT_SIGMOID: r = half * (tanh(half * x) + one); break;
+        case ACT_SILU: r = x * (half * (tanh(half * x) + one)); break;
+        case ACT_TANH: r = tanh(x); break;
+        case ACT_GELU: r = (half * x) * (one + tanh((0.7978845608028654 * x) * fma(0.044715 * x, x, one))); break;
+        case ACT_GELU_FP16: {
+            if (x > 10.0) {
+                r = x;
+            } else if (x < -10.0) {
+                r = 0.0;
+            } else {
+                const double h = half_round(x);
+                r = half_round((half * h) * (one + tanh((0.7978845608028654 * h) * fma(0.044715 * h, h, one))));
+            }
+            break;
+        }
+        case ACT_SCALE: r = factor * x; break;
+        default: return 0;
+    }
+    *out = r;
+    return 1;
+}
+
+static double act_apply(int code, double factor, double x) {
+    double r = NAN;
+    orc_activation(code, factor, x, &r);
+    return r;
+}
 
 static double row_dot_f64(int format, const uint8_t* row_bytes, int64_t cols, const double* x) {
     const int bv = orc_block_values(format), bb = orc_block_bytes(format);
@@ -339,27 +434,34 @@ static int64_t row_bytes_of(int format, int64_t cols) {
     return cols / orc_block_values(format) * orc_block_bytes(format);
 }
 
-/* One SiLU-GLU expert (recipe.rs:23386-23401 lower_experts + lower_gated):
- * out += weight * down(silu(gate x) * up x). */
+/* One gated expert (recipe.rs:23386-23401 lower_experts + lower_gated,
+ * 23279-23286): out += weight * down(act(gate x) * up x). */
 static void expert_add(int format, int d, int hidden, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
-                       const double* x, double weight, double* h, double* out) {
+                       int activation, double factor, const double* x, double weight, double* h, double* out) {
     const int64_t in_row = row_bytes_of(format, d), out_row = row_bytes_of(format, hidden);
     for (int f = 0; f < hidden; ++f) {
         double g = row_dot_f64(format, gate + f * in_row, d, x);
         double u = row_dot_f64(format, up + f * in_row, d, x);
-        h[f] = act_silu(g) * u;
+        h[f] = act_apply(activation, factor, g) * u;
     }
     for (int n = 0; n < d; ++n) out[n] += weight * row_dot_f64(format, down + n * out_row, hidden, h);
 }
 
 /* lower_gguf_moe (recipe.rs:23415-23459): router contraction over f16 weights,
- * TopK, routed scale, the routed experts in ascending id, then the sigmoid-gated
- * shared expert added. */
+ * TopK (with the selection bias when given), routed scale, the routed experts
+ * in ascending id, then the shared expert added: weighted by its gate's
+ * activation of a [d] f16 vector when gated (SharedExpert::Gated), by one
+ * when not (SharedExpert::Ungated). */
 int orc_moe_f64(int format, int d_model, int experts, int top, int hidden, int scoring, int renormalize, double scale,
-                const uint16_t* router, const uint8_t* gate_bank, const uint8_t* up_bank, const uint8_t* down_bank,
-                int hidden_shared, const uint16_t* shared_gate_vec, const uint8_t* gate_sh, const uint8_t* up_sh,
-                const uint8_t* down_sh, const double* x, double* y, double* route_weights) {
+                int activation, double activation_factor, const double* selection_bias, const uint16_t* router,
+                const uint8_t* gate_bank, const uint8_t* up_bank, const uint8_t* down_bank, int hidden_shared,
+                const uint16_t* shared_gate_vec, int shared_gate_activation, const uint8_t* gate_sh,
+                const uint8_t* up_sh, const uint8_t* down_sh, const double* x, double* y, double* route_weights) {
     if (!shape_ok(format, 1, d_model) || !shape_ok(format, 1, hidden)) return -1;
+    double probe;
+    if (!orc_activation(activation, activation_factor, 0.5, &probe) ||
+        !orc_activation(shared_gate_activation, activation_factor, 0.5, &probe))
+        return -2;
     double* scores = (double*)malloc(sizeof(double) * (size_t)experts);
     double* weights = (double*)malloc(sizeof(double) * (size_t)experts);
     int hmax = hidden > hidden_shared ? hidden : hidden_shared;
@@ -369,7 +471,7 @@ int orc_moe_f64(int format, int d_model, int experts, int top, int hidden, int s
         for (int k = 0; k < d_model; ++k) s += (double)orc_f32_from_fp16(router[(int64_t)e * d_model + k]) * x[k];
         scores[e] = s;
     }
-    int rc = orc_topk(scores, experts, top, scoring, renormalize, weights);
+    int rc = orc_topk_biased(scores, experts, top, scoring, renormalize, selection_bias, weights);
     if (rc == 0) {
         for (int n = 0; n < d_model; ++n) y[n] = 0.0;
         const int64_t bank_in = (int64_t)hidden * row_bytes_of(format, d_model);
@@ -378,15 +480,20 @@ int orc_moe_f64(int format, int d_model, int experts, int top, int hidden, int s
             weights[e] *= scale;
             if (weights[e] == 0.0) continue;
             expert_add(format, d_model, hidden, gate_bank + e * bank_in, up_bank + e * bank_in,
-                       down_bank + e * bank_out, x, weights[e], h, y);
+                       down_bank + e * bank_out, activation, activation_factor, x, weights[e], h, y);
         }
         if (route_weights)
             for (int e = 0; e < experts; ++e) route_weights[e] = weights[e];
-        if (shared_gate_vec && gate_sh && up_sh && down_sh && hidden_shared > 0) {
-            double g = 0.0;
-            for (int k = 0; k < d_model; ++k) g += (double)orc_f32_from_fp16(shared_gate_vec[k]) * x[k];
+        if (gate_sh && up_sh && down_sh && hidden_shared > 0) {
+            double weight = 1.0;
+            if (shared_gate_vec) {
+                double g = 0.0;
+                for (int k = 0; k < d_model; ++k) g += (double)orc_f32_from_fp16(shared_gate_vec[k]) * x[k];
+                weight = act_apply(shared_gate_activation, activation_factor, g);
+            }
             double* shared = (double*)calloc((size_t)d_model, sizeof(double));
-            expert_add(format, d_model, hidden_shared, gate_sh, up_sh, down_sh, x, act_sigmoid(g), h, shared);
+            expert_add(format, d_model, hidden_shared, gate_sh, up_sh, down_sh, activation, activation_factor, x,
+                       weight, h, shared);
             for (int n = 0; n < d_model; ++n) y[n] = y[n] + shared[n];
             free(shared);
         }

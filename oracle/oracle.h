@@ -62,18 +62,30 @@ int orc_matvec_recipe_f32(int format, const uint8_t* bytes, int64_t rows, int64_
                           int64_t ldx, float* y, int64_t ldy, int threads);
 
 /* Top-k routing of one position (amd-nv-cpu.ll:4653-4716): dense weights[E],
- * zero off the kept set. scoring 0 = softmax, 1 = sigmoid. */
+ * zero off the kept set. scoring 0 = softmax, 1 = sigmoid. orc_topk_biased
+ * chooses by probability + bias[e] (bias may be NULL: the raw score). */
 int orc_topk(const double* scores, int experts, int top, int scoring, int renormalize, double* weights);
+int orc_topk_biased(const double* scores, int experts, int top, int scoring, int renormalize, const double* bias,
+                    double* weights);
+
+/* recipe's activation `code` (Activation::code, recipe.rs:13925-13950; 32 =
+ * Gelu under the gelu table) applied to x in f64 (activation_program,
+ * recipe.rs:22579-22727); factor = Scale's constant / PReLU's slope. Returns 0
+ * for an unknown code. */
+int orc_activation(int code, double factor, double x, double* out);
 
 /* The gguf_moe block at one position in f64 (recipe.rs:23386-23459):
  * router [experts x d] f16, banks [experts x hidden x d] (gate, up) and
- * [experts x d x hidden] (down) in `format`; shared expert (hidden_shared
- * wide) with a sigmoid gate of a [d] f16 vector; SiLU-GLU. Any shared
- * pointer NULL disables the shared expert. */
+ * [experts x d x hidden] (down) in `format`, gated by `activation`
+ * (act(gate x) * up x); an optional selection bias (experts values); a shared
+ * expert (hidden_shared wide) weighted by shared_gate_activation of a [d] f16
+ * vector, or by one when that vector is NULL. Any of gate_sh/up_sh/down_sh
+ * NULL disables the shared expert. Returns -2 for an unknown activation. */
 int orc_moe_f64(int format, int d_model, int experts, int top, int hidden, int scoring, int renormalize, double scale,
-                const uint16_t* router, const uint8_t* gate_bank, const uint8_t* up_bank, const uint8_t* down_bank,
-                int hidden_shared, const uint16_t* shared_gate_vec, const uint8_t* gate_sh, const uint8_t* up_sh,
-                const uint8_t* down_sh, const double* x, double* y, double* route_weights);
+                int activation, double activation_factor, const double* selection_bias, const uint16_t* router,
+                const uint8_t* gate_bank, const uint8_t* up_bank, const uint8_t* down_bank, int hidden_shared,
+                const uint16_t* shared_gate_vec, int shared_gate_activation, const uint8_t* gate_sh,
+                const uint8_t* up_sh, const uint8_t* down_sh, const double* x, double* y, double* route_weights);
 
 /* evidence/2026-10-10-m60-p2p/bench.rs:193-226: Q4_K rows (cols multiple of
  * 256) against x quantized to Q8_1-style records, int dots, f64 block scales.

@@ -163,7 +163,11 @@ bool read_shard(const std::string& path, uint64_t index, Shard* s, std::string* 
             if ((uint64_t)elements % be)
                 throw Fail{"tensor " + t.name + " holds " + std::to_string((uint64_t)elements) +
                            " elements, not a multiple of its " + std::to_string(be) + "-element block"};
-            t.bytes = (uint64_t)elements / be * bb;
+            // the byte count in 128 bits: a shape whose bytes do not fit in 63 bits is refused
+            // before any size derived from it can wrap
+            const unsigned __int128 nbytes = elements / be * bb;
+            if (nbytes >> 63) throw Fail{"tensor " + t.name + " shape overflows"};
+            t.bytes = (uint64_t)nbytes;
             t.shard = (int)index;
             s->tensors.push_back(std::move(t));
         }

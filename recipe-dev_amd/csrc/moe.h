@@ -16,8 +16,12 @@ struct MoeBank {
 struct MoeDims {
     int d_model, experts, top, hidden, hidden_shared;  // hidden_shared = 0: no shared expert
     int scoring, renormalize;
-    int shared_gated;  // 1: the shared expert is weighted by sigmoid(gate . x); 0: by one
+    int shared_gated;  // 1: the shared expert is weighted by shared_gate_act(gate . x); 0: by one
     float scale;
+    int activation;       // act(gate x) * up x of every expert (act.h codes)
+    int shared_gate_act;  // the shared gate's activation
+    float act_factor;     // Scale's constant / PReLU's slope
+    const float* sel_bias = nullptr;  // experts fp32: the top-k selection key is probability + bias
 };
 
 // Workspace carve-up (floats unless noted), all in one device buffer.
@@ -41,8 +45,8 @@ struct MoeBatch {
 };
 
 // Routes the position (ws.ids, ws.weights and route_dense when not null,
-// topk_forward_wave_body semantics, amd-nv-cpu.ll:4489-4652) and computes
-// h[slot][f] = silu(gate_slot[f] . x) * (up_slot[f] . x) for every routed slot
+// topk_forward_body semantics, amd-nv-cpu.ll:4653-4716) and computes
+// h[slot][f] = act(gate_slot[f] . x) * (up_slot[f] . x) for every routed slot
 // and the shared expert.
 hipError_t launch_moe_glu(int fmt, int xtype, const MoeDims& d, const MoeBank& gate, const MoeBank& up,
                           const MoeBank& gate_sh, const MoeBank& up_sh, const void* x, MoeWorkspace ws,

@@ -9,15 +9,16 @@
 //
 // Here the router and the shared expert's gate run as one F16 matvec, then:
 //   moe_glu   every wave first routes the position (a radix select of the k
-//             best scores, the lower expert on a tie; the routing weights;
-//             slots in ascending expert id), then one lane group per (slot,
-//             hidden row) reads the gate and up rows of the
-//             slot's expert are read together against x staged in LDS, and
-//             silu(gate) * up is written per slot (routed slots, then shared);
+//             best selection keys, the lower expert on a tie; the routing
+//             weights; slots in ascending expert id), then one lane group per
+//             (slot, hidden row) reads the gate and up rows of the slot's
+//             expert together against x staged in LDS, and act(gate) * up is
+//             written per slot (routed slots, then shared);
 //   moe_down  one lane group per output row: its lanes walk the chunks of every
 //             slot's down row (K = all slots' hidden widths back to back, h staged
 //             in LDS), scale each chunk by its slot's weight, and reduce across
 //             lanes; no atomics, no second pass.
+#include "act.h"
 #include "moe.h"
 #include "stage.h"
 
@@ -55,6 +56,7 @@ MoeWorkspace moe_workspace(void* base, const MoeDims& d) {
     return w;
 }
 
+// @sigmoid of the router's scoring (amd-nv-cpu.ll:5007-5009): 1 / (1 + exp(-v)).
 __device__ __forceinline__ float sigmoidf_dev(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // The workspace of position p of a batch.
@@ -105,15 +107,19 @@ __device__ __forceinline__ float wave_sum_fixed(float v) {
 }
 
 // Top-k routing (topk_forward_body semantics, amd-nv-cpu.ll:4486-4716) on one
-// wave. The router scores sit in registers (expert lane + 64 j in v[j]) as
-// order-preserving 32-bit keys; a radix select over the 32 key bits (one
-// ballot and population count per register per bit) finds the k-th largest
-// key T; the experts above T are kept, and of those equal to T the lowest ids,
-// so a tie goes to the lower expert. Slots are the kept experts in ascending
-// id, counted from the ballots. The picked ids go to the wave's `slot_ids`
-// (LDS); with `publish` the wave also writes the routing (ids, weights, the
-// shared expert's weight, the dense routing plane) to the workspace. Sums run
-// in a fixed order, so the weights are deterministic.
+// wave. The selection keys sit in registers (expert lane + 64 j in key[j]) as
+// order-preserving 32-bit patterns: the router score itself, or with a
+// selection bias (topk_key, amd-nv-cpu.ll:4653-4660) the expert's probability
+// (its sigmoid, or exp(score - max) / total over every expert) plus its bias,
+// formed in fp32. A radix select over the 32 key bits (one ballot and
+// population count per register per bit) finds the k-th largest key T; the
+// experts above T are kept, and of those equal to T the lowest ids, so a tie
+// goes to the lower expert. Slots are the kept experts in ascending id,
+// counted from the ballots. The weights come from the unbiased scores. The
+// picked ids go to the wave's `slot_ids` (LDS); with `publish` the wave also
+// writes the routing (ids, weights, the shared expert's weight, the dense
+// routing plane) to the workspace. Sums run in a fixed order, so the weights
+// are deterministic.
 constexpr int kTopkMaxExperts = 2048;
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -134,13 +140,37 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
     const bool sigmoid = d.scoring != 0, renorm = d.renormalize != 0;
     float v[S];
     uint32_t key[S];
+    float bias[S];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int e = lane + 64 * j;
         v[j] = ws.logits[e < E ? e : E - 1];
+        bias[j] = d.sel_bias ? d.sel_bias[e < E ? e : E - 1] : 0.f;
         key[j] = e < E ? order_key(v[j]) : 0u;  // an absent expert ranks below every score
     }
     const float shared_logit = ws.logits[E];  // read early; used only with a gated shared expert
+    if (d.sel_bias) {
+        // probability over every expert, plus the bias
+        float am = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+            if (lane + 64 * j < E) am = fmaxf(am, v[j]);
+        {
+            int ii = 0;
+            wave_argmax(am, ii);
+        }
+        float at = 0.f;
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+            if (lane + 64 * j < E) at += sigmoid ? sigmoidf_dev(v[j]) : expf(v[j] - am);
+        const float all_total = wave_sum_fixed(at);
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const float raw = sigmoid ? sigmoidf_dev(v[j]) : expf(v[j] - am);
+            const float prob = sigmoid ? raw : raw / all_total;
+            key[j] = lane + 64 * j < E ? order_key(prob + bias[j]) : 0u;
+        }
+    }
     // T = the largest key with at least k keys >= T
     uint32_t T = 0;
     for (int bit = 31; bit >= 0; --bit) {
@@ -201,10 +231,10 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
             }
             if (route_dense) route_dense[e] = kept[j] ? w : 0.f;
         }
-        // The shared expert's weight: its gate's Sigmoid activation, 0.5 (tanh(v/2) + 1)
-        // (recipe.rs:22662-22668), or 1 when it has no gate.
+        // The shared expert's weight: its gate's activation (SharedExpert::Gated,
+        // recipe.rs:23440-23452), or 1 when it has no gate.
         if (lane == 0 && d.hidden_shared > 0)
-            ws.weights[k] = d.shared_gated ? 0.5f * (tanhf(0.5f * shared_logit) + 1.0f) : 1.0f;
+            ws.weights[k] = d.shared_gated ? act_apply(d.shared_gate_act, d.act_factor, shared_logit) : 1.0f;
     }
 }
 
@@ -281,7 +311,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
             }
             ag = group_sum(ag, G);
             au = group_sum(au, G);
-            if (r < total_rows && g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
+            if (r < total_rows && g == G - 1) ws.h[r] = act_apply(d.activation, d.act_factor, ag) * au;
         }
         return;
     }
@@ -304,7 +334,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
         }
         ag = group_sum(ag, G);
         au = group_sum(au, G);
-        if (r < total_rows && g == G - 1) ws.h[r] = ag * sigmoidf_dev(ag) * au;
+        if (r < total_rows && g == G - 1) ws.h[r] = act_apply(d.activation, d.act_factor, ag) * au;
     };
     while (tile < tiles) {
         step(tile, dg0, du0, dg1, du1);

@@ -54,9 +54,14 @@ static uint32_t q6_high_word(const uint8_t* q6) {
     return w;
 }
 
+// Shapes the kernels take: rows below 2^31 (their row indices are 32-bit)
+// and cols at most 2^30, a whole number of blocks; both products below are
+// then checked for overflow, so that a shape read from an untrusted file
+// cannot wrap a size.
 static bool shape_ok(int fmt, int64_t rows, int64_t cols) {
     FormatInfo f = format_info(fmt);
     if (f.block_values == 0 || rows <= 0 || cols <= 0) return false;
+    if (rows > kMaxRows || cols > kMaxCols) return false;
     if (cols % f.block_values != 0) return false;
     if (cols % 32 != 0) return false;
     if (fmt == F16 && cols % 64 != 0) return false;
@@ -66,12 +71,16 @@ static bool shape_ok(int fmt, int64_t rows, int64_t cols) {
 int64_t gguf_bytes(int fmt, int64_t rows, int64_t cols) {
     FormatInfo f = format_info(fmt);
     if (!shape_ok(fmt, rows, cols)) return -1;
-    return rows * (cols / f.block_values) * f.block_bytes;
+    int64_t n;
+    if (__builtin_mul_overflow(rows, (cols / f.block_values) * f.block_bytes, &n)) return -1;
+    return n;
 }
 
 int64_t layout_bytes(int fmt, int64_t rows, int64_t cols) {
     if (!shape_ok(fmt, rows, cols)) return -1;
-    return rows * row_bytes(fmt, cols);
+    int64_t n;
+    if (__builtin_mul_overflow(rows, row_bytes(fmt, cols), &n)) return -1;
+    return n;
 }
 
 // Copies one chunk between its GGUF blocks (a row's block bytes) and the
@@ -201,7 +210,7 @@ static void chunk_copy(int fmt, const uint8_t* src_blocks, uint8_t* dst_blocks, 
 }
 
 int repack(int fmt, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* dst) {
-    if (!shape_ok(fmt, rows, cols)) return -1;
+    if (layout_bytes(fmt, rows, cols) < 0 || gguf_bytes(fmt, rows, cols) < 0) return -1;
     const FormatInfo f = format_info(fmt);
     const int64_t rb = row_bytes(fmt, cols);
     const int64_t nch = chunks_per_row(fmt, cols);
@@ -215,7 +224,7 @@ int repack(int fmt, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* dst
 }
 
 int unpack(int fmt, int64_t rows, int64_t cols, const uint8_t* src, uint8_t* dst) {
-    if (!shape_ok(fmt, rows, cols)) return -1;
+    if (layout_bytes(fmt, rows, cols) < 0 || gguf_bytes(fmt, rows, cols) < 0) return -1;
     const FormatInfo f = format_info(fmt);
     const int64_t rb = row_bytes(fmt, cols);
     const int64_t nch = chunks_per_row(fmt, cols);

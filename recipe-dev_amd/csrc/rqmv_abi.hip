@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "../../include/rqmv.h"
+#include "act.h"
 #include "kernels.h"
 #include "decode.h"
 #include "gguf.h"
@@ -86,12 +87,14 @@ int create(int format, int64_t experts, int64_t rows, int64_t cols, const void* 
     *out = nullptr;
     if (!rq::format_supported(format) || format == rq::F32) return fail(RQMV_EINVAL, "unsupported format " + std::to_string(format));
     if (experts <= 0 || rows <= 0 || cols <= 0) return fail(RQMV_EINVAL, "shape must be positive");
-    if (cols > (1 << 30)) return fail(RQMV_EINVAL, "cols too large");
-    const int64_t total_rows = experts * rows;
+    if (cols > rq::kMaxCols) return fail(RQMV_EINVAL, "cols too large");
+    int64_t total_rows;
+    if (__builtin_mul_overflow(experts, rows, &total_rows) || total_rows > rq::kMaxRows)
+        return fail(RQMV_EINVAL, "experts x rows must stay below 2^31 rows");
     const int64_t want = rq::gguf_bytes(format, total_rows, cols);
     if (want < 0)
         return fail(RQMV_EINVAL, "cols is not a whole number of blocks for this format (a multiple of 32, and of "
-                                 "256 for Q4_K/Q6_K and 64 for F16)");
+                                 "256 for Q4_K/Q6_K and 64 for F16), or the shape's size overflows");
     if (!bytes || (size_t)want != nbytes)
         return fail(RQMV_EINVAL, "expected " + std::to_string(want) + " GGUF bytes, got " + std::to_string(nbytes));
     DeviceInfo info;
@@ -299,7 +302,9 @@ int rqmv_weight_create_int8(int format, int64_t experts, int64_t rows, int64_t c
     *out = nullptr;
     if (format == rq::Q4_K || format == rq::Q8_0) return create(format, experts, rows, cols, gguf_bytes, nbytes, out);
     if (experts <= 0 || rows <= 0) return fail(RQMV_EINVAL, "shape must be positive");
-    const int64_t total = experts * rows;
+    int64_t total;
+    if (__builtin_mul_overflow(experts, rows, &total) || total > rq::kMaxRows)
+        return fail(RQMV_EINVAL, "experts x rows must stay below 2^31 rows");
     std::vector<uint8_t> q8;
     const int64_t q8_bytes = rq::gguf_bytes(rq::Q8_0, total, cols);
     if (q8_bytes < 0) return fail(RQMV_EINVAL, "cols is not a whole number of Q8_0 blocks");
@@ -316,6 +321,7 @@ int rqmv_glu_weight_create(int format, int64_t rows, int64_t cols, const void* g
     const int64_t want = rq::gguf_bytes(format, rows, cols);
     if (rows <= 0 || want < 0 || (size_t)want != nbytes_each)
         return fail(RQMV_EINVAL, "gate and up must each hold rows x cols GGUF blocks");
+    if (rows > rq::kMaxRows / 2) return fail(RQMV_EINVAL, "2 x rows must stay below 2^31 rows");
     // rows interleaved: row 2i = gate row i, row 2i + 1 = up row i
     const size_t rb = (size_t)want / (size_t)rows;
     std::vector<uint8_t> pairs(2 * (size_t)want);
@@ -473,6 +479,11 @@ int moe_dims(const rqmv_moe_params* p, rq::MoeDims* d, const DeviceInfo& info) {
     if (p->top_k < 1 || p->top_k > 64 || p->top_k > E) return fail(RQMV_EINVAL, "top_k must be in 1..min(64, experts)");
     if (E > 2048) return fail(RQMV_EINVAL, "at most 2048 experts");
     if (p->scoring != RQMV_SCORE_SOFTMAX && p->scoring != RQMV_SCORE_SIGMOID) return fail(RQMV_EINVAL, "bad scoring");
+    if (!rq::act_known(p->activation) || !rq::act_known(p->shared_gate_activation))
+        return fail(RQMV_EINVAL, "unknown activation code (rqmv_activation)");
+    if (!(p->scale == p->scale) || p->scale - p->scale != 0.f) return fail(RQMV_EINVAL, "moe routed scale must be finite");
+    if (reinterpret_cast<uintptr_t>(p->selection_bias) % 4 != 0)
+        return fail(RQMV_EINVAL, "selection_bias must be 4-byte aligned");
     int64_t HS = 0;
     const bool any_shared = p->gate_shexp || p->up_shexp || p->down_shexp;
     if (any_shared) {
@@ -501,6 +512,10 @@ int moe_dims(const rqmv_moe_params* p, rq::MoeDims* d, const DeviceInfo& info) {
     d->renormalize = p->renormalize ? 1 : 0;
     d->shared_gated = p->shared_gate_inp ? 1 : 0;
     d->scale = p->scale;
+    d->activation = p->activation;
+    d->shared_gate_act = p->shared_gate_activation;
+    d->act_factor = p->activation_factor;
+    d->sel_bias = p->selection_bias;
     return RQMV_OK;
 }
 

@@ -183,15 +183,30 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
             v[2 * e + 1] = half_hi(word(it.raw[0], e));
         }
     }
+    // A NaN or an infinity anywhere in the block makes the block's scale NaN
+    // (its digits are zero), so every product that reads the block is NaN:
+    // a non-finite activation is never dropped by the maximum or the rounding.
     float amax = 0.f;
+    int bad = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    for (int k = 0; k < 8; ++k) {
+        amax = fmaxf(amax, fabsf(v[k]));
+        bad |= !(fabsf(v[k]) <= 3.402823466e38f);
+    }
     amax = fmaxf(amax, dpp_quad_f32<0xB1>(amax));  // quad_perm [1,0,3,2]
     amax = fmaxf(amax, dpp_quad_f32<0x4E>(amax));  // quad_perm [2,3,0,1]
+    bad |= dpp_i32<0xB1>(bad);
+    bad |= dpp_i32<0x4E>(bad);
     if (!live) amax = 0.f;
+    if (bad) {
+        amax = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = 0.f;
+    }
     uint32_t w4[4];
     int sum;
-    const float s = encode_item<FMT>(v, amax, w4, sum);
+    float s = encode_item<FMT>(v, amax, w4, sum);
+    if (bad && live) s = __builtin_nanf("");
     uint32_t* xdw = reinterpret_cast<uint32_t*>(xd);
     if constexpr (FMT == Q8_0) {
         // low-byte words 2q, 2q+1 in parts 0-1, high-byte words in parts 2-3

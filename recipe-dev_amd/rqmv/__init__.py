@@ -462,19 +462,40 @@ class MoeParams(ctypes.Structure):
     _fields_ = [("router", c_void_p), ("gate_exps", c_void_p), ("up_exps", c_void_p), ("down_exps", c_void_p),
                 ("shared_gate_inp", c_void_p), ("gate_shexp", c_void_p), ("up_shexp", c_void_p),
                 ("down_shexp", c_void_p), ("top_k", c_int), ("scoring", c_int), ("renormalize", c_int),
-                ("scale", c_float)]
+                ("scale", c_float), ("activation", c_int), ("shared_gate_activation", c_int),
+                ("activation_factor", c_float), ("selection_bias", c_void_p)]
+
+
+# recipe's Activation::code() values (recipe.rs:13925-13950), as rqmv_activation
+# names them; "gelu_fp16" is Gelu under the llama.cpp profile's gelu table.
+ACTIVATIONS = {"linear": 0, "cos": 1, "exp": 2, "log": 3, "ln": 4, "huber": 5, "tan": 6, "relu": 7, "leak": 8,
+               "sigmoid": 9, "tanh": 10, "selu": 11, "gelu": 12, "silu": 13, "elu": 14, "prelu": 15, "scale": 16,
+               "sqrt": 17, "softplus": 18, "gelu_fp16": 32}
+
+
+def _act(a) -> int:
+    return ACTIVATIONS[a] if isinstance(a, str) else int(a)
 
 
 class Moe:
-    """A gguf_moe block's weights and workspace on the device."""
+    """A gguf_moe block's weights and workspace on the device: gguf_moe(experts,
+    top_k, hidden, activation, scoring, renormalize, shared, scale,
+    selection_bias) (recipe.rs:14722). The shared expert is absent (no shared
+    weights), ungated (shared weights without shared_gate_inp: weight one) or
+    gated by shared_gate_activation(shared_gate_inp . x). selection_bias is a
+    device buffer of `experts` fp32 values (exp_probs_b.bias) or None."""
 
     def __init__(self, router: Weight, gate: Weight, up: Weight, down: Weight, top_k: int, scoring: int = SCORE_SOFTMAX,
                  renormalize: bool = True, scale: float = 1.0, shared_gate_inp: Weight | None = None,
-                 gate_sh: Weight | None = None, up_sh: Weight | None = None, down_sh: Weight | None = None):
+                 gate_sh: Weight | None = None, up_sh: Weight | None = None, down_sh: Weight | None = None,
+                 activation="silu", shared_gate_activation="sigmoid", activation_factor: float = 0.0,
+                 selection_bias: "DeviceBuffer | None" = None):
         h = lambda w: w.handle if w is not None else None  # noqa: E731
         self.params = MoeParams(h(router), h(gate), h(up), h(down), h(shared_gate_inp), h(gate_sh), h(up_sh),
-                                h(down_sh), top_k, scoring, 1 if renormalize else 0, scale)
-        self.keep = (router, gate, up, down, shared_gate_inp, gate_sh, up_sh, down_sh)
+                                h(down_sh), top_k, scoring, 1 if renormalize else 0, scale, _act(activation),
+                                _act(shared_gate_activation), activation_factor,
+                                selection_bias.ptr if selection_bias is not None else None)
+        self.keep = (router, gate, up, down, shared_gate_inp, gate_sh, up_sh, down_sh, selection_bias)
         self.d_model = router.cols
         self.experts = router.rows
         n = c_size_t()

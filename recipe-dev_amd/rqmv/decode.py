@@ -140,6 +140,7 @@ class DecodeModel:
         self.workspace = attention_workspace(s.q_heads, s.kv_heads, s.head_dim, self.max_ctx)
         self.argmax_ws = argmax_workspace()
         self.rope = rope_table(s.head_dim, s.rope_base, self.max_ctx)
+        self._pos: int | None = None  # host count of the position (set_position, step, replay)
 
     # ---------------------------------------------------------------- setup
     def set_layer(self, index: int, t: LayerTensors):
@@ -174,8 +175,46 @@ class DecodeModel:
             buf.upload(full)
 
     def set_position(self, token: int, pos: int):
+        """The next step decodes `token` at `pos`; pos must lie inside the
+        cache (recipe refuses a step whose token window is outside the
+        placement's capacity, recipe.rs:21330-21331)."""
+        if not 0 <= pos < self.max_ctx:
+            raise ValueError(f"position {pos} is outside the cache (0..{self.max_ctx - 1}): the token window is "
+                             "outside the placement capacity")
         self.token.upload(np.array([token], dtype=np.int32))
         self.pos.upload(np.array([pos], dtype=np.int32))
+        self._pos = pos
+
+    def _room(self, steps: int):
+        """Raises unless `steps` more steps stay inside the cache (host count
+        of the steps run through step() and replay())."""
+        if self._pos is None:
+            raise RuntimeError("set_position must come before the first step")
+        if self._pos + steps > self.max_ctx:
+            raise ValueError(f"{steps} step(s) from position {self._pos} run past the cache's {self.max_ctx} "
+                             "positions: the token window is outside the placement capacity")
+
+    def step(self, stream: Stream | None = None):
+        """One eager step at the current position; raises before a step past the cache."""
+        self._room(1)
+        self.enqueue_step(stream)
+        self._pos += 1
+
+    def replay(self, graph: Graph, stream: Stream, times: int = 1):
+        """`times` replays of a captured step; raises before any would run past the cache."""
+        self._room(times)
+        for _ in range(times):
+            graph.launch(stream)
+        self._pos += times
+
+    def _check_inside(self):
+        """The device position after a step is at most max_ctx; beyond it a
+        step ran past the cache (a graph launched directly, past the end), and
+        its results are refused."""
+        p = self.read_position()
+        if p > self.max_ctx:
+            raise RuntimeError(f"a step ran at position {p - 1}, outside the cache (0..{self.max_ctx - 1}): the "
+                               "token window is outside the placement capacity")
 
     # ----------------------------------------------------------------- step
     def enqueue_step(self, stream: Stream | None = None):
@@ -214,9 +253,11 @@ class DecodeModel:
         return Graph(stream, lambda: self.enqueue_step(stream))
 
     def read_logits(self) -> np.ndarray:
+        self._check_inside()
         return self.logits.download(np.float32, self.shape.vocab)
 
     def read_token(self) -> int:
+        self._check_inside()
         return int(self.token.download(np.int32, 1)[0])
 
     def read_position(self) -> int:

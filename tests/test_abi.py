@@ -145,6 +145,30 @@ def test_bad_shapes_are_rejected(fmt, rows, cols):
         rqmv.layout_bytes(fmt, rows, cols)
 
 
+@pytest.mark.parametrize("fmt,rows,cols", [("f16", 2 ** 31, 64), ("q4_k", 1, 2 ** 30 + 256), ("q8_0", -5, 32),
+                                           ("q6_k", 2 ** 62, 2 ** 30)])
+def test_shapes_past_the_kernels_limits_are_rejected(fmt, rows, cols):
+    """Row indices are 32-bit in the kernels and sizes are checked for
+    overflow, so an oversized shape is an error, never a wrapped size."""
+    with pytest.raises(rqmv.RqmvError):
+        rqmv.layout_bytes(fmt, rows, cols)
+    out = np.zeros(16, np.uint8)
+    assert rqmv.lib().lib.rqmv_repack_host(rqmv._fmt(fmt), rows, cols,
+                                           out.ctypes.data, out.ctypes.data) == -1
+
+
+def test_weight_create_refuses_overflowing_shapes_before_any_copy():
+    """experts x rows that wraps in 64 bits, or a bank past 2^31 rows, is
+    refused from the shape alone (the byte buffer is never read)."""
+    L = rqmv.lib().lib
+    h = ctypes.c_void_p()
+    data = np.zeros(128, np.uint8)
+    for experts, rows in ((2 ** 40, 2 ** 40), (2 ** 20, 2 ** 12), (1, 2 ** 31)):
+        rc = L.rqmv_expert_bank_create(1, experts, rows, 64, data.ctypes.data, 128, ctypes.byref(h))
+        assert rc == -1 and h.value is None
+        assert b"2^31" in L.rqmv_last_error() or b"overflow" in L.rqmv_last_error()
+
+
 def test_last_error_names_the_failure():
     L = rqmv.lib().lib
     rc = L.rqmv_layout_bytes(12, 4, 100, None, None, None)

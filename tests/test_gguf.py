@@ -172,3 +172,13 @@ def test_synthetic_blocks_through_the_file(tmp_path):
     gw.write(path, [], [("blk.0.ffn_up.weight", [512, 16], 12, w.tobytes())])
     g = rqmv.Gguf(path)
     assert np.array_equal(g.data("blk.0.ffn_up.weight"), w)
+
+
+def test_shape_whose_byte_count_wraps_is_refused(tmp_path):
+    """An F16 tensor [64, 2^57 + 1] holds 2^63 + 64 elements: its byte count,
+    2^64 + 128, would wrap to 128 in 64-bit arithmetic and match a 128-byte
+    data section. The reader counts in 128 bits and refuses the shape."""
+    path = str(tmp_path / "wrap.gguf")
+    gw.write(path, [], [("wrap", [64, 2 ** 57 + 1], 1, bytes(128))])
+    with pytest.raises(rqmv.RqmvError, match="overflows"):
+        rqmv.Gguf(path)

@@ -206,6 +206,45 @@ def test_decode_steps_match_reference(gpu, proj_fmt, head_fmt):
     stream.close()
 
 
+def test_decode_refuses_steps_past_the_cache(gpu):
+    """recipe refuses a step whose token window lies outside the placement's
+    capacity (recipe.rs:21330-21331): set_position checks the position, step()
+    and replay() count steps on the host and raise before one would run past
+    the cache, and the results of a graph launched directly past the end are
+    refused when read. (A step past the end reads and writes only inside the
+    cache: the kernels clamp the position.)"""
+    shape = DecoderShape(layers=1, d=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=256)
+    ctx, max_ctx = 4, 6
+    model, _ = _small_decoder(gpu, shape, ctx, max_ctx, seed=2)
+    for bad in (max_ctx, max_ctx + 5, -1):
+        with pytest.raises(ValueError):
+            model.set_position(1, bad)
+    stream = gpu.Stream()
+    with pytest.raises(RuntimeError):
+        model.step(stream)  # no position yet
+    model.set_position(1, ctx)  # positions 4 and 5 fit
+    model.step(stream)
+    graph = model.capture(stream)
+    with pytest.raises(ValueError):
+        model.replay(graph, stream, 2)
+    model.replay(graph, stream)  # position 5, the cache's last
+    stream.synchronize()
+    assert np.isfinite(model.read_logits()).all()
+    with pytest.raises(ValueError):
+        model.step(stream)
+    with pytest.raises(ValueError):
+        model.replay(graph, stream)
+    assert model.read_position() == max_ctx
+    graph.launch(stream)  # bypasses the host count
+    stream.synchronize()
+    with pytest.raises(RuntimeError):
+        model.read_logits()
+    with pytest.raises(RuntimeError):
+        model.read_token()
+    graph.close()
+    stream.close()
+
+
 def test_decode_real_head_shapes(gpu):
     """One step at the full decoder's attention and projection widths (two
     layers, smaller vocab), against the f64 reference."""

@@ -122,6 +122,31 @@ def test_matvec_parity(gpu, fmt, xdt, m):
         assert err <= limit, (fmt, xdt, m, rows, cols, err)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("m", [1, 2, 3, 16])
+def test_non_finite_activations_propagate(gpu, fmt, xdt, m):
+    """A NaN or an infinity in an activation row makes every output of that
+    row non-finite (the integer kernels give the row's blocks a NaN scale; the
+    matrix cores carry them through the products); the other rows keep their
+    values."""
+    rows, cols = 70, 512
+    w = _weights(fmt, rows, cols, seed=90 + m)
+    W = gpu.Weight(fmt, rows, cols, w)
+    for bad in (np.nan, np.inf, -np.inf):
+        xh, dt, x32 = _x(m, cols, xdt, seed=91 + m)
+        xh = np.array(xh, copy=True)
+        if xdt == "f16":
+            xh[0, 37] = np.float16(bad).view(np.uint16)
+        else:
+            xh[0, 37] = bad
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        assert not np.isfinite(y[0]).any(), (bad, int(np.isfinite(y[0]).sum()))
+        if m > 1:
+            ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32[1:], threads=THREADS)
+            assert rel_l2(y[1:], ref) <= 2e-4
+
+
 @pytest.mark.parametrize("xdt", ["f16", "f32"])
 def test_f16_sixteen_row_launches(gpu, xdt):
     """F16 weights (routers over a batch of positions) take sixteen activation
@@ -308,22 +333,87 @@ def test_moe_parity(gpu, fmt, d, E, top, H, HS, gated, scoring, renorm, xdt):
     y, route = moe(xh[0])
     y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
                                    x32[0].astype(np.float64), scoring=scoring, renormalize=renorm, **okw)
-    if shared is not None and not gated:
-        # an ungated shared expert runs at weight one; the oracle's composition takes a gate vector,
-        # so compare against its routed part plus the shared expert computed densely
-        y_r, _ = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
-                                x32[0].astype(np.float64), scoring=scoring, renormalize=renorm)
-        gs_w = oracle.dequant_rows(fmt, shared[1], HS, d).astype(np.float64)
-        us_w = oracle.dequant_rows(fmt, shared[2], HS, d).astype(np.float64)
-        ds_w = oracle.dequant_rows(fmt, shared[3], d, HS).astype(np.float64)
-        xv = x32[0].astype(np.float64)
-        g = gs_w @ xv
-        y_ref = y_r + ds_w @ (g / (1 + np.exp(-g)) * (us_w @ xv))
     assert np.array_equal(route != 0, rw_ref != 0), "routed experts differ"
     assert np.allclose(route, rw_ref, rtol=1e-5, atol=1e-7)
     err = rel_l2(y, y_ref)
     print(f"moe {fmt} d={d} E={E} top={top}: rel-L2 {err:.3e}", flush=True)
     assert err <= REL_L2
+
+
+@pytest.mark.parametrize("act,gate_act,biased,scoring,renorm,fmt,d,E,top,H,HS", [
+    ("silu", "sigmoid", True, 1, True, "q4_k", 2048, 256, 8, 512, 512),   # the decode workload, biased
+    ("gelu", "tanh", True, 0, True, "q4_k", 512, 32, 4, 256, 256),
+    ("gelu_fp16", "sigmoid", False, 1, False, "q6_k", 256, 16, 3, 256, 256),
+    ("relu", "linear", True, 1, False, "q8_0", 256, 24, 5, 128, 64),
+    ("softplus", "silu", False, 0, True, "q4_0", 256, 8, 2, 128, 128),
+    ("selu", "elu", True, 0, False, "q4_k", 256, 64, 6, 256, 256),
+    ("linear", "relu", False, 1, True, "q4_k", 256, 8, 2, 256, 256),
+])
+def test_moe_activation_and_selection_bias(gpu, act, gate_act, biased, scoring, renorm, fmt, d, E, top, H, HS):
+    """gguf_moe's activation (every expert's act(gate x) * up x), the shared
+    gate's activation and the selection bias (probability + bias chooses, the
+    unbiased scores weigh), against the f64 oracle."""
+    router, gate, up, down, shared = _moe_case(fmt, d, E, top, H, HS, True, seed=7 * E + d)
+    xh, dt, x32 = _x(1, d, "f16", seed=d + 3)
+    sg, gs, us, ds = shared
+    rng = np.random.default_rng(E + top)
+    bias = (rng.standard_normal(E) * (0.05 if scoring == 0 else 0.3)).astype(np.float32) if biased else None
+    B = gpu.DeviceBuffer.from_array(bias) if biased else None
+    moe = gpu.Moe(gpu.Weight("f16", E, d, router), gpu.Weight(fmt, H, d, gate, experts=E),
+                  gpu.Weight(fmt, H, d, up, experts=E), gpu.Weight(fmt, d, H, down, experts=E), top, scoring=scoring,
+                  renormalize=renorm, shared_gate_inp=gpu.Weight("f16", 1, d, sg), gate_sh=gpu.Weight(fmt, HS, d, gs),
+                  up_sh=gpu.Weight(fmt, HS, d, us), down_sh=gpu.Weight(fmt, d, HS, ds), activation=act,
+                  shared_gate_activation=gate_act, selection_bias=B)
+    y, route = moe(xh[0])
+    y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
+                                   x32[0].astype(np.float64), scoring=scoring, renormalize=renorm, hidden_shared=HS,
+                                   shared_gate_bits=sg.view(np.uint16), gate_sh=gs, up_sh=us, down_sh=ds,
+                                   activation=act, shared_gate_activation=gate_act,
+                                   selection_bias=None if bias is None else bias.astype(np.float64))
+    assert np.array_equal(route != 0, rw_ref != 0), "routed experts differ"
+    assert np.allclose(route, rw_ref, rtol=1e-5, atol=1e-7)
+    if biased:  # the bias did change the choice somewhere in these cases, or at least is honoured
+        plain = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down, x32[0].astype(np.float64),
+                               scoring=scoring, renormalize=renorm)[1]
+        print(f"bias moved {int(np.sum((plain != 0) != (rw_ref != 0)))} selections", flush=True)
+    err = rel_l2(y, y_ref)
+    print(f"moe {act}/{gate_act} bias={biased} {fmt} d={d} E={E}: rel-L2 {err:.3e}", flush=True)
+    assert err <= REL_L2
+
+
+@pytest.mark.parametrize("scoring,renorm", [(0, True), (1, False), (1, True)])
+def test_moe_router_ties_go_to_the_lower_expert(gpu, scoring, renorm):
+    """Router logits with exact ties: every router row is a power-of-two
+    multiple of one row, so the device's logits are exact multiples of one
+    value. The rows with coefficient 2 tie at the top-k boundary; the lower
+    ids must be kept (topk_forward_body's strict greater-than,
+    amd-nv-cpu.ll:4666-4716). A selection bias that is equal everywhere keeps
+    the same choice."""
+    fmt, d, E, top, H = "q4_k", 256, 16, 3, 256
+    base = synth.f16_weights(1, d, 0.05, seed=31, tag="tie").view(np.uint16)
+    xh, dt, x32 = _x(1, d, "f16", seed=32)
+    L = float(synth.fp16_to_f32(base).astype(np.float64) @ x32[0].astype(np.float64))
+    sign = 1.0 if L > 0 else -1.0
+    coef = np.ones(E)
+    coef[[9, 4, 13, 6]] = 2.0      # four-way tie for the last two slots: ids 4 and 6 win
+    coef[11] = 4.0                 # the clear winner
+    rows = np.stack([synth.fp16_bits(synth.fp16_to_f32(base) * np.float32(sign * c)) for c in coef])
+    assert np.array_equal(synth.fp16_to_f32(rows), np.stack([synth.fp16_to_f32(base) * np.float32(sign * c) for c in coef]))
+    _, gate, up, down, _ = _moe_case(fmt, d, E, top, H, 0, False, seed=33)
+    Wr = gpu.Weight("f16", E, d, rows)
+    banks = (gpu.Weight(fmt, H, d, gate, experts=E), gpu.Weight(fmt, H, d, up, experts=E),
+             gpu.Weight(fmt, d, H, down, experts=E))
+    for bias in (None, np.full(E, 0.25, np.float32)):
+        B = gpu.DeviceBuffer.from_array(bias) if bias is not None else None
+        moe = gpu.Moe(Wr, *banks, top, scoring=scoring, renormalize=renorm, selection_bias=B)
+        y, route = moe(xh[0])
+        assert list(np.nonzero(route)[0]) == [4, 6, 11], np.nonzero(route)[0]
+        y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, rows, gate, up, down, x32[0].astype(np.float64),
+                                       scoring=scoring, renormalize=renorm,
+                                       selection_bias=None if bias is None else bias.astype(np.float64))
+        assert list(np.nonzero(rw_ref)[0]) == [4, 6, 11]
+        assert np.allclose(route, rw_ref, rtol=1e-5, atol=1e-7)
+        assert rel_l2(y, y_ref) <= REL_L2
 
 
 # -------------------------------------------------------- error paths ----

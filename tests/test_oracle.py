@@ -328,6 +328,106 @@ def test_topk_brute_force(scoring, renorm):
         assert np.allclose(got, ref, rtol=1e-13, atol=1e-15)
 
 
+def _topk_biased_brute(scores, top, scoring, renorm, bias):
+    """The selection by probability + bias (probability: the sigmoid, or the
+    softmax over every expert), by a stable sort instead of repeated scans;
+    the weights from the unbiased scores, as _topk_brute computes them."""
+    if scoring == 0:
+        e = np.exp(scores - scores.max())
+        prob = e / e.sum()
+    else:
+        prob = 1 / (1 + np.exp(-scores))
+    order = np.argsort(-(prob + bias), kind="stable")
+    kept = np.sort(order[:top])
+    out = np.zeros_like(scores)
+    if scoring == 0:
+        m = scores[kept].max() if renorm else scores.max()
+        ex = np.exp(scores - m)
+        out[kept] = ex[kept] / (ex[kept].sum() if renorm else ex.sum())
+    else:
+        sg = 1 / (1 + np.exp(-scores))
+        out[kept] = sg[kept] / (sg[kept].sum() if renorm else 1.0)
+    return out
+
+
+@pytest.mark.parametrize("scoring", [0, 1])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_topk_selection_bias_brute_force(scoring, renorm):
+    """A selection bias changes which experts are kept, never the weights
+    given to them (topk_key, amd-nv-cpu.ll:4653-4660)."""
+    rng = np.random.default_rng(40 + scoring * 2 + renorm)
+    changed = 0
+    for trial in range(30):
+        e = int(rng.integers(4, 300))
+        top = int(rng.integers(1, min(e, 16) + 1))
+        s = rng.standard_normal(e)
+        bias = rng.standard_normal(e) * (0.5 if trial % 2 else 0.02)
+        got = oracle.topk(s, top, scoring, renorm, bias=bias)
+        ref = _topk_biased_brute(s, top, scoring, renorm, bias)
+        assert np.array_equal(got != 0, ref != 0)
+        assert np.allclose(got, ref, rtol=1e-12, atol=1e-15)
+        changed += not np.array_equal(got != 0, oracle.topk(s, top, scoring, renorm) != 0)
+    assert changed > 5  # the bias does move the selection
+    # equal keys: the lower expert wins; a bias that only lifts one expert's key above the others' picks it
+    s = np.zeros(6)
+    assert list(np.nonzero(oracle.topk(s, 2, scoring, renorm, bias=np.zeros(6)))[0]) == [0, 1]
+    b = np.zeros(6)
+    b[4] = 1e-3
+    assert list(np.nonzero(oracle.topk(s, 2, scoring, renorm, bias=b))[0]) == [0, 4]
+
+
+@pytest.mark.parametrize("name", ["linear", "relu", "sigmoid", "silu", "tanh", "gelu", "elu", "selu", "softplus",
+                                  "leak", "exp", "cos", "sqrt", "ln", "log", "huber", "tan", "prelu", "scale"])
+def test_activation_against_independent_forms(name):
+    """The oracle's activation programs against torch's CPU implementations
+    or textbook closed forms written differently (expit, logaddexp, erf-based
+    GELU within the tanh approximation's known error)."""
+    import torch
+    import torch.nn.functional as F
+    from scipy.special import erf, expit
+    x = np.concatenate([np.linspace(-12, 12, 961), [0.0, -0.0, 1e-30, -1e-30, 40.0, -40.0]])
+    if name in ("sqrt",):
+        x = np.abs(x)
+    got = oracle.activation(name, x, factor=0.3)
+    t = torch.from_numpy(x)
+    ref = {
+        "linear": lambda: x,
+        "relu": lambda: np.maximum(x, 0),
+        "sigmoid": lambda: expit(x),
+        "silu": lambda: x * expit(x),
+        "tanh": lambda: np.tanh(x),
+        "gelu": lambda: F.gelu(t, approximate="tanh").numpy(),
+        "elu": lambda: F.elu(t).numpy(),
+        "selu": lambda: F.selu(t).numpy(),
+        "softplus": lambda: np.logaddexp(0, x),
+        "leak": lambda: F.leaky_relu(t, 0.01).numpy(),
+        "exp": lambda: np.exp(x),
+        "cos": lambda: np.cos(x),
+        "sqrt": lambda: np.sqrt(x),
+        "ln": lambda: np.sign(x) * np.log1p(np.abs(x)),
+        "log": lambda: np.sign(x) * np.log10(1 + np.abs(x)),
+        "huber": lambda: np.where(np.abs(x) <= 1, 0.5 * x * x, np.abs(x) - 0.5),
+        "tan": lambda: np.tan(x),
+        "prelu": lambda: np.where(x > 0, x, 0.3 * x),
+        "scale": lambda: 0.3 * x,
+    }[name]()
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-14), name
+    if name == "gelu":  # the tanh form stays within 5e-4 of the exact erf GELU
+        assert np.max(np.abs(got - 0.5 * x * (1 + erf(x / np.sqrt(2))))) < 5e-4
+
+
+def test_activation_gelu_fp16_table():
+    """Gelu under the gelu table: the fp16-rounded input through the tanh form,
+    the result rounded to fp16, inside (-10, 10); x itself above 10, 0 below -10."""
+    x = np.concatenate([np.linspace(-11, 11, 2201), [10.0, -10.0, 10.5, -10.5]])
+    got = oracle.activation("gelu_fp16", x)
+    h = x.astype(np.float16).astype(np.float64)
+    inner = oracle.activation("gelu", h)
+    ref = np.where(x > 10, x, np.where(x < -10, 0.0, inner.astype(np.float32).astype(np.float16).astype(np.float64)))
+    assert np.array_equal(got, ref)
+    assert np.array_equal(got[(x > -10) & (x < 10)].astype(np.float16).astype(np.float64), got[(x > -10) & (x < 10)])
+
+
 # ------------------------------------------------------------------- moe ----
 
 def test_moe_against_numpy_composition():
@@ -359,4 +459,50 @@ def test_moe_against_numpy_composition():
     US = ggml_q4_k(us, 0).reshape(HS, d)
     DS = ggml_q4_k(ds, 0).reshape(d, HS)
     ref += g * (DS @ (silu(GS @ x) * (US @ x)))
+    assert np.allclose(y, ref, rtol=1e-10, atol=1e-10 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("act,gate_act,biased,gated", [("gelu", "sigmoid", True, True), ("relu", "tanh", False, True),
+                                                        ("silu", "linear", True, False)])
+def test_moe_activation_bias_and_ungated_shared(act, gate_act, biased, gated):
+    """gguf_moe's activation, the shared gate's activation, the selection
+    bias and an ungated shared expert, against a numpy composition of the
+    dequantized tensors (textbook decoders), torch's activations and the
+    brute-force biased selection."""
+    import torch
+    import torch.nn.functional as F
+    from scipy.special import expit
+    d, E, top, H, HS = 256, 8, 3, 256, 256
+    fmt = "q4_k"
+    router = synth.f16_weights(E, d, 0.05, seed=11, tag="router")
+    gate = synth.q4_k(E * H, d, seed=12, tag="gate")
+    up = synth.q4_k(E * H, d, seed=13, tag="up")
+    down = synth.q4_k(E * d, H, seed=14, tag="down")
+    sg = synth.f16_weights(1, d, 0.05, seed=15, tag="sg")
+    gs, us, ds = synth.q4_k(HS, d, seed=16, tag="gs"), synth.q4_k(HS, d, seed=17, tag="us"), synth.q4_k(d, HS, seed=18, tag="ds")
+    x = synth.fp16_to_f32(synth.activations_f16(d, seed=19)).astype(np.float64)
+    bias = np.random.default_rng(20).standard_normal(E) * 0.3 if biased else None
+    y, rw = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down, x, scoring=1, hidden_shared=HS,
+                           shared_gate_bits=sg.view(np.uint16) if gated else None, gate_sh=gs, up_sh=us, down_sh=ds,
+                           activation=act, shared_gate_activation=gate_act, selection_bias=bias)
+    R = synth.fp16_to_f32(router.view(np.uint16)).astype(np.float64).reshape(E, d)
+    scores = R @ x
+    w = _topk_biased_brute(scores, top, 1, True, bias) if biased else _topk_brute(scores, top, 1, True)
+    assert np.allclose(rw, w, rtol=1e-12)
+    torch_act = {"gelu": lambda v: F.gelu(torch.from_numpy(v), approximate="tanh").numpy(),
+                 "relu": lambda v: np.maximum(v, 0), "silu": lambda v: v * expit(v), "sigmoid": expit,
+                 "tanh": np.tanh, "linear": lambda v: v}
+    G = ggml_q4_k(gate, 0).reshape(E, H, d)
+    U = ggml_q4_k(up, 0).reshape(E, H, d)
+    D = ggml_q4_k(down, 0).reshape(E, d, H)
+    f = torch_act[act]
+    ref = np.zeros(d)
+    for e in np.nonzero(w)[0]:
+        ref += w[e] * (D[e] @ (f(G[e] @ x) * (U[e] @ x)))
+    SGv = synth.fp16_to_f32(sg.view(np.uint16)).astype(np.float64)
+    g = float(torch_act[gate_act](np.array([SGv @ x]))[0]) if gated else 1.0
+    GS = ggml_q4_k(gs, 0).reshape(HS, d)
+    US = ggml_q4_k(us, 0).reshape(HS, d)
+    DS = ggml_q4_k(ds, 0).reshape(d, HS)
+    ref += g * (DS @ (f(GS @ x) * (US @ x)))
     assert np.allclose(y, ref, rtol=1e-10, atol=1e-10 * np.abs(ref).max())
