@@ -183,6 +183,18 @@ int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, floa
 int rqmv_moe_batch(const rqmv_moe_params* params, const void* x_dev, int x_dtype, int m, int64_t ldx, float* y_dev,
                    int64_t ldy, float* route_dev, void* workspace, size_t workspace_bytes, void* stream);
 
+/* rqmv_moe_batch without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * workspace is the library's own 1 MiB scratch array, one per GPU, held until
+ * the process ends: m positions fit when m * rqmv_moe_workspace_size bytes
+ * <= 1 MiB (the 2048 x 512, 256-expert top-8 block takes about 20 KiB per
+ * position), else RQMV_EINVAL. The call allocates nothing. Every call on one
+ * GPU shares that GPU's scratch: calls that overlap on it (other streams,
+ * other threads) race, so order them. */
+int rqmv_moe_batch_noalloc(const rqmv_moe_params* params, const void* x_dev, int x_dtype, int m, int64_t ldx,
+                           float* y_dev, int64_t ldy, float* route_dev, void* stream);
+
 /* Decode-step helpers. They have no counterpart at the matrix-vector
  * boundary: they run the rest of a decoder layer on the device between the
  * projections, for the end-to-end single-token decode, with the semantics of

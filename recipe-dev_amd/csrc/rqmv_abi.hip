@@ -50,7 +50,15 @@ struct DeviceInfo {
     bool ready = false;
     int cus = 0;
     size_t lds_limit = 0;
+    void* scratch = nullptr;  // this device's copy of `scratch` (rqmv_moe_batch_noalloc)
 };
+
+// The workspace of rqmv_moe_batch_noalloc, for callers that cannot allocate:
+// one copy per GPU, held until the process ends. Host code never passes the
+// array's name to a kernel (on the host it names no device address); it uses
+// each device's address from hipGetSymbolAddress (DeviceInfo::scratch).
+constexpr size_t kMoeScratchBytes = size_t(1) << 20;
+__device__ __align__(256) uint8_t scratch[kMoeScratchBytes];
 
 std::mutex g_mutex;
 DeviceInfo g_devices[64];
@@ -217,6 +225,12 @@ int rqmv_init(int device) {
     e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device);
     if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
     std::lock_guard<std::mutex> lock(g_mutex);
+    if (!g_devices[device].scratch) {  // this device's address of the no-alloc workspace (with it current)
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_devices[device].scratch = ptr;
+    }
     g_devices[device].cus = cus > 0 ? cus : 1;
     g_devices[device].lds_limit = lds > 0 ? (size_t)lds : 65536;
     g_devices[device].ready = true;
@@ -588,6 +602,26 @@ int rqmv_moe_batch(const rqmv_moe_params* params, const void* x_dev, int x_dtype
     e = rq::launch_moe_down(fmt, d, bank_of(params->down_exps), bank_of(params->down_shexp), ws, y_dev, b, info.cus, s);
     if (e != hipSuccess) return hip_fail(e, "moe down launch");
     return RQMV_OK;
+}
+
+int rqmv_moe_batch_noalloc(const rqmv_moe_params* params, const void* x_dev, int x_dtype, int m, int64_t ldx,
+                           float* y_dev, int64_t ldy, float* route_dev, void* stream) {
+    DeviceInfo info;
+    int rc = check_launch(params ? params->router : nullptr, &info);
+    if (rc != RQMV_OK) return rc;
+    rq::MoeDims d;
+    rc = moe_dims(params, &d, info);
+    if (rc != RQMV_OK) return rc;
+    if (m < 1 || m > 65535) return fail(RQMV_EINVAL, "moe: m must be in 1..65535");
+    const size_t per = rq::moe_workspace_bytes(d);
+    if (per * (size_t)m > kMoeScratchBytes)
+        return fail(RQMV_EINVAL, "moe_batch_noalloc: " + std::to_string(m) + " position(s) need " +
+                                     std::to_string(per * (size_t)m) + " bytes of workspace, beyond its " +
+                                     std::to_string(kMoeScratchBytes) + "-byte scratch; use rqmv_moe_batch");
+    // every workspace byte is written before it is read (logits, routing, slot
+    // activations), so nothing needs clearing between calls
+    return rqmv_moe_batch(params, x_dev, x_dtype, m, ldx, y_dev, ldy, route_dev, info.scratch, kMoeScratchBytes,
+                          stream);
 }
 
 int rqmv_moe(const rqmv_moe_params* params, const void* x_dev, int x_dtype, float* y_dev, float* route_dev,

@@ -56,6 +56,8 @@ class _Lib:
         L.rqmv_expert_matvec.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p]
         L.rqmv_moe_workspace_size.argtypes = [c_void_p, POINTER(c_size_t)]
         L.rqmv_moe.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        L.rqmv_moe_batch_noalloc.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p,
+                                             c_void_p]
         L.rqmv_moe_batch.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
                                      c_size_t, c_void_p]
         L.rqmv_add_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]
@@ -517,6 +519,14 @@ class Moe:
         _check(lib().lib.rqmv_moe_batch(byref(self.params), x.ptr, x_dtype, m, ldx, y.ptr, ldy,
                                         route.ptr if route else None, workspace.ptr, workspace.nbytes,
                                         stream.handle if stream else None), "rqmv_moe_batch")
+
+    def run_batch_noalloc(self, x: DeviceBuffer, x_dtype: int, m: int, ldx: int, y: DeviceBuffer, ldy: int,
+                          route: DeviceBuffer | None = None, stream: Stream | None = None):
+        """m positions on the library's own per-GPU scratch (rqmv_moe_batch_noalloc):
+        no workspace and no allocation; calls on one GPU must not overlap."""
+        _check(lib().lib.rqmv_moe_batch_noalloc(byref(self.params), x.ptr, x_dtype, m, ldx, y.ptr, ldy,
+                                                route.ptr if route else None, stream.handle if stream else None),
+               "rqmv_moe_batch_noalloc")
 
     def batch_workspace(self, m: int) -> DeviceBuffer:
         return DeviceBuffer(self.workspace.nbytes * m)
