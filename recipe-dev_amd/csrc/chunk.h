@@ -209,93 +209,143 @@ __device__ __forceinline__ int dot_nibbles4(const uint4& W, const uint4* xd, int
 }
 
 // -------------------------------------------------------------------------
-// Integer dot of one chunk for M activation rows. xd[m][] holds the chunk's
-// activation digit words as staged (Traits::XP parts), xb[m][] its block data:
-// xb[m][0] = (s_0, s_1, sx_0, sx_1), xb[m][1] = (sx_2, sx_3, 0, 0), where s_b is
-// block b's scale and sx the scaled activation sums (per 32-block for Q4_K, per
-// 16-value scale group for Q6_K). Accumulates sum_j w_j x_j into acc[m].
+// Integer dot of one chunk for one activation row. xd[] holds the chunk's
+// activation digit words as staged (Traits::XP parts), xb[] its block data:
+// xb[0] = (s_0, s_1, sx_0, sx_1), xb[1] = (sx_2, sx_3, 0, 0), where s_b is
+// block b's scale (its sign bit set when the chunk holds an outlier) and sx
+// the scaled activation sums (per 32-block for Q4_K, per 16-value scale group
+// for Q6_K). Accumulates sum_j w_j x_j into acc, the outliers' terms aside
+// (dot_outliers).
 // -------------------------------------------------------------------------
-template <int FMT, int M>
-__device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const uint4 (*xd)[Traits<FMT>::XP],
-                                        const uint4 (*xb)[2], float* acc) {
+
+// Word i (0..3, per lane) of a 16-byte part, by selects and a shift (a
+// run-time index into the registers would go through scratch memory).
+__device__ __forceinline__ uint32_t word_at(const uint4& v, int i) {
+    const uint64_t lo = ((uint64_t)v.y << 32) | v.x, hi = ((uint64_t)v.w << 32) | v.z;
+    const uint64_t pair = (i & 2) ? hi : lo;
+    return (uint32_t)(pair >> (32 * (i & 1)));
+}
+
+// True in every active lane when the chunk of any active lane holds an outlier.
+__device__ __forceinline__ bool wave_has_outlier(const uint4& b0) {
+    return __builtin_amdgcn_ballot_w64(((b0.x | b0.y) >> 31) != 0) != 0;
+}
+
+template <int FMT>
+__device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const uint4 (&xd)[Traits<FMT>::XP],
+                                        const uint4 (&xb)[2], float& acc) {
+    const float sb0 = fabsf(wordf(xb[0], 0)), sb1 = fabsf(wordf(xb[0], 1));
     if constexpr (FMT == Q4_K) {
         uint32_t sc0, m0, sc1, m1;
         q4k_scales(d.meta, c & 3, sc0, m0, sc1, m1);
         const float dd = half_lo(d.meta.x), dmin = half_hi(d.meta.x);
         const float s0 = dd * (float)sc0, s1 = dd * (float)sc1;
         const float k0 = fmaf(8.f, s0, -dmin * (float)m0), k1 = fmaf(8.f, s1, -dmin * (float)m1);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const int a0 = dot_nibbles4(d.q[0], xd[m], 0);
-            const int a1 = dot_nibbles4(d.q[1], xd[m], 1);
-            const uint4 b = xb[m][0];
-            float y = acc[m];
-            y = fmaf(s0 * wordf(b, 0), (float)a0, y);
-            y = fmaf(k0, wordf(b, 2), y);
-            y = fmaf(s1 * wordf(b, 1), (float)a1, y);
-            y = fmaf(k1, wordf(b, 3), y);
-            acc[m] = y;
-        }
+        const int a0 = dot_nibbles4(d.q[0], xd, 0);
+        const int a1 = dot_nibbles4(d.q[1], xd, 1);
+        float y = acc;
+        y = fmaf(s0 * sb0, (float)a0, y);
+        y = fmaf(k0, wordf(xb[0], 2), y);
+        y = fmaf(s1 * sb1, (float)a1, y);
+        y = fmaf(k1, wordf(xb[0], 3), y);
+        acc = y;
     } else if constexpr (FMT == Q4_0) {
         const float d0 = half_lo(d.meta.x), d1 = half_hi(d.meta.x);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const int a0 = dot_nibbles4(d.q[0], xd[m], 0);
-            const int a1 = dot_nibbles4(d.q[1], xd[m], 1);
-            const uint4 b = xb[m][0];
-            float y = acc[m];
-            y = fmaf(d0 * wordf(b, 0), (float)a0, y);
-            y = fmaf(d1 * wordf(b, 1), (float)a1, y);
-            acc[m] = y;
-        }
+        const int a0 = dot_nibbles4(d.q[0], xd, 0);
+        const int a1 = dot_nibbles4(d.q[1], xd, 1);
+        float y = acc;
+        y = fmaf(d0 * sb0, (float)a0, y);
+        y = fmaf(d1 * sb1, (float)a1, y);
+        acc = y;
     } else if constexpr (FMT == Q8_0) {
         const float dd = half_lo(d.meta.x);
+        // digit planes: xd[0..1] low bytes, xd[2..3] high bytes (words 0-3, 4-7)
+        int lo = 0, hi = 0;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            // digit planes: xd[m][0..1] low bytes, xd[m][2..3] high bytes (words 0-3, 4-7)
-            int lo = 0, hi = 0;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint4 W = d.q[h], L = xd[m][h], H = xd[m][2 + h];
-                lo = sdot4(W.x, L.x, lo);
-                lo = sdot4(W.y, L.y, lo);
-                lo = sdot4(W.z, L.z, lo);
-                lo = sdot4(W.w, L.w, lo);
-                hi = sdot4(W.x, H.x, hi);
-                hi = sdot4(W.y, H.y, hi);
-                hi = sdot4(W.z, H.z, hi);
-                hi = sdot4(W.w, H.w, hi);
-            }
-            acc[m] = fmaf(dd * wordf(xb[m][0], 0), (float)hi * 256.f + (float)lo, acc[m]);
+        for (int h = 0; h < 2; ++h) {
+            const uint4 W = d.q[h], L = xd[h], H = xd[2 + h];
+            lo = sdot4(W.x, L.x, lo);
+            lo = sdot4(W.y, L.y, lo);
+            lo = sdot4(W.z, L.z, lo);
+            lo = sdot4(W.w, L.w, lo);
+            hi = sdot4(W.x, H.x, hi);
+            hi = sdot4(W.y, H.y, hi);
+            hi = sdot4(W.z, H.z, hi);
+            hi = sdot4(W.w, H.w, hi);
         }
+        acc = fmaf(dd * sb0, (float)hi * 256.f + (float)lo, acc);
     } else if constexpr (FMT == Q6_K) {
         const float dd = half_lo(d.meta.y);
+        float y = acc;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const uint32_t L0 = word(d.q[g >> 1], (g & 1) * 2), L1 = word(d.q[g >> 1], (g & 1) * 2 + 1);
             const uint32_t H = word(d.q[2], g);
             const uint32_t He = H & 0x33333333u, Ho = (H >> 2) & 0x33333333u;
             const float dsc = dd * (float)(int8_t)((d.meta.x >> (8 * g)) & 0xffu);
+            int al[4], ah[4];
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                int al[4], ah[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // words 2g, 2g+1 of digit i: part 2i + g/2, components (g&1)*2, (g&1)*2+1
-                    const uint4 D = xd[m][2 * i + (g >> 1)];
-                    const uint32_t D0 = word(D, (g & 1) * 2), D1 = word(D, (g & 1) * 2 + 1);
-                    al[i] = sdot8(L1, D1, sdot8(L0, D0, 0));
-                    ah[i] = sdot8(Ho, D1, sdot8(He, D0, 0));
-                }
-                const int l = ((al[3] * 16 + al[2]) * 16 + al[1]) * 16 + al[0];
-                const int h = ((ah[3] * 16 + ah[2]) * 16 + ah[1]) * 16 + ah[0];
-                const float s = wordf(xb[m][0], g >> 1);
-                const float sx = g < 2 ? wordf(xb[m][0], 2 + g) : wordf(xb[m][1], g - 2);
-                float y = fmaf(dsc * s, (float)(h * 16 + l), acc[m]);
-                acc[m] = fmaf(-24.f * dsc, sx, y);
+            for (int i = 0; i < 4; ++i) {
+                // words 2g, 2g+1 of digit i: part 2i + g/2, components (g&1)*2, (g&1)*2+1
+                const uint4 D = xd[2 * i + (g >> 1)];
+                const uint32_t D0 = word(D, (g & 1) * 2), D1 = word(D, (g & 1) * 2 + 1);
+                al[i] = sdot8(L1, D1, sdot8(L0, D0, 0));
+                ah[i] = sdot8(Ho, D1, sdot8(He, D0, 0));
             }
+            const int l = ((al[3] * 16 + al[2]) * 16 + al[1]) * 16 + al[0];
+            const int h = ((ah[3] * 16 + ah[2]) * 16 + ah[1]) * 16 + ah[0];
+            const float s = g < 2 ? sb0 : sb1;
+            const float sx = g < 2 ? wordf(xb[0], 2 + g) : wordf(xb[1], g - 2);
+            y = fmaf(dsc * s, (float)(h * 16 + l), y);
+            y = fmaf(-24.f * dsc, sx, y);
+        }
+        acc = y;
+    }
+}
+
+// The outliers' terms of one chunk: o = (v_0, v_1, i_0, i_1), each block's
+// extracted activation (0 if none) and its index; adds w_{i_b} v_b with the
+// weight decoded exactly (w = d sc q - dmin m for Q4_K, d (q - 8) for Q4_0,
+// d q for Q8_0, d sc (q - 32) for Q6_K). Run when wave_has_outlier says some
+// lane of the wave needs it.
+template <int FMT>
+__device__ __forceinline__ void dot_outliers(const ChunkData<FMT>& d, int c, const uint4& o, float& acc) {
+    float y = acc;
+    if constexpr (FMT == Q4_K) {
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(d.meta, c & 3, sc0, m0, sc1, m1);
+        const float dd = half_lo(d.meta.x), dmin = half_hi(d.meta.x);
+        const float s0 = dd * (float)sc0, s1 = dd * (float)sc1;
+        const float k0 = fmaf(8.f, s0, -dmin * (float)m0), k1 = fmaf(8.f, s1, -dmin * (float)m1);
+        const int j0 = (int)o.z, j1 = (int)o.w;
+        const int q0 = sbfe(word_at(d.q[0], j0 >> 3), 4 * (j0 & 7), 4);
+        const int q1 = sbfe(word_at(d.q[1], j1 >> 3), 4 * (j1 & 7), 4);
+        y = fmaf(fmaf(s0, (float)q0, k0), wordf(o, 0), y);
+        y = fmaf(fmaf(s1, (float)q1, k1), wordf(o, 1), y);
+    } else if constexpr (FMT == Q4_0) {
+        const int j0 = (int)o.z, j1 = (int)o.w;
+        const int q0 = sbfe(word_at(d.q[0], j0 >> 3), 4 * (j0 & 7), 4);
+        const int q1 = sbfe(word_at(d.q[1], j1 >> 3), 4 * (j1 & 7), 4);
+        y = fmaf((float)q0 * half_lo(d.meta.x), wordf(o, 0), y);
+        y = fmaf((float)q1 * half_hi(d.meta.x), wordf(o, 1), y);
+    } else if constexpr (FMT == Q8_0) {
+        const int j = (int)o.z;
+        const uint32_t w0 = word_at(d.q[0], (j >> 2) & 3), w1 = word_at(d.q[1], (j >> 2) & 3);
+        const uint32_t wd = j < 16 ? w0 : w1;  // (selecting the part first would index registers at run time)
+        y = fmaf(half_lo(d.meta.x) * (float)sbfe(wd, 8 * (j & 3), 8), wordf(o, 0), y);
+    } else if constexpr (FMT == Q6_K) {
+        // the outlier at position e = 32 b + i_b of the chunk, in scale group e / 16
+        const float dd = half_lo(d.meta.y);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int e = 32 * b + (int)word(o, 2 + b), g = e >> 4, j = e & 15;
+            const int l = sbfe(word_at(d.q[b], (e >> 3) & 3), 4 * (e & 7), 4) + 8;
+            const int h = (int)bfe(word_at(d.q[2], g), j < 8 ? 4 * j : 4 * (j - 8) + 2, 2);
+            const float dsc = dd * (float)(int8_t)((d.meta.x >> (8 * g)) & 0xffu);
+            y = fmaf(dsc * (float)(l + 16 * h - 32), wordf(o, b), y);
         }
     }
+    acc = y;
 }
 
 // fp16 activation pairs against F16 weights (router-sized products).

@@ -57,6 +57,12 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
 hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const LaunchShape& s, hipStream_t stream,
                          hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 
+// The burst form of the M <= 2 integer product (long rows, every weight load
+// issued at launch), when it applies: returns false (nothing launched) when
+// the shape does not suit it, else launches and puts the result in *err.
+bool try_launch_burst(int fmt, int xtype, int M, const MvParams& p, int cus, hipStream_t stream, hipEvent_t ev0,
+                      hipEvent_t ev1, hipError_t* err);
+
 // Exact fp32 decode of every weight, rows x cols in GGUF order.
 hipError_t launch_dequant(int fmt, const Planes& P, int64_t rows, int cols, float* out, hipStream_t stream);
 

@@ -136,7 +136,8 @@ __device__ __forceinline__ void load_rows_rs(const MvParams& p, __amdgpu_buffer_
 // digits of every activation row; the tile's reduction after its last step.
 template <int FMT, int M, int R, bool NORM = false>
 __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, int sub, int g, const ChunkData<FMT> (&d)[R],
-                                         float (&acc)[R][M], const uint4* xd, const uint4* xb, float norm_scale = 1.f) {
+                                         float (&acc)[R][M], const uint4* xd, const uint4* xb, bool outliers,
+                                         float norm_scale = 1.f) {
     constexpr int XP = Traits<FMT>::XP;
     const int nch = p.P.nch;
     const int c = w.chunk();
@@ -145,15 +146,21 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
         // one activation row's digits live at a time; the weights stay in registers
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
-            uint4 xv[1][XP];
-            uint4 bv[1][2];
+            uint4 xv[XP];
+            uint4 bv[2];
 #pragma unroll
-            for (int j = 0; j < XP; ++j) xv[0][j] = xd[(mm * XP + j) * nch + c];
-            bv[0][0] = xb[(mm * 2 + 0) * nch + c];
-            bv[0][1] = xb[(mm * 2 + 1) * nch + c];
+            for (int j = 0; j < XP; ++j) xv[j] = xd[(mm * XP + j) * nch + c];
+            bv[0] = xb[(mm * 3 + 0) * nch + c];
+            bv[1] = xb[(mm * 3 + 1) * nch + c];
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < rows) dot_int<FMT, 1>(d[r], c, xv, bv, &acc[r][mm]);
+                if (row0 + r < rows) dot_int<FMT>(d[r], c, xv, bv, acc[r][mm]);
+            if (outliers && wave_has_outlier(bv[0])) {
+                const uint4 o = xb[(mm * 3 + 2) * nch + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (row0 + r < rows) dot_outliers<FMT>(d[r], c, o, acc[r][mm]);
+            }
         }
     }
     if (w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, norm_scale);
@@ -176,6 +183,7 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     constexpr int NB = ring_depth<M, R>();
     extern __shared__ uint4 smem[];
     __shared__ float block_scalar[8];  // NORM: the waves' sums of squares
+    __shared__ int wave_flags[8];      // the waves' "a staged block holds an outlier"
     const int nch = p.P.nch;
     uint4* xd = smem;
     uint4* xb = smem + M * XP * nch;
@@ -202,17 +210,22 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
-        stage_multi_finish<FMT, XF32, NORM>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb), nin, &ssq);
+        publish_outliers(
+            stage_multi_finish<FMT, XF32, NORM>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb), nin, &ssq),
+            wave_flags);
     } else {
 #pragma unroll
         for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
-        stage_all<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, xd, reinterpret_cast<float*>(xb), nin, &ssq);
+        publish_outliers(
+            stage_all<FMT, XF32, NORM>(nch, p.K, p.x, p.ldx, M, p.block, xd, reinterpret_cast<float*>(xb), nin, &ssq),
+            wave_flags);
     }
     if constexpr (NORM) {
         ssq = group_sum(ssq, 64);
         if (lane == 63) block_scalar[threadIdx.x >> 6] = ssq;
     }
     __syncthreads();
+    const bool outliers = read_outliers(wave_flags, p.block);
     float norm_scale = 1.f;
     if constexpr (NORM) {  // the waves' sums in order: every workgroup forms the same factor
         float t = 0.f;
@@ -229,7 +242,7 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             if (!w[i].valid()) goto done;
-            step_int<FMT, M, R, NORM>(p, w[i], sub, g, buf[i], acc, xd, xb, norm_scale);
+            step_int<FMT, M, R, NORM>(p, w[i], sub, g, buf[i], acc, xd, xb, outliers, norm_scale);
             // this buffer takes the step after the latest one issued
             w[i] = w[(i + NB - 1) % NB];
             w[i].next();
@@ -238,6 +251,78 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     }
 done:
     return;
+}
+
+// Burst form of matvec_int for long rows at one or two activation rows: every
+// wave owns U units (row, step) fixed at launch and issues the loads of all of
+// them before anything else, so that the whole matrix is requested within the
+// first moments of the launch and HBM streams it at full rate; then the
+// activations are staged (their loads were issued first, so waiting for them
+// leaves every weight load in flight), and the units are computed in the order
+// their loads return. Rows are dealt to waves round-robin (row = wave + r *
+// waves), so that the waves' r-th rows together are one contiguous region.
+// A wave covers a row with all 64 lanes (chunk lane + 64 s at step s); S
+// steps per row, U / S rows per wave.
+template <int FMT, int M, int U, bool XF32>
+__global__ void __launch_bounds__(256) matvec_burst(MvParams p, int S) {
+    constexpr int XP = Traits<FMT>::XP;
+    extern __shared__ uint4 smem[];
+    const int nch = p.P.nch;
+    uint4* xd = smem;
+    uint4* xb = smem + M * XP * nch;
+    const int lane = threadIdx.x & 63;
+    const int waves = (int)gridDim.x * (p.block >> 6);
+    const int wave = (int)blockIdx.x * (p.block >> 6) + (int)(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
+    const int rows = (int)p.rows;
+
+    __shared__ int wave_flags[4];
+    ChunkData<FMT> d[U];
+    StageItem<XF32> it[kStageNJ];
+    stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, M, p.block, it);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int r = u / S, st = u - r * S;
+        const int row = wave + r * waves, c = lane + 64 * st;
+        load_chunk_rs<FMT>(rs, p.P, (uint32_t)row, c, row < rows && c < nch, d[u]);
+    }
+    publish_outliers(stage_multi_finish<FMT, XF32>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb)),
+                     wave_flags);
+    __syncthreads();
+    const bool outliers = read_outliers(wave_flags, p.block);
+
+    float acc[M];
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) acc[mm] = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int r = u / S, st = u - r * S;
+        const int row = wave + r * waves, c = lane + 64 * st;
+        if (c < nch) {
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) {
+                uint4 xv[XP];
+                uint4 bv[2];
+#pragma unroll
+                for (int j = 0; j < XP; ++j) xv[j] = xd[(mm * XP + j) * nch + c];
+                bv[0] = xb[(mm * 3 + 0) * nch + c];
+                bv[1] = xb[(mm * 3 + 1) * nch + c];
+                dot_int<FMT>(d[u], c, xv, bv, acc[mm]);
+                if (outliers && wave_has_outlier(bv[0]))
+                    dot_outliers<FMT>(d[u], c, xb[(mm * 3 + 2) * nch + c], acc[mm]);
+            }
+        }
+        if (st == S - 1) {
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) {
+                const float v = group_sum(acc[mm], 64);
+                if (lane == 63 && row < rows) p.y[(int64_t)mm * p.ldy + row] = v;
+                acc[mm] = 0.f;
+            }
+        }
+    }
 }
 
 // F16 weights (router-sized): fp16 activations through v_dot2_f32_f16, fp32
@@ -421,6 +506,72 @@ static hipError_t launch_fmt(int xtype, int M, const MvParams& p, const LaunchSh
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
+}
+
+// When the burst form runs, and its units per wave. Measured on MI355X (one
+// product, weights rotating through HBM): it wins on products of a few tens of
+// MB at most, whose ring form holds one tile per wave anyway (Q4_K 4096x4096,
+// fp16 x: 6.03 -> 5.21 us; Q8_0 4096x4096, fp32 x: 6.27 -> 5.68 us, each at
+// U = 4), and loses on larger ones, where all of a wave's loads in flight at
+// once delay its first row and the tail (Q4_K 4096->14336: 9.5 -> 10.7 us at
+// U = 4, 11.3-12.4 at U = 2, 6, 8). U = 4 units: 4 rows of one step, or 2 of
+// two. RQMV_BURST=0 turns it off, RQMV_BURST_U forces U.
+constexpr int64_t kBurstMaxBytes = 20ll << 20;
+
+static bool burst_plan(int fmt, int64_t rows, int64_t nch, int64_t row_bytes, int M, int& U, int& S, int& grid) {
+    if (env_int("RQMV_BURST", 1) == 0 || M > 2 || fmt == F16 || nch < 48) return false;
+    if (rows * row_bytes > kBurstMaxBytes && env_int("RQMV_BURST_U", 0) == 0) return false;
+    S = (int)((nch + 63) / 64);
+    U = env_int("RQMV_BURST_U", 4);
+    if (U % S != 0 || (U != 2 && U != 4 && U != 6 && U != 8)) return false;
+    const int64_t waves = (rows + U / S - 1) / (U / S);
+    grid = (int)((waves + 3) / 4);
+    return true;
+}
+
+template <int FMT, int M, int U>
+static hipError_t launch_burst_u(int xtype, const MvParams& p_in, int S, int grid, hipStream_t stream, hipEvent_t ev0,
+                                 hipEvent_t ev1) {
+    MvParams p = p_in;
+    p.block = 256;
+    const size_t lds = matvec_lds_bytes(FMT, xtype, M, p.K);
+    auto kernel = xtype == X_F16 ? matvec_burst<FMT, M, U, false> : matvec_burst<FMT, M, U, true>;
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    if (ev0 || ev1)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(256), (uint32_t)lds, stream, ev0, ev1, 0u, p, S);
+    else
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, stream, p, S);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t launch_burst(int xtype, int M, int U, const MvParams& p, int S, int grid, hipStream_t stream,
+                               hipEvent_t ev0, hipEvent_t ev1) {
+#define RQ_B(MM, UU) \
+    if (M == MM && U == UU) return launch_burst_u<FMT, MM, UU>(xtype, p, S, grid, stream, ev0, ev1);
+    RQ_B(1, 2) RQ_B(1, 4) RQ_B(1, 6) RQ_B(1, 8) RQ_B(2, 2) RQ_B(2, 4) RQ_B(2, 6) RQ_B(2, 8)
+#undef RQ_B
+    return hipErrorInvalidValue;
+}
+
+bool try_launch_burst(int fmt, int xtype, int M, const MvParams& p, int cus, hipStream_t stream, hipEvent_t ev0,
+                      hipEvent_t ev1, hipError_t* err) {
+    int U, S, grid;
+    (void)cus;
+    if (!burst_plan(fmt, p.rows, p.P.nch, p.P.row_bytes, M, U, S, grid)) return false;
+    if (stage_items_host(fmt, p.P.nch, M) > kStageNJ * 256) return false;  // the staging holds four items a thread
+    switch (fmt) {
+        case Q4_0: *err = launch_burst<Q4_0>(xtype, M, U, p, S, grid, stream, ev0, ev1); break;
+        case Q8_0: *err = launch_burst<Q8_0>(xtype, M, U, p, S, grid, stream, ev0, ev1); break;
+        case Q4_K: *err = launch_burst<Q4_K>(xtype, M, U, p, S, grid, stream, ev0, ev1); break;
+        case Q6_K: *err = launch_burst<Q6_K>(xtype, M, U, p, S, grid, stream, ev0, ev1); break;
+        default: return false;
+    }
+    return true;
 }
 
 hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const LaunchShape& s, hipStream_t stream,

@@ -290,8 +290,11 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     // the first tile's weights are requested before the activations are staged
     ChunkData<FMT> dg0, du0, dg1, du1;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, dg0, du0);
-    stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb));
+    __shared__ int wave_flags[kMoeThreads / 64];
+    publish_outliers(stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
+                     wave_flags);
     __syncthreads();
+    const bool outliers = read_outliers(wave_flags, kMoeThreads);
     if constexpr (!RING) {
         bool fetched = true;
         for (; tile < tiles; tile += stride) {
@@ -300,14 +303,19 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
             for (int c = g; c < nch; c += G) {
                 if (!fetched) fetch(r, c, dg0, du0);
                 fetched = false;
-                uint4 xv[1][XP];
-                uint4 bv[1][2];
+                uint4 xv[XP];
+                uint4 bv[2];
 #pragma unroll
-                for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
-                bv[0][0] = xb[c];
-                bv[0][1] = xb[nch + c];
-                dot_int<FMT, 1>(dg0, c, xv, bv, &ag);
-                dot_int<FMT, 1>(du0, c, xv, bv, &au);
+                for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+                bv[0] = xb[c];
+                bv[1] = xb[nch + c];
+                dot_int<FMT>(dg0, c, xv, bv, ag);
+                dot_int<FMT>(du0, c, xv, bv, au);
+                if (outliers && wave_has_outlier(bv[0])) {
+                    const uint4 o = xb[2 * nch + c];
+                    dot_outliers<FMT>(dg0, c, o, ag);
+                    dot_outliers<FMT>(du0, c, o, au);
+                }
             }
             ag = group_sum(ag, G);
             au = group_sum(au, G);
@@ -323,14 +331,19 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
         float ag = 0.f, au = 0.f;
         for (int c = g; c < nch; c += G) {
             if (c != g) fetch(r, c, dg, du);  // a row longer than one chunk per lane
-            uint4 xv[1][XP];
-            uint4 bv[1][2];
+            uint4 xv[XP];
+            uint4 bv[2];
 #pragma unroll
-            for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
-            bv[0][0] = xb[c];
-            bv[0][1] = xb[nch + c];
-            dot_int<FMT, 1>(dg, c, xv, bv, &ag);
-            dot_int<FMT, 1>(du, c, xv, bv, &au);
+            for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+            bv[0] = xb[c];
+            bv[1] = xb[nch + c];
+            dot_int<FMT>(dg, c, xv, bv, ag);
+            dot_int<FMT>(du, c, xv, bv, au);
+            if (outliers && wave_has_outlier(bv[0])) {
+                const uint4 o = xb[2 * nch + c];
+                dot_outliers<FMT>(dg, c, o, ag);
+                dot_outliers<FMT>(du, c, o, au);
+            }
         }
         ag = group_sum(ag, G);
         au = group_sum(au, G);
@@ -384,8 +397,11 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
     float w0, w1;
     int lc0, lc1;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd0, w0, lc0);
-    stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb));
+    __shared__ int wave_flags[kMoeThreads / 64];
+    publish_outliers(stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
+                     wave_flags);
     __syncthreads();
+    const bool outliers = read_outliers(wave_flags, kMoeThreads);
     if constexpr (!RING) {
         bool fetched = true;
         for (; tile < tiles; tile += stride) {
@@ -394,14 +410,15 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
             for (int c = g; c < nch; c += G) {
                 if (!fetched) fetch(n, c, cd0, w0, lc0);
                 fetched = false;
-                uint4 xv[1][XP];
-                uint4 bv[1][2];
+                uint4 xv[XP];
+                uint4 bv[2];
 #pragma unroll
-                for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
-                bv[0][0] = xb[c];
-                bv[0][1] = xb[nch + c];
+                for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+                bv[0] = xb[c];
+                bv[1] = xb[nch + c];
                 float part = 0.f;
-                dot_int<FMT, 1>(cd0, lc0, xv, bv, &part);
+                dot_int<FMT>(cd0, lc0, xv, bv, part);
+                if (outliers && wave_has_outlier(bv[0])) dot_outliers<FMT>(cd0, lc0, xb[2 * nch + c], part);
                 acc = fmaf(w0, part, acc);
             }
             acc = group_sum(acc, G);
@@ -417,14 +434,15 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
         float acc = 0.f;
         for (int c = g; c < nch; c += G) {
             if (c != g) fetch(n, c, cd, w, lc);  // the lane's later chunks of the row, in turn
-            uint4 xv[1][XP];
-            uint4 bv[1][2];
+            uint4 xv[XP];
+            uint4 bv[2];
 #pragma unroll
-            for (int j = 0; j < XP; ++j) xv[0][j] = xd[j * nch + c];
-            bv[0][0] = xb[c];
-            bv[0][1] = xb[nch + c];
+            for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+            bv[0] = xb[c];
+            bv[1] = xb[nch + c];
             float part = 0.f;
-            dot_int<FMT, 1>(cd, lc, xv, bv, &part);
+            dot_int<FMT>(cd, lc, xv, bv, part);
+            if (outliers && wave_has_outlier(bv[0])) dot_outliers<FMT>(cd, lc, xb[2 * nch + c], part);
             acc = fmaf(w, part, acc);
         }
         acc = group_sum(acc, G);

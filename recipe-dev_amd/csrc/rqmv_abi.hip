@@ -201,7 +201,14 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
         rq::LaunchShape s = rq::plan_matvec(w->fmt, rows, w->cols, mb, xtype, info.cus);
         p.G = s.G;
         const bool first = done == 0, last = done + mb >= m;
-        hipError_t e = rq::launch_matvec(w->fmt, xtype, mb, p, s, stream, first ? ev0 : nullptr, last ? ev1 : nullptr);
+        hipError_t e = hipSuccess;
+        if (!extra_row && rq::try_launch_burst(w->fmt, xtype, mb, p, info.cus, stream, first ? ev0 : nullptr,
+                                               last ? ev1 : nullptr, &e)) {
+            if (e != hipSuccess) return hip_fail(e, "matvec launch");
+            done += mb;
+            continue;
+        }
+        e = rq::launch_matvec(w->fmt, xtype, mb, p, s, stream, first ? ev0 : nullptr, last ? ev1 : nullptr);
         if (e != hipSuccess) return hip_fail(e, "matvec launch");
         done += mb;
     }

@@ -2,7 +2,12 @@
 //
 // Quantized weights (integer kernels). Each 32-value block b of an activation
 // row becomes 16-bit integers x = rint(v * 30583 / max|v|) with scale
-// s_b = max|v| / 30583. For 4-bit formats each x is split into four balanced
+// s_b = max|v| / 30583, so every value is within s_b / 2 (1.64e-5 of the
+// block's largest magnitude) of s_b x. A block whose largest magnitude is more
+// than kOutlierRatio times its second largest has that one value taken out
+// (encoded as 0, the block scaled by the second largest): it goes to the
+// block's outlier slot and the kernels multiply it exactly in fp32 with its
+// weight, so one outlier per block does not coarsen the others. For 4-bit formats each x is split into four balanced
 // hex digits (x + 0x8888 has hex digits d_i + 8, so (x + 0x8888) ^ 0x8888 holds
 // every d_i as a signed nibble) and the digits are transposed into words of
 // eight values per digit, the weights' nibble order. For Q8_0 x is split into
@@ -10,8 +15,11 @@
 //   LDS: xd [m][part][chunk] 16-byte digit words (Traits::XP parts per chunk:
 //        nibble formats: part 2i + b holds digit i of the chunk's block b;
 //        Q8_0: parts 0-1 low bytes, parts 2-3 high bytes),
-//        xb [m][2][chunk] block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -),
-//        sx = s * sum x over the block (Q4_K) or the 16-value group (Q6_K).
+//        xb [m][3][chunk] block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -),
+//        sx = s * sum x over the block (Q4_K) or the 16-value group (Q6_K),
+//        and the outlier slot (v_0, v_1, i_0, i_1): each block's extracted
+//        value (0 if none) and its index in the block; a chunk with an
+//        outlier stores its s_0 (or s_1) with the sign bit set.
 // F16 weights: fp16 activations as [m][part][chunk] 16-byte units of natural
 // pairs, or fp32 activations as [m][part][chunk] units of four floats.
 // Columns at or beyond K read as zero; lanes on consecutive chunks read
@@ -23,6 +31,7 @@
 namespace rq {
 
 constexpr float kXMax = 30583.f;  // 7 * (1 + 16 + 256 + 4096): four balanced hex digits
+constexpr float kOutlierRatio = 4.f;  // largest / second largest magnitude beyond which the largest is exact
 
 // Work item u = ((m * nch + c) * BLK + b) * 4 + q stages the eight values
 // 8q..8q+7 of block b of chunk c of row m. The four items of a block sit in an
@@ -30,6 +39,10 @@ constexpr float kXMax = 30583.f;  // 7 * (1 + 16 + 256 + 4096): four balanced he
 template <int FMT>
 __device__ __forceinline__ int stage_items(int nch, int M) {
     return M * nch * Traits<FMT>::BLK * 4;
+}
+
+inline int stage_items_host(int fmt, int64_t nch, int M) {
+    return (int)(M * nch * (fmt == Q8_0 ? 1 : 2) * 4);
 }
 
 template <bool XF32, bool NORM = false>
@@ -137,8 +150,9 @@ __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, ui
 
 // Encodes item u and stores it into LDS. Every lane of the item's quad must
 // run it together (the block maximum and sums move through DPP).
+// Returns whether the item's block holds an outlier.
 template <int FMT, bool XF32, bool NORM = false>
-__device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageItem<XF32, NORM>& it, uint4* xd,
+__device__ __forceinline__ bool stage_finish(int u, int nch, int K, const StageItem<XF32, NORM>& it, uint4* xd,
                                              float* xbf, const NormIn& nin = NormIn{}, float* ss = nullptr) {
     constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP;
     const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
@@ -186,18 +200,58 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
     // A NaN or an infinity anywhere in the block makes the block's scale NaN
     // (its digits are zero), so every product that reads the block is NaN:
     // a non-finite activation is never dropped by the maximum or the rounding.
-    float amax = 0.f;
+    float imax = 0.f;  // this item's largest magnitude
     int bad = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        amax = fmaxf(amax, fabsf(v[k]));
+        imax = fmaxf(imax, fabsf(v[k]));
         bad |= !(fabsf(v[k]) <= 3.402823466e38f);
     }
+    float amax = imax;
     amax = fmaxf(amax, dpp_quad_f32<0xB1>(amax));  // quad_perm [1,0,3,2]
     amax = fmaxf(amax, dpp_quad_f32<0x4E>(amax));  // quad_perm [2,3,0,1]
     bad |= dpp_i32<0xB1>(bad);
     bad |= dpp_i32<0x4E>(bad);
     if (!live) amax = 0.f;
+    // The largest magnitude exceeds kOutlierRatio times the second largest
+    // exactly when it is the block's only value at or above amax / 4. When two
+    // of the quad's items reach amax / 4 (ordinary activations, always) there
+    // is none; otherwise the values are counted (a rare, quad-uniform branch).
+    const float thr = amax * (1.0f / kOutlierRatio);
+    int hi_items = imax >= thr;
+    hi_items += dpp_i32<0xB1>(hi_items);
+    hi_items += dpp_i32<0x4E>(hi_items);
+    bool outlier = false;
+    if (hi_items == 1 && live && !bad) {
+        int big = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) big += fabsf(v[k]) >= thr;
+        big += dpp_i32<0xB1>(big);
+        big += dpp_i32<0x4E>(big);
+        outlier = big == 1;
+    }
+    float ov = 0.f;
+    int gi = 0;
+    if (outlier) {  // (rare: a quad-uniform branch)
+        // its owner takes the value out; the block is scaled by the rest
+        float rest = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (fabsf(v[k]) >= amax * (1.0f / kOutlierRatio)) {
+                ov = v[k];
+                gi = q * 8 + k;
+                v[k] = 0.f;
+            }
+            rest = fmaxf(rest, fabsf(v[k]));
+        }
+        rest = fmaxf(rest, dpp_quad_f32<0xB1>(rest));
+        rest = fmaxf(rest, dpp_quad_f32<0x4E>(rest));
+        ov += dpp_quad_f32<0xB1>(ov);  // the value and its index, in every lane of the quad
+        ov += dpp_quad_f32<0x4E>(ov);
+        gi += dpp_i32<0xB1>(gi);
+        gi += dpp_i32<0x4E>(gi);
+        amax = rest;
+    }
     if (bad) {
         amax = 0.f;
 #pragma unroll
@@ -222,12 +276,22 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
 #pragma unroll
         for (int i = 0; i < 4; ++i) xdw[((m * XP + 2 * i + b) * nch + c) * 4 + q] = w4[i];
     }
-    // block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -)
+    // block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -), outlier slot (v_0, v_1, i_0, i_1)
     const int pair = sum + dpp_i32<0xB1>(sum);   // this half block (16 values)
     const int whole = pair + dpp_i32<0x4E>(pair);  // the block
-    float* b0 = xbf + ((m * 2 + 0) * nch + c) * 4;
-    float* b1 = xbf + ((m * 2 + 1) * nch + c) * 4;
-    if (q == 0) b0[b] = s;
+    float* b0 = xbf + ((m * 3 + 0) * nch + c) * 4;
+    float* b1 = xbf + ((m * 3 + 1) * nch + c) * 4;
+    float* bo = xbf + ((m * 3 + 2) * nch + c) * 4;
+    if (q == 0) {
+        b0[b] = outlier ? -s : s;  // the sign bit marks a chunk with an outlier (s >= 0 otherwise)
+        bo[b] = ov;
+        reinterpret_cast<int*>(bo)[2 + b] = outlier ? gi : 0;
+        if constexpr (BLK == 1) {
+            b0[1] = 0.f;  // (read with s_0 for the outlier mark)
+            bo[1] = 0.f;
+            reinterpret_cast<int*>(bo)[3] = 0;
+        }
+    }
     if constexpr (FMT == Q4_K) {
         if (q == 0) b0[2 + b] = s * (float)whole;
     } else if constexpr (FMT == Q6_K) {
@@ -237,6 +301,20 @@ __device__ __forceinline__ void stage_finish(int u, int nch, int K, const StageI
             if (g < 2) b0[2 + g] = sx; else b1[g - 2] = sx;
         }
     }
+    return outlier;
+}
+
+// A workgroup-uniform "some staged block holds an outlier", from each
+// thread's own answer: one word per wave in `wave_flags` (every wave writes
+// its own), read back after the barrier that follows the staging.
+__device__ __forceinline__ void publish_outliers(bool mine, int* wave_flags) {
+    const bool any = __builtin_amdgcn_ballot_w64(mine) != 0;
+    if ((threadIdx.x & 63) == 0) wave_flags[threadIdx.x >> 6] = any ? 1 : 0;
+}
+__device__ __forceinline__ bool read_outliers(const int* wave_flags, int nthreads) {
+    int any = 0;
+    for (int i = 0; i < (nthreads >> 6); ++i) any |= wave_flags[i];
+    return __builtin_amdgcn_readfirstlane(any) != 0;
 }
 
 // Staging with up to NJ items per thread: all activation loads are issued
@@ -260,33 +338,38 @@ __device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x,
 }
 
 template <int FMT, bool XF32, bool NORM = false>
-__device__ __forceinline__ void stage_multi_finish(int nch, int K, int M, int nthreads,
+__device__ __forceinline__ bool stage_multi_finish(int nch, int K, int M, int nthreads,
                                                    const StageItem<XF32, NORM> (&it)[kStageNJ], uint4* xd, float* xbf,
                                                    const NormIn& nin = NormIn{}, float* ss = nullptr) {
     const int total = stage_items<FMT>(nch, M);
+    bool out = false;
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
         const int u = (int)threadIdx.x + j * nthreads;
-        if (u < total) stage_finish<FMT, XF32, NORM>(u, nch, K, it[j], xd, xbf, nin, ss);
+        if (u < total) out |= stage_finish<FMT, XF32, NORM>(u, nch, K, it[j], xd, xbf, nin, ss);
     }
+    return out;
 }
 
 // Plain loop (used when a block has more items than kStageNJ per thread).
 template <int FMT, bool XF32, bool NORM = false>
-__device__ __forceinline__ void stage_all(int nch, int K, const void* x, int64_t ldx, int M, int nthreads, uint4* xd,
+__device__ __forceinline__ bool stage_all(int nch, int K, const void* x, int64_t ldx, int M, int nthreads, uint4* xd,
                                           float* xbf, const NormIn& nin = NormIn{}, float* ss = nullptr) {
     const int total = stage_items<FMT>(nch, M);
+    bool out = false;
     for (int u = threadIdx.x; u < total; u += nthreads) {
         StageItem<XF32, NORM> it;
         stage_issue<FMT, XF32, NORM>(u, nch, K, x, ldx, it, nin);
-        stage_finish<FMT, XF32, NORM>(u, nch, K, it, xd, xbf, nin, ss);
+        out |= stage_finish<FMT, XF32, NORM>(u, nch, K, it, xd, xbf, nin, ss);
     }
+    return out;
 }
 
-// LDS bytes of a staged activation block for the integer kernels.
+// LDS bytes of a staged activation block for the integer kernels: digit
+// words, then xb [m][3][chunk] (block data and the outlier slot).
 __host__ __device__ inline size_t stage_bytes_int(int fmt, int M, int nch) {
     const int xp = fmt == Q8_0 ? 4 : 8;
-    return (size_t)M * nch * (size_t)(xp + 2) * 16;
+    return (size_t)M * nch * (size_t)(xp + 3) * 16;
 }
 
 // F16 weights: fp16 activations as natural pairs, or fp32 activations.

@@ -1,0 +1,76 @@
+"""A CPU restatement of the activation encoding of the integer matvec
+kernels (recipe-dev_amd/csrc/stage.h), test infrastructure.
+
+Every 32-value block of an activation row becomes 16-bit integers
+x_i = clamp(rint(v_i * (30583 / amax)), -30583, 30583) with the block scale
+s = amax * fp32(1 / 30583); the kernels' products are exact integer dots of
+these against the weights' integer codes, scaled per block in fp32, so the
+activation a kernel multiplies is s * x_i. With outlier extraction, a block
+whose largest magnitude exceeds `threshold` times its second largest has that
+one value (the lowest index among equal magnitudes) taken out: it is encoded
+as 0, the block is scaled by the second largest magnitude, and the value
+itself is multiplied exactly (in fp32) with its weight.
+
+The functions return the effective activations and the error bound they
+obey: |v_i - s x_i| <= 0.51 s for every encoded value (half a step, plus the
+fp32 roundings of v * inv and of s, each below 2^-23 * 30583 steps), i.e.
+about (the block's scaling magnitude) / 60000.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+XMAX = np.float32(30583.0)
+INV_XMAX = np.float32(1.0) / XMAX
+
+
+def encode_block(v: np.ndarray, threshold: float | None = None):
+    """One block (32 fp32 values) -> (effective values, scale s, outlier index
+    or -1, outlier value). Arithmetic in fp32 as the kernel does it."""
+    v = np.asarray(v, dtype=np.float32)
+    a = np.abs(v)
+    amax = np.float32(a.max()) if a.size else np.float32(0)
+    out_i, out_v = -1, np.float32(0)
+    if threshold is not None and amax > 0:
+        i = int(np.argmax(a))  # lowest index among the largest
+        rest = a.copy()
+        rest[i] = 0
+        amax2 = np.float32(rest.max())
+        if amax > np.float32(threshold) * amax2:
+            out_i, out_v = i, v[i]
+            v = v.copy()
+            v[i] = 0
+            amax = amax2
+    if not np.isfinite(amax) or not np.isfinite(v).all():
+        return np.full(v.shape, np.nan, np.float32), np.float32(np.nan), -1, np.float32(0)
+    inv = XMAX / amax if amax > 0 else np.float32(0)
+    x = np.clip(np.rint(v * np.float32(inv)), -30583, 30583).astype(np.float32)
+    s = np.float32(amax * INV_XMAX)
+    eff = (s * x).astype(np.float32)
+    if out_i >= 0:
+        eff[out_i] = out_v
+    return eff, s, out_i, out_v
+
+
+def effective_row(x: np.ndarray, threshold: float | None = None) -> np.ndarray:
+    """The activation row a kernel multiplies, block by block (len(x) a
+    multiple of 32)."""
+    x = np.asarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    for b in range(0, x.size, 32):
+        out[b:b + 32] = encode_block(x[b:b + 32], threshold)[0]
+    return out
+
+
+def block_bound(x: np.ndarray, threshold: float | None = None) -> np.ndarray:
+    """Per-value error bound |v - eff|: 0.51 s (s the block's scale), 0 for
+    an extracted outlier."""
+    x = np.asarray(x, dtype=np.float32)
+    out = np.empty(x.size, np.float64)
+    for b in range(0, x.size, 32):
+        blk = x[b:b + 32]
+        eff, s, oi, _ = encode_block(blk, threshold)
+        out[b:b + 32] = 0.51 * float(s) + 1e-45
+        if oi >= 0:
+            out[b + oi] = 0.0
+    return out
