@@ -80,11 +80,33 @@ def f32_from_fp16(bits) -> np.ndarray:
     return np.array([lib().orc_f32_from_fp16(int(v)) for v in b], dtype=np.float32)
 
 
-def dequant_rows(fmt, gguf: np.ndarray, rows: int, cols: int) -> np.ndarray:
+def _row_split(g: np.ndarray, rows: int, threads: int, call) -> None:
+    """Run call(r0, r1, row_bytes) over contiguous row ranges on `threads`
+    threads (the C routines work row by row and release the GIL)."""
+    if rows <= 0 or g.size % rows:
+        raise ValueError("GGUF bytes must hold whole rows")
+    row_bytes = g.size // rows
+    threads = max(1, min(int(threads), rows))
+    edges = [rows * t // threads for t in range(threads + 1)]
+    if threads == 1:
+        call(0, rows, row_bytes)
+        return
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(threads) as pool:
+        for f in [pool.submit(call, edges[t], edges[t + 1], row_bytes) for t in range(threads)]:
+            f.result()
+
+
+def dequant_rows(fmt, gguf: np.ndarray, rows: int, cols: int, threads: int = 1) -> np.ndarray:
     g = _as_bytes(gguf)
     out = np.empty(rows * cols, np.float32)
-    rc = lib().orc_dequant_rows(_fmt(fmt), g.ctypes.data, rows, cols, out.ctypes.data)
-    assert rc == 0, rc
+
+    def run(r0, r1, row_bytes):
+        rc = lib().orc_dequant_rows(_fmt(fmt), g.ctypes.data + r0 * row_bytes, r1 - r0, cols,
+                                    out.ctypes.data + 4 * r0 * cols)
+        assert rc == 0, rc
+
+    _row_split(g, rows, threads, run)
     return out.reshape(rows, cols)
 
 
@@ -93,14 +115,19 @@ def dequant_value(fmt, block: np.ndarray, index: int) -> float:
     return lib().orc_dequant_value(_fmt(fmt), b.ctypes.data, index)
 
 
-def matvec_f64(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+def matvec_f64(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 1) -> np.ndarray:
     """x (M, K) float64 -> y (M, N) float64."""
     g = _as_bytes(gguf)
     x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float64)
     m = x2.shape[0]
     y = np.empty((m, rows), np.float64)
-    rc = lib().orc_matvec_f64(_fmt(fmt), g.ctypes.data, rows, cols, x2.ctypes.data, m, cols, y.ctypes.data, rows)
-    assert rc == 0, rc
+
+    def run(r0, r1, row_bytes):
+        rc = lib().orc_matvec_f64(_fmt(fmt), g.ctypes.data + r0 * row_bytes, r1 - r0, cols, x2.ctypes.data, m, cols,
+                                  y.ctypes.data + 8 * r0, rows)
+        assert rc == 0, rc
+
+    _row_split(g, rows, threads, run)
     return y
 
 

@@ -33,7 +33,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import dequant_rows
+from . import dequant_rows, matvec_f64
 
 
 def rmsnorm(x: np.ndarray, scale: np.ndarray, eps: float) -> np.ndarray:
@@ -78,6 +78,60 @@ def _fp16_round(values: np.ndarray) -> np.ndarray:
     return np.asarray(values, dtype=np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
 
 
+def layer_forward(s, mv, attn_norm, ffn_norm, caches, X, pos: int) -> np.ndarray:
+    """One decoder layer at `pos` for each row of X (m residual streams,
+    float64). mv(name, A) multiplies projection `name` ("qkv", "o", "gate",
+    "up", "down") by each row of A and returns the products as rows;
+    caches[j] = (k, v), float64 arrays [kv_heads, > pos, head_dim] of stream j,
+    which receive that stream's key and value at pos. Returns the streams
+    after the layer."""
+    hd, nq, nkv = s.head_dim, s.q_heads, s.kv_heads
+    X = np.atleast_2d(np.asarray(X, dtype=np.float64))
+    QKV = mv("qkv", np.stack([rmsnorm(x, attn_norm, s.eps) for x in X]))
+    A = []
+    for j, qkv in enumerate(QKV):
+        q = rope_neox(qkv[:nq * hd].reshape(nq, hd), pos, s.rope_base)
+        k = rope_neox(qkv[nq * hd:(nq + nkv) * hd].reshape(nkv, hd), pos, s.rope_base)
+        v = qkv[(nq + nkv) * hd:].reshape(nkv, hd)
+        kc, vc = caches[j]
+        kc[:, pos] = _fp16_round(k)
+        vc[:, pos] = _fp16_round(v)
+        A.append(attention(q, kc, vc, pos + 1).reshape(-1))
+    X = X + mv("o", np.stack(A))
+    XN = np.stack([rmsnorm(x, ffn_norm, s.eps) for x in X])
+    return X + mv("down", silu_mul(mv("gate", XN), mv("up", XN)))
+
+
+def f64_cache(bits: np.ndarray, max_ctx: int) -> np.ndarray:
+    """fp16 bits [kv_heads, n, head_dim] -> float64 [kv_heads, max_ctx, head_dim], zero past n."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    out = np.zeros((bits.shape[0], max_ctx, bits.shape[2]))
+    out[:, :bits.shape[1]] = bits.view(np.float16).astype(np.float64)
+    return out
+
+
+class QuantLayer:
+    """One layer's projections as stored (GGUF blocks), multiplied by the
+    oracle's f64 row products on `threads` threads, without dequantizing the
+    whole matrix: the checker of decoders too large to hold as float64."""
+
+    def __init__(self, s, t, threads: int = 1):
+        fmts = getattr(t, "fmts", None) or {}
+        f = lambda name: fmts.get(name, s.proj_fmt)  # noqa: E731
+        qkv_rows = (s.q_heads + 2 * s.kv_heads) * s.head_dim
+        parts = getattr(t, "qkv_parts", None) or [(f("qkv"), qkv_rows, t.qkv)]
+        self.parts = {"qkv": [(fmt, rows, s.d, blocks) for fmt, rows, blocks in parts],
+                      "o": [(f("o"), s.d, s.d, t.o)], "gate": [(f("gate"), s.ffn, s.d, t.gate)],
+                      "up": [(f("up"), s.ffn, s.d, t.up)], "down": [(f("down"), s.d, s.ffn, t.down)]}
+        self.attn_norm = np.asarray(t.attn_norm, dtype=np.float64)
+        self.ffn_norm = np.asarray(t.ffn_norm, dtype=np.float64)
+        self.threads = threads
+
+    def __call__(self, name: str, A: np.ndarray) -> np.ndarray:
+        return np.hstack([matvec_f64(fmt, blocks, rows, cols, A, self.threads)
+                          for fmt, rows, cols, blocks in self.parts[name]])
+
+
 class DecoderReference:
     """The decoder's weights dequantized once; `step` advances one token.
 
@@ -117,31 +171,14 @@ class DecoderReference:
                 "up": deq(f("up"), t.up, s.ffn, s.d),
                 "down": deq(f("down"), t.down, s.d, s.ffn),
             })
-        self.k, self.v = [], []
-        for kc, vc in caches:
-            n = kc.shape[1]
-            kf = np.zeros((s.kv_heads, max_ctx, s.head_dim))
-            vf = np.zeros((s.kv_heads, max_ctx, s.head_dim))
-            kf[:, :n] = np.asarray(kc, dtype=np.uint16).view(np.float16).astype(np.float64)
-            vf[:, :n] = np.asarray(vc, dtype=np.uint16).view(np.float16).astype(np.float64)
-            self.k.append(kf)
-            self.v.append(vf)
+        self.k = [f64_cache(kc, max_ctx) for kc, _ in caches]
+        self.v = [f64_cache(vc, max_ctx) for _, vc in caches]
 
     def step(self, token: int, pos: int) -> np.ndarray:
         """Logits of the token at `pos` (its key and value join the caches)."""
         s = self.shape
-        hd, nq, nkv = s.head_dim, s.q_heads, s.kv_heads
         x = self.embed[token % s.vocab].copy()
         for i, L in enumerate(self.layers):
-            xn = rmsnorm(x, L["attn_norm"], s.eps)
-            qkv = L["qkv"] @ xn
-            q = rope_neox(qkv[:nq * hd].reshape(nq, hd), pos, s.rope_base)
-            k = rope_neox(qkv[nq * hd:(nq + nkv) * hd].reshape(nkv, hd), pos, s.rope_base)
-            v = qkv[(nq + nkv) * hd:].reshape(nkv, hd)
-            self.k[i][:, pos] = _fp16_round(k)
-            self.v[i][:, pos] = _fp16_round(v)
-            a = attention(q, self.k[i], self.v[i], pos + 1).reshape(-1)
-            x = x + L["o"] @ a
-            xn = rmsnorm(x, L["ffn_norm"], s.eps)
-            x = x + L["down"] @ silu_mul(L["gate"] @ xn, L["up"] @ xn)
+            x = layer_forward(s, lambda name, A, L=L: A @ L[name].T, L["attn_norm"], L["ffn_norm"],
+                              [(self.k[i], self.v[i])], x, pos)[0]
         return self.head @ rmsnorm(x, self.out_norm, s.eps)

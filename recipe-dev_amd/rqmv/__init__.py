@@ -186,11 +186,7 @@ class DeviceBuffer:
         _hip(lib().hip.hipMemcpy(self.ptr, arr.ctypes.data, arr.nbytes, _H2D), "hipMemcpy H2D")
 
     def download(self, dtype, count: int | None = None) -> np.ndarray:
-        dtype = np.dtype(dtype)
-        n = self.nbytes // dtype.itemsize if count is None else count
-        out = np.empty(n, dtype=dtype)
-        _hip(lib().hip.hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, _D2H), "hipMemcpy D2H")
-        return out
+        return _download(self.ptr, self.nbytes, dtype, count)
 
     def fill_zero(self):
         _hip(lib().hip.hipMemset(self.ptr, 0, self.nbytes), "hipMemset")
@@ -225,6 +221,20 @@ class BufferView:
 
     def __init__(self, parent: DeviceBuffer, ptr: int, nbytes: int):
         self.parent, self.ptr, self.nbytes = parent, ptr, nbytes
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        return _download(self.ptr, self.nbytes, dtype, count)
+
+
+def _download(ptr: int, nbytes: int, dtype, count: int | None) -> np.ndarray:
+    """`count` values of `dtype` (all that fit when None) copied from device memory."""
+    dtype = np.dtype(dtype)
+    n = nbytes // dtype.itemsize if count is None else int(count)
+    if not 0 <= n * dtype.itemsize <= nbytes:
+        raise ValueError(f"{n} values of {dtype} do not fit in {nbytes} bytes")
+    out = np.empty(n, dtype=dtype)
+    _hip(lib().hip.hipMemcpy(out.ctypes.data, ptr, out.nbytes, _D2H), "hipMemcpy D2H")
+    return out
 
 
 class Stream:

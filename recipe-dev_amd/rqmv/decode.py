@@ -141,6 +141,7 @@ class DecodeModel:
         self.argmax_ws = argmax_workspace()
         self.rope = rope_table(s.head_dim, s.rope_base, self.max_ctx)
         self._pos: int | None = None  # host count of the position (set_position, step, replay)
+        self._hidden: DeviceBuffer | None = None  # the buffer the head's prologue writes the stream to
 
     # ---------------------------------------------------------------- setup
     def set_layer(self, index: int, t: LayerTensors):
@@ -217,16 +218,21 @@ class DecodeModel:
                                "token window is outside the placement capacity")
 
     # ----------------------------------------------------------------- step
-    def enqueue_step(self, stream: Stream | None = None):
+    def enqueue_step(self, stream: Stream | None = None, layers: int | None = None):
         """Enqueue one decode step on `stream` (capturable: no allocation, no
-        host synchronisation)."""
+        host synchronisation). `layers` < the decoder's depth runs only the
+        first `layers` layers before the head (an early exit); read_hidden()
+        then returns the stream that layer `layers` would take as input."""
         s = self.shape
         if any(layer is None for layer in self.layers):
             raise RuntimeError("every layer must be set before a step")
+        depth = s.layers if layers is None else int(layers)
+        if not 1 <= depth <= s.layers:
+            raise ValueError(f"layers must be 1..{s.layers}, got {layers}")
         xs = self.xs
         embed_row(self.embed, s.vocab, s.d, self.token, xs[0], stream)
         cur, pending = 0, None  # pending: the down projection not yet added to the stream
-        for i, L in enumerate(self.layers):
+        for i, L in enumerate(self.layers[:depth]):
             (w0, y0), rest = L["qkv"][0], L["qkv"][1:]
             if pending is None:
                 matvec_fused(w0, xs[cur], y0, EPI_PLAIN, L["attn_norm"], s.eps, stream=stream)
@@ -245,6 +251,7 @@ class DecodeModel:
             pending = self.y_f
         matvec_fused(self.head, xs[cur], self.logits, EPI_PLAIN, self.out_norm, s.eps, pending, xs[1 - cur],
                      stream=stream)
+        self._hidden = xs[1 - cur]
         argmax(self.logits, s.vocab, self.token, self.argmax_ws, stream)
         advance(self.pos, stream)
 
@@ -259,6 +266,14 @@ class DecodeModel:
     def read_token(self) -> int:
         self._check_inside()
         return int(self.token.download(np.int32, 1)[0])
+
+    def read_hidden(self) -> np.ndarray:
+        """The residual stream after the last layer of the latest step (the
+        head's input, before its norm)."""
+        if self._hidden is None:
+            raise RuntimeError("no step has been enqueued")
+        self._check_inside()
+        return self._hidden.download(np.float32, self.shape.d)
 
     def read_position(self) -> int:
         return int(self.pos.download(np.int32, 1)[0])

@@ -125,3 +125,36 @@ def test_layer_variants_keep_block_scales_and_differ():
         assert np.array_equal(v.reshape(-1, 144)[:, :4], a.reshape(-1, 144)[:, :4])
     assert not np.array_equal(v1, v2)
     assert np.array_equal(synth.layer_variant("q4_k", v1, 1, "t.l0"), a)  # an involution
+
+
+def test_streaming_layers_equal_the_dequantized_decoder():
+    """The streaming form used for decoders too large to dequantize whole
+    (QuantLayer: the oracle's f64 row products on threads, several streams per
+    layer) equals the dequantized decoder's step, with a Q4_K_M-style QKV of
+    mixed formats in one layer."""
+    import oracle
+    s = DecoderShape(layers=2, d=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=64)
+    D = synth.DecoderSynth(s, seed=8, norm_std=0.2)
+    layers = [D.layer(i) for i in range(s.layers)]
+    t = layers[1]
+    q_rows, kv_rows = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
+    v6 = synth.weights("q6_k", kv_rows, s.d, seed=4)
+    qkv = t.qkv.reshape(q_rows + 2 * kv_rows, -1)
+    layers[1] = LayerTensors(t.attn_norm, None, t.o, t.ffn_norm, t.gate, t.up, t.down,
+                             qkv_parts=[("q4_k", q_rows, qkv[:q_rows].reshape(-1)),
+                                        ("q4_k", kv_rows, qkv[q_rows:q_rows + kv_rows].reshape(-1)),
+                                        ("q6_k", kv_rows, v6)])
+    embed, caches, ctx = D.embed()[: s.vocab], [D.cache(i, 6) for i in range(s.layers)], 6
+    R = ref.DecoderReference(s, embed, D.out_norm(), D.head(), layers, caches, 8)
+    want = R.step(5, ctx)
+    x = np.stack([embed[5].astype(np.float64)] * 2)
+    for i in range(s.layers):
+        L = ref.QuantLayer(s, layers[i], threads=3)
+        c = [(ref.f64_cache(caches[i][0], 8), ref.f64_cache(caches[i][1], 8)) for _ in range(2)]
+        x = ref.layer_forward(s, L, L.attn_norm, L.ffn_norm, c, x, ctx)
+        assert np.array_equal(c[0][0], c[1][0]) and np.array_equal(c[0][0][:, ctx], R.k[i][:, ctx])
+    head = oracle.matvec_f64(s.head_fmt, D.head(), s.vocab, s.d, ref.rmsnorm(x[0], D.out_norm(), s.eps), 2)[0]
+    assert np.array_equal(x[0], x[1])
+    # the dequantized decoder holds each weight rounded to fp32, the row
+    # products the f64 value of the decoder's formula: 1e-7 covers that
+    assert np.allclose(head, want, rtol=1e-7, atol=1e-7 * np.abs(want).max())
