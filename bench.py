@@ -51,15 +51,58 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def traffic_from_profiles(workload, m):
-    """HBM bytes per launch measured by rocprofv3 counters, if recorded."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+def _profile_entry(name, key):
+    """One workload's entry of a measured-counter file under profiles/, if recorded."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     try:
-        return json.load(open(path)).get(f"{workload}_m{m}")
+        return json.load(open(path)).get(key)
     except (OSError, ValueError):
         return None
+
+
+def traffic_from_profiles(workload, m):
+    """HBM bytes per launch measured by rocprofv3 counters, if recorded."""
+    return _profile_entry("traffic.json", f"{workload}_m{m}")
+
+
+def rocprof_roofline(workload, m, alg_bytes):
+    """The dominant kernel's mean duration in a committed rocprofv3 kernel
+    trace of the same bench command, and the roofline fraction it gives: the
+    profiler's dispatch timestamps, beside the live event timing."""
+    e = _profile_entry("kernel_time.json", f"{workload}_m{m}")
+    if not e:
+        return None
+    gbs = alg_bytes / (e["mean_us"] * 1e-6) / 1e9
+    return {"kernel": e["kernel"], "mean_us": e["mean_us"], "achieved": round(gbs, 2),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "source": e["source"]}
+
+
+def host_cpu():
+    """Threads the CPU baseline runs on, and the host it ran on. recipe's CPU
+    backend runs one worker per host core (cpu-worker-threads = 0, Cargo.toml:52;
+    recipe.rs:28613-28616): every core in this process's affinity mask, capped
+    by OMP_NUM_THREADS where the host grants a job a share of its cores."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    threads = affinity
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        threads = min(threads, int(share))
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return threads, {"nproc": os.cpu_count(), "affinity": affinity, "omp_num_threads": share or None,
+                     "cpu_model": model}
 
 
 def stream_copy(achieved_gbs, nbytes=1 << 30, reps=20):
@@ -92,23 +135,20 @@ def stream_copy(achieved_gbs, nbytes=1 << 30, reps=20):
 def cpu_baseline(fmt, rows, cols, x32, seconds, weights_bytes, alg_bytes):
     import oracle
 
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+    cores, host = host_cpu()
     # the same matvec, repeated over the full weight for ~`seconds`
     runs, t0 = 0, time.perf_counter()
     while True:
-        oracle.matvec_recipe_f32(fmt, weights_bytes, rows, cols, x32, threads=cores)
+        oracle.matvec_recipe_fast(fmt, weights_bytes, rows, cols, x32, threads=cores)
         runs += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
     per = el / runs
-    return {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+    return {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port", **host,
             "sample": f"{runs} full {fmt} {cols}->{rows} matvecs (M={x32.shape[0]}) in {el:.1f} s, "
-                      f"{per * 1e3:.2f} ms each, fp32 recipe-order restatement, {cores} threads"}
+                      f"{per * 1e3:.2f} ms each: recipe's fp32 float path (exact fp32 weights, fp32 fma chain per "
+                      f"block, eight rows per SIMD lane group) restated in C, {cores} threads"}
 
 
 def copy_calibration(mb, steps):
@@ -225,27 +265,87 @@ def moe_bench(args):
                    "positions_per_s": round(m / ms_per_step * 1e3, 1),
                    "launches_per_step": 3, "weight_sets": 2, "tokens": 16, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                     "note": "whole step (three launches) from the graph replay"},
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("moe_c4", m),
+                     "note": "whole step (three launches) from the graph replay; traffic sums the three kernels"},
         "stream_copy": stream_copy(value),
         "parity_rel_l2": rel,
     }
     if not args.no_cpu:
-        import oracle
-
-        router, gate, up, down, sg, gs, us, ds = hosts[0]
-        runs, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            x64 = synth.fp16_to_f32(tokens[runs % 16]).astype(np.float64)
-            oracle.moe_f64("q4_k", d, E, top, H, router.view(np.uint16), gate, up, down, x64, scoring=0,
-                           renormalize=True, hidden_shared=H, shared_gate_bits=sg.view(np.uint16), gate_sh=gs,
-                           up_sh=us, down_sh=ds)
-            runs += 1
-        el = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": round(alg_bytes * runs / el / 1e9, 3), "unit": "GB/s", "cores": 1,
-                               "kind": "port", "sample": f"{runs} moe steps in {el:.1f} s (f64 restatement, one thread)"}
+        out["cpu_baseline"] = moe_cpu_baseline(hosts[0], tokens, d, E, top, H, alg_bytes, args.cpu_seconds)
     print(json.dumps(out), flush=True)
     graph.close()
+
+
+def moe_cpu_baseline(host, tokens, d, E, top, H, alg_bytes, seconds):
+    """recipe's CPU path for the gguf_moe step at one position: the fp16
+    router in fp32, top-k, then each selected expert's and the shared
+    expert's gate and up rows, SiLU-GLU and down rows on the fp32 float path
+    (oracle.matvec_recipe_fast), experts and their row halves spread over the
+    CPU share's threads; one step checked against the f64 oracle first."""
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+
+    from rqmv import synth
+
+    cores, hostinfo = host_cpu()
+    router, gate, up, down, sg, gs, us, ds = host
+    rw = synth.fp16_to_f32(router.view(np.uint16)).reshape(E, d)
+    sgw = synth.fp16_to_f32(sg.view(np.uint16)).reshape(d)
+    eb_up, eb_down = H * d // 256 * 144, d * H // 256 * 144
+    split = max(1, cores // (top + 1))
+
+    def silu(v):
+        return v * (np.float32(0.5) * (np.tanh(np.float32(0.5) * v) + np.float32(1.0)))
+
+    def rows_of(n):
+        return [(n * c // split, n * (c + 1) // split) for c in range(split)]
+
+    def step(pool, x):
+        logits = (rw @ x).astype(np.float64)
+        wts = oracle.topk(logits, top, scoring=0, renormalize=True)
+        chosen = [int(e) for e in np.nonzero(wts)[0]]
+        banks = [(gate[e * eb_up:(e + 1) * eb_up], up[e * eb_up:(e + 1) * eb_up], down[e * eb_down:(e + 1) * eb_down])
+                 for e in chosen] + [(gs, us, ds)]
+        hidden = [np.empty(H, np.float32) for _ in banks]
+
+        def glu(j, r0, r1):
+            g, u, _ = banks[j]
+            rb = d // 256 * 144
+            a = oracle.matvec_recipe_fast("q4_k", g[r0 * rb:r1 * rb], r1 - r0, d, x)[0]
+            b = oracle.matvec_recipe_fast("q4_k", u[r0 * rb:r1 * rb], r1 - r0, d, x)[0]
+            hidden[j][r0:r1] = silu(a) * b
+
+        list(pool.map(lambda t: glu(*t), [(j, r0, r1) for j in range(len(banks)) for r0, r1 in rows_of(H)]))
+        outs = [np.empty(d, np.float32) for _ in banks]
+
+        def dn(j, r0, r1):
+            rb = H // 256 * 144
+            outs[j][r0:r1] = oracle.matvec_recipe_fast("q4_k", banks[j][2][r0 * rb:r1 * rb], r1 - r0, H, hidden[j])[0]
+
+        list(pool.map(lambda t: dn(*t), [(j, r0, r1) for j in range(len(banks)) for r0, r1 in rows_of(d)]))
+        y = np.zeros(d, np.float32)
+        for j, e in enumerate(chosen):
+            y += np.float32(wts[e]) * outs[j]
+        gate_w = np.float32(1.0) / (np.float32(1.0) + np.exp(-np.float32(sgw @ x)))
+        return y + gate_w * outs[-1]
+
+    with ThreadPoolExecutor(cores) as pool:
+        x0 = synth.fp16_to_f32(tokens[0])
+        got = step(pool, x0)
+        ref, _ = oracle.moe_f64("q4_k", d, E, top, H, router.view(np.uint16), gate, up, down, x0.astype(np.float64),
+                                scoring=0, renormalize=True, hidden_shared=H, shared_gate_bits=sg.view(np.uint16),
+                                gate_sh=gs, up_sh=us, down_sh=ds)
+        rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+        runs, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            step(pool, synth.fp16_to_f32(tokens[runs % 16]))
+            runs += 1
+        el = time.perf_counter() - t0
+    return {"value": round(alg_bytes * runs / el / 1e9, 3), "unit": "GB/s", "cores": min(cores, (top + 1) * split),
+            "kind": "port", **hostinfo,
+            "sample": f"{runs} moe steps in {el:.1f} s ({el / runs * 1e3:.2f} ms each): fp32 router, top-8, the "
+                      f"9 experts' products on recipe's fp32 float path, {(top + 1) * split} tasks per phase over "
+                      f"{cores} threads; rel-L2 {rel:.1e} against the f64 oracle"}
 
 
 def decode_bench(args):
@@ -325,14 +425,15 @@ def decode_bench(args):
                    "launches_per_token": 1 + 6 * s.layers + 4, "activations": "f32", "kv_cache": "f16",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "note": "whole token (every launch of the step) from graph replays"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("decode_c5", 1),
+                     "note": "whole token (every launch of the step) from graph replays; traffic sums every "
+                             "kernel of one token"},
         "stream_copy": stream_copy(achieved),
     }
     if not args.no_cpu:
         import oracle
 
-        cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+        cores, hostinfo = host_cpu()
         # recipe's CPU float path on layer 0's four projections, timed per layer
         # and scaled to 32 layers, plus the head, plus f64 attention over one
         # layer's cache scaled to 32 layers
@@ -343,14 +444,14 @@ def decode_bench(args):
         runs = 0
         while time.perf_counter() - t0 < args.cpu_seconds * 0.6:
             for k in ("qkv", "o", "gate", "up", "down"):
-                oracle.matvec_recipe_f32(s.proj_fmt, getattr(layer0, k), rows[k], xs[k],
-                                         rng.standard_normal(xs[k]).astype(np.float32), threads=cores)
+                oracle.matvec_recipe_fast(s.proj_fmt, getattr(layer0, k), rows[k], xs[k],
+                                          rng.standard_normal(xs[k]).astype(np.float32), threads=cores)
             runs += 1
         layer_s = (time.perf_counter() - t0) / runs
         head = D.head()
         t0 = time.perf_counter()
-        oracle.matvec_recipe_f32(s.head_fmt, head, s.vocab, s.d, rng.standard_normal(s.d).astype(np.float32),
-                                 threads=cores)
+        oracle.matvec_recipe_fast(s.head_fmt, head, s.vocab, s.d, rng.standard_normal(s.d).astype(np.float32),
+                                  threads=cores)
         head_s = time.perf_counter() - t0
         from oracle import decode as oref
         kc, vc = D.cache(0, ctx)
@@ -360,7 +461,7 @@ def decode_bench(args):
         attn_s = time.perf_counter() - t0
         token_s = s.layers * (layer_s + attn_s) + head_s
         out["cpu_baseline"] = {
-            "value": round(1.0 / token_s, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "value": round(1.0 / token_s, 4), "unit": "tok/s", "cores": cores, "kind": "port", **hostinfo,
             "sample": f"layer-0 projections x{runs} ({layer_s * 1e3:.0f} ms/layer, recipe fp32 float path), head "
                       f"once ({head_s * 1e3:.0f} ms), attention over 4096 positions once ({attn_s * 1e3:.0f} ms, "
                       f"numpy), scaled to 32 layers; {cores} threads"}
@@ -442,17 +543,28 @@ def int8_bench(args):
     if not args.no_cpu:
         import oracle
 
-        runs, t0 = 0, time.perf_counter()
-        while True:
-            oracle.int8_matvec(fmt, w, rows, cols, x32, step)
-            runs += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds:
-                break
+        from concurrent.futures import ThreadPoolExecutor
+
+        cores, hostinfo = host_cpu()
+        rb = w.nbytes // rows
+        chunks = [(rows * c // cores, rows * (c + 1) // cores) for c in range(cores)]
+
+        def part(r0, r1):
+            return oracle.int8_matvec(fmt, w[r0 * rb:r1 * rb], r1 - r0, cols, x32, step)
+
+        with ThreadPoolExecutor(cores) as pool:
+            runs, t0 = 0, time.perf_counter()
+            while True:
+                list(pool.map(lambda c: part(*c), chunks))
+                runs += 1
+                el = time.perf_counter() - t0
+                if el >= args.cpu_seconds:
+                    break
         per = el / runs
-        out["cpu_baseline"] = {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                               "sample": f"{runs} full int(8) matvecs in {el:.1f} s, {per * 1e3:.2f} ms each, "
-                                         f"oracle restatement, one thread"}
+        out["cpu_baseline"] = {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s", "cores": cores,
+                               "kind": "port", **hostinfo,
+                               "sample": f"{runs} full int(8) matvecs in {el:.1f} s, {per * 1e3:.2f} ms each: the "
+                                         f"oracle's restatement of the int(8) sum, rows split over {cores} threads"}
     print(json.dumps(out), flush=True)
     graph.close()
 
@@ -583,12 +695,22 @@ def main():
                    "activations": xdt, "accumulate": "f32", "weight_copies": copies,
                    "bytes_per_step": alg_bytes, "flops_per_step": flops, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.workload, m)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.workload, m),
+                     "timing": "mean of per-dispatch start/stop events recorded by each launch itself "
+                               "(hipExtLaunchKernelGGL), live in this run",
+                     "rocprof": rocprof_roofline(args.workload, m, alg_bytes)},
         "stream_copy": stream_copy(achieved),
         "kernel_us": round(ker_ms * 1e3, 3),
+        "kernel_us_median": round(float(np.median(ker)) * 1e3, 3),
         "gflops": round(flops / (ker_ms * 1e-3) / 1e9, 1),
         "parity_rel_l2": rel,
     }
+    mfma = _profile_entry("mfma_util.json", f"{args.workload}_m{m}")
+    if mfma:
+        out["mfma"] = {"util": mfma["mfma_util"], "tflops_under_counters": mfma["tflops"],
+                       "kernel_us_under_counters": mfma["kernel_us_under_counters"],
+                       "source": mfma.get("source", "profiles/mfma_util.json"),
+                       "definition": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)"}
     if not args.no_cpu:
         log("bench: cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(fmt, rows, cols, x32, args.cpu_seconds, w, alg_bytes)

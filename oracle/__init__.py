@@ -43,6 +43,8 @@ def lib():
         L.orc_matvec_f64.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int64, c_void_p, c_int64]
         L.orc_matvec_recipe_f32.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int64, c_void_p,
                                             c_int64, c_int]
+        L.orc_matvec_recipe_fast.argtypes = [c_int, c_void_p, c_int64, c_int64, c_void_p, c_int, c_int64, c_void_p,
+                                             c_int64, c_int]
         L.orc_topk.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_void_p]
         L.orc_topk_biased.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]
         L.orc_activation.argtypes = [c_int, c_double, c_double, c_void_p]
@@ -139,6 +141,19 @@ def matvec_recipe_f32(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray
     y = np.empty((m, rows), np.float32)
     rc = lib().orc_matvec_recipe_f32(_fmt(fmt), g.ctypes.data, rows, cols, x2.ctypes.data, m, cols, y.ctypes.data,
                                      rows, threads)
+    assert rc == 0, rc
+    return y
+
+
+def matvec_recipe_fast(fmt, gguf: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """matvec_recipe_f32's products bit for bit, on recipe's compiled schedule
+    (the timed CPU baseline)."""
+    g = _as_bytes(gguf)
+    x2 = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    m = x2.shape[0]
+    y = np.empty((m, rows), np.float32)
+    rc = lib().orc_matvec_recipe_fast(_fmt(fmt), g.ctypes.data, rows, cols, x2.ctypes.data, m, cols, y.ctypes.data,
+                                      rows, threads)
     assert rc == 0, rc
     return y
 

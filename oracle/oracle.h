@@ -18,6 +18,7 @@
  *        algebra of evidence/2026-10-10-m60-p2p/bench.rs:193-226.
  *   orc_matvec_f64     brute force on tiny shapes, linearity, scale-by-2.
  *   orc_matvec_recipe_f32  within 1e-6 of orc_matvec_f64, suite.rs known answer.
+ *   orc_matvec_recipe_fast bit-identical to orc_matvec_recipe_f32.
  *   orc_topk           brute force with a stable sort and closed-form softmax.
  *   orc_moe_f64        a numpy composition of the block on tiny shapes.
  *   orc_q4k_q81_reference  is itself the bench.rs algorithm (a second,
@@ -60,6 +61,13 @@ int orc_matvec_f64(int format, const uint8_t* bytes, int64_t rows, int64_t cols,
  * split contiguously over that many POSIX threads (the CPU backend's workers). */
 int orc_matvec_recipe_f32(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const float* x, int m_count,
                           int64_t ldx, float* y, int64_t ldy, int threads);
+
+/* The same products as orc_matvec_recipe_f32, bit for bit, on recipe's
+ * compiled schedule (block headers decoded once per block, eight rows per SIMD
+ * lane group, rows split over `threads` POSIX threads): the timed CPU
+ * baseline (recipe_cpu.c). Q4_0, Q8_0, Q4_K and Q6_K. */
+int orc_matvec_recipe_fast(int format, const uint8_t* bytes, int64_t rows, int64_t cols, const float* x, int m_count,
+                           int64_t ldx, float* y, int64_t ldy, int threads);
 
 /* Top-k routing of one position (amd-nv-cpu.ll:4653-4716): dense weights[E],
  * zero off the kept set. scoring 0 = softmax, 1 = sigmoid. orc_topk_biased

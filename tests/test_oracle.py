@@ -262,6 +262,21 @@ def test_matvec_recipe_f32_close_to_f64(fmt):
 
 
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("rows,m,threads", [(1, 1, 1), (13, 2, 1), (77, 3, 4), (300, 1, 7)])
+def test_matvec_recipe_fast_bit_identical(fmt, rows, m, threads):
+    """The timed CPU baseline (recipe's compiled schedule: eight rows per lane
+    group, headers decoded once per block) gives the per-value path's bits,
+    ragged row groups and extreme activations included."""
+    cols = 768
+    rng = np.random.default_rng(rows * 10 + m)
+    w = synth.weights(fmt, rows, cols, seed=rows + m)
+    x = (rng.standard_normal((m, cols)) * 10.0 ** rng.integers(-3, 4, (m, cols))).astype(np.float32)
+    want = oracle.matvec_recipe_f32(fmt, w, rows, cols, x)
+    got = oracle.matvec_recipe_fast(fmt, w, rows, cols, x, threads=threads)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q4_k", "q6_k"])
 def test_matvec_scales_exactly_with_block_scale(fmt):
     """Doubling every fp16 block scale (exponent + 1) doubles y exactly."""
     rows, cols = 16, 512
