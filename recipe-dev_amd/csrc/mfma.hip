@@ -1,8 +1,87 @@
 // Small-M quantized products on the matrix cores: launch planning and the
 // fp16-activation kernels (the kernels themselves are in mfma_impl.h).
 #include "mfma_impl.h"
+#include "mfma_rt.h"
 
 namespace rq {
+
+// ---- streaming form (mfma_rt.h) ----
+template <int FMT, int RB, int NT, int WR, int WK>
+static hipError_t launch_rt_one(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
+                                hipEvent_t ev1) {
+    using C = RtCfg<FMT, RB, NT, WR, WK>;
+    const int total_steps = (p.P.nch + C::CPS - 1) / C::CPS;
+    const int spw = (total_steps + WK - 1) / WK;
+    const int quads = spw * C::CPS / 4;
+    const size_t lds = (size_t)C::lds_bytes(quads);
+    if (quads > kRtMaxQuads || lds > 160 * 1024) return hipErrorNotSupported;
+    auto kernel = matvec_mfma_rt<FMT, RB, NT, WR, WK>;
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const int64_t tiles = (p.rows + 15) / 16;
+    const int grid = (int)((tiles + WR - 1) / WR);
+    if (ev0 || ev1)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WR * WK), (uint32_t)lds, stream, ev0, ev1, 0u, p, M, x_bytes,
+                              spw);
+    else
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WR * WK), lds, stream, p, M, x_bytes, spw);
+    return hipGetLastError();
+}
+
+// LDS of a launch shape, for choosing the step (0 if the K range does not fit).
+template <int FMT, int RB, int NT, int WR, int WK>
+static size_t rt_lds(const MvParams& p) {
+    using C = RtCfg<FMT, RB, NT, WR, WK>;
+    const int total_steps = (p.P.nch + C::CPS - 1) / C::CPS;
+    const int quads = (total_steps + WK - 1) / WK * C::CPS / 4;
+    return quads > kRtMaxQuads ? 0 : (size_t)C::lds_bytes(quads);
+}
+
+template <int FMT, int NT, int WR, int WK>
+static hipError_t launch_rt_w(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
+                              hipEvent_t ev1) {
+    // whole 128-byte runs per row (RB = 8) while two workgroups still fit a CU
+    const char* env = getenv("RQMV_RT_RB");
+    const int want = env && *env ? atoi(env) : 0;
+    if constexpr (NT == 1 && WR >= 2 && FMT != Q6_K) {  // (the others need too many registers)
+        const size_t l8 = rt_lds<FMT, 8, NT, WR, WK>(p);
+        if (want != 16 && l8 && (want == 8 || l8 <= 80 * 1024))
+            return launch_rt_one<FMT, 8, NT, WR, WK>(p, M, x_bytes, stream, ev0, ev1);
+    }
+    (void)want;
+    return launch_rt_one<FMT, 16, NT, WR, WK>(p, M, x_bytes, stream, ev0, ev1);
+}
+
+// Workgroup shape: four row tiles sharing each activation window when there
+// are tiles enough to give every CU several waves, else split K.
+template <int FMT, int NT>
+static hipError_t launch_rt(const MvParams& p, int M, uint32_t x_bytes, int cus, hipStream_t stream, hipEvent_t ev0,
+                            hipEvent_t ev1) {
+    const int64_t tiles = (p.rows + 15) / 16;
+    const char* env = getenv("RQMV_RT_SHAPE");  // "41", "22" or "14" (WR, WK) for tuning
+    // (measured: two K ranges beat four up to K ranges of 4096 weights; past
+    // that, four)
+    int shape = env && *env ? atoi(env) : (tiles >= (int64_t)6 * cus ? 41 : p.K > 8192 ? 14 : 22);
+    // split K four ways stages four activation windows per workgroup: for two
+    // tiles of 32-weight blocks of 64-weight chunks that is too many registers
+    if (NT == 2 && FMT != Q8_0 && shape == 14) shape = 22;
+    hipError_t e = hipErrorNotSupported;
+    if (shape == 41) e = launch_rt_w<FMT, NT, 4, 1>(p, M, x_bytes, stream, ev0, ev1);
+    if (e == hipErrorNotSupported && shape >= 22) e = launch_rt_w<FMT, NT, 2, 2>(p, M, x_bytes, stream, ev0, ev1);
+    if constexpr (NT == 1 || FMT == Q8_0)
+        if (e == hipErrorNotSupported) e = launch_rt_w<FMT, NT, 1, 4>(p, M, x_bytes, stream, ev0, ev1);
+    return e;
+}
+
+template <int FMT>
+static hipError_t launch_rt_fmt(const MvParams& p, int M, uint32_t x_bytes, int cus, hipStream_t stream, hipEvent_t ev0,
+                                hipEvent_t ev1) {
+    if (M > 16) return launch_rt<FMT, 2>(p, M, x_bytes, cus, stream, ev0, ev1);
+    return launch_rt<FMT, 1>(p, M, x_bytes, cus, stream, ev0, ev1);
+}
 
 template <int FMT>
 static hipError_t launch_mfma_sk(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
@@ -76,6 +155,21 @@ hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, int 
     const size_t esize = xtype == X_F32 ? 4 : 2;
     const int64_t x_bytes = ((int64_t)(M - 1) * p.ldx + p.K) * (int64_t)esize;
     if (x_bytes >= (int64_t)kOobOffset) return hipErrorInvalidValue;
+    // fp16 activations: the streaming form, unless its scale table does not
+    // fit (K ranges longer than it holds) or RQMV_MFMA_RT=0 asks for the
+    // staged forms below.
+    const char* rt_env = getenv("RQMV_MFMA_RT");
+    if (xtype == X_F16 && !(rt_env && *rt_env == '0')) {
+        hipError_t e = hipErrorInvalidValue;
+        switch (fmt) {
+            case Q4_0: e = launch_rt_fmt<Q4_0>(p, M, (uint32_t)x_bytes, cus, stream, ev0, ev1); break;
+            case Q4_K: e = launch_rt_fmt<Q4_K>(p, M, (uint32_t)x_bytes, cus, stream, ev0, ev1); break;
+            case Q8_0: e = launch_rt_fmt<Q8_0>(p, M, (uint32_t)x_bytes, cus, stream, ev0, ev1); break;
+            case Q6_K: e = launch_rt_fmt<Q6_K>(p, M, (uint32_t)x_bytes, cus, stream, ev0, ev1); break;
+            default: break;
+        }
+        if (e != hipErrorNotSupported) return e;
+    }
     // Split-K for short and medium matrices (each wave re-reads its
     // activations from the caches, which pays off while the stripes are too
     // few to fill the GPU); the shared-staging form for tall ones.

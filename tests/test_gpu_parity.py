@@ -305,9 +305,11 @@ def test_matvec_parity_matrix_core_sizes(gpu, fmt, xdt, m):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("form", ["split-k", "staged-1", "staged-2", "staged-4"])
 def test_matrix_core_forms(gpu, fmt, form, monkeypatch):
-    """Both matrix-core kernels, the split-K one and the staged one at every
-    workgroup size (RQMV_MFMA_SK, RQMV_MFMA_WAVES), with partial row tiles,
-    fp16 and fp32 activations, one and two 16-row tiles."""
+    """Both staged-activation matrix-core kernels, the split-K one and the
+    staged one at every workgroup size (RQMV_MFMA_SK, RQMV_MFMA_WAVES; fp16
+    activations reach them with RQMV_MFMA_RT=0), with partial row tiles, fp16
+    and fp32 activations, one and two 16-row tiles."""
+    monkeypatch.setenv("RQMV_MFMA_RT", "0")
     if form == "split-k":
         monkeypatch.setenv("RQMV_MFMA_SK", "1")
         waves = "4"
@@ -324,6 +326,30 @@ def test_matrix_core_forms(gpu, fmt, form, monkeypatch):
             y = _run_matvec(gpu, W, xh, dt, rows)
             ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
             assert rel_l2(y, ref) <= 2e-4, (fmt, waves, xdt, m)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape,rb", [("41", "8"), ("41", "16"), ("22", "8"), ("22", "16"), ("14", "16")])
+def test_streaming_matrix_core_shapes(gpu, fmt, shape, rb, monkeypatch):
+    """The streaming matrix-core form (fp16 activations) at every workgroup
+    shape (RQMV_RT_SHAPE: four row tiles, two tiles x two K ranges, four K
+    ranges) and step (RQMV_RT_RB: 8 rows x 8 chunks or 16 rows x 4 chunks per
+    load): partial row tiles and workgroups, a last step past the row's end,
+    rows of more than one 64-chunk group, K ranges of unequal length, one and
+    two 16-row activation tiles."""
+    monkeypatch.setenv("RQMV_RT_SHAPE", shape)
+    monkeypatch.setenv("RQMV_RT_RB", rb)
+    kq = fmt in ("q4_k", "q6_k")
+    shapes = [(83, 768), (300, 5376), (37, 256)] if kq else [(83, 800), (300, 4160), (21, 96)]
+    for rows, cols in shapes:
+        w = _weights(fmt, rows, cols, seed=rows + cols + int(shape))
+        W = gpu.Weight(fmt, rows, cols, w)
+        for m in (3, 16, 17, 32):
+            xh, dt, x32 = _x(m, cols, "f16", seed=m + cols)
+            y = _run_matvec(gpu, W, xh, dt, rows)
+            ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+            assert np.isfinite(y).all(), (fmt, shape, rb, rows, cols, m)
+            assert rel_l2(y, ref) <= 2e-4, (fmt, shape, rb, rows, cols, m, rel_l2(y, ref))
 
 
 @pytest.mark.parametrize("fmt", FMTS)
