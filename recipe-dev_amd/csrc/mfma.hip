@@ -9,6 +9,7 @@ namespace rq {
 template <int FMT, int RB, int NT, int WR, int WK>
 static hipError_t launch_rt_one(const MvParams& p, int M, uint32_t x_bytes, hipStream_t stream, hipEvent_t ev0,
                                 hipEvent_t ev1) {
+    const int ys = (M + 16 * NT - 1) / (16 * NT);  // activation row groups (grid y)
     using C = RtCfg<FMT, RB, NT, WR, WK>;
     const int total_steps = (p.P.nch + C::CPS - 1) / C::CPS;
     const int spw = (total_steps + WK - 1) / WK;
@@ -24,10 +25,10 @@ static hipError_t launch_rt_one(const MvParams& p, int M, uint32_t x_bytes, hipS
     const int64_t tiles = (p.rows + 15) / 16;
     const int grid = (int)((tiles + WR - 1) / WR);
     if (ev0 || ev1)
-        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WR * WK), (uint32_t)lds, stream, ev0, ev1, 0u, p, M, x_bytes,
-                              spw);
+        hipExtLaunchKernelGGL(kernel, dim3(grid, ys), dim3(64 * WR * WK), (uint32_t)lds, stream, ev0, ev1, 0u, p, M,
+                              x_bytes, spw);
     else
-        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WR * WK), lds, stream, p, M, x_bytes, spw);
+        hipLaunchKernelGGL(kernel, dim3(grid, ys), dim3(64 * WR * WK), lds, stream, p, M, x_bytes, spw);
     return hipGetLastError();
 }
 
@@ -55,32 +56,62 @@ static hipError_t launch_rt_w(const MvParams& p, int M, uint32_t x_bytes, hipStr
     return launch_rt_one<FMT, 16, NT, WR, WK>(p, M, x_bytes, stream, ev0, ev1);
 }
 
-// Workgroup shape: four row tiles sharing each activation window when there
-// are tiles enough to give every CU several waves, else split K.
+// Workgroup shape (WR row tiles x WK K ranges), from the units of work (row
+// tiles x activation row groups) against the CUs. Measured on MI355X (kernel
+// us, fp16 x):
+//   four row tiles per workgroup once there are units for three waves per CU:
+//     Q4_K 4096->14336 at 32 rows (896 tiles) 34.8 (2 x 2) -> 25.3,
+//   with two K ranges each below six (8 waves per workgroup): the same at
+//     16 rows 19.7 -> 18.6;
+//   split K four ways for long rows on few units: Q4_K 14336->4096 at 16 rows
+//     26.2 (2 x 2: 33.4); with the rows split in two, 2 x 2 (33.3; 4 K ranges
+//     50.9);
+//   Q8_0 with its rows split in two: four row tiles (Q8_0 5120x5120 at 32 rows
+//     24.4 -> 20.5);
+//   else two tiles x two K ranges.
+// RQMV_RT_SHAPE ("41", "42", "22" or "14") overrides it for tuning.
 template <int FMT, int NT>
-static hipError_t launch_rt(const MvParams& p, int M, uint32_t x_bytes, int cus, hipStream_t stream, hipEvent_t ev0,
-                            hipEvent_t ev1) {
-    const int64_t tiles = (p.rows + 15) / 16;
-    const char* env = getenv("RQMV_RT_SHAPE");  // "41", "22" or "14" (WR, WK) for tuning
-    // (measured: two K ranges beat four up to K ranges of 4096 weights; past
-    // that, four)
-    int shape = env && *env ? atoi(env) : (tiles >= (int64_t)6 * cus ? 41 : p.K > 8192 ? 14 : 22);
+static hipError_t launch_rt(const MvParams& p, int M, uint32_t x_bytes, int cus, int ys, hipStream_t stream,
+                            hipEvent_t ev0, hipEvent_t ev1) {
+    const int64_t units = (p.rows + 15) / 16 * ys;
+    const char* env = getenv("RQMV_RT_SHAPE");
+    int shape;
+    if (env && *env) shape = atoi(env);
+    else if (units >= (int64_t)6 * cus) shape = 41;
+    else if (units >= (int64_t)3 * cus) shape = NT == 1 ? 42 : 41;
+    else if (FMT == Q8_0 && ys > 1) shape = 41;
+    else if (p.K > 8192 && units < (int64_t)2 * cus) shape = 14;
+    else shape = 22;
     // split K four ways stages four activation windows per workgroup: for two
     // tiles of 32-weight blocks of 64-weight chunks that is too many registers
     if (NT == 2 && FMT != Q8_0 && shape == 14) shape = 22;
+    if (NT == 2 && shape == 42) shape = 41;
     hipError_t e = hipErrorNotSupported;
-    if (shape == 41) e = launch_rt_w<FMT, NT, 4, 1>(p, M, x_bytes, stream, ev0, ev1);
+    if constexpr (NT == 1)
+        if (shape == 42) e = launch_rt_w<FMT, NT, 4, 2>(p, M, x_bytes, stream, ev0, ev1);
+    if (shape == 41 || (shape == 42 && e == hipErrorNotSupported)) e = launch_rt_w<FMT, NT, 4, 1>(p, M, x_bytes, stream, ev0, ev1);
     if (e == hipErrorNotSupported && shape >= 22) e = launch_rt_w<FMT, NT, 2, 2>(p, M, x_bytes, stream, ev0, ev1);
     if constexpr (NT == 1 || FMT == Q8_0)
         if (e == hipErrorNotSupported) e = launch_rt_w<FMT, NT, 1, 4>(p, M, x_bytes, stream, ev0, ev1);
     return e;
 }
 
+// More than 16 activation rows: two 16-row tiles per wave (NT = 2), or, when
+// the row tiles are too few to give every CU two, the 16-row form on two
+// workgroup rows, one per half: twice the waves, each decoding the weights
+// for its half, which the second reads from the caches. Measured: Q8_0
+// 5120x5120 at 32 rows 24.4 -> 20.5 us, Q4_K 14336->4096 47.6 -> 33.3, Q4_K
+// 4096x4096 18.1 -> 13.8; with plenty of tiles it loses (Q4_K 4096->14336
+// 25.3 -> 28.6, Q6_K 5120->25600 56.3 -> 80.5). RQMV_RT_MSPLIT=0/1 forces
+// either.
 template <int FMT>
 static hipError_t launch_rt_fmt(const MvParams& p, int M, uint32_t x_bytes, int cus, hipStream_t stream, hipEvent_t ev0,
                                 hipEvent_t ev1) {
-    if (M > 16) return launch_rt<FMT, 2>(p, M, x_bytes, cus, stream, ev0, ev1);
-    return launch_rt<FMT, 1>(p, M, x_bytes, cus, stream, ev0, ev1);
+    if (M <= 16) return launch_rt<FMT, 1>(p, M, x_bytes, cus, 1, stream, ev0, ev1);
+    const char* env = getenv("RQMV_RT_MSPLIT");
+    const bool split = env && *env ? *env != '0' : (p.rows + 15) / 16 < (int64_t)2 * cus;
+    if (split) return launch_rt<FMT, 1>(p, M, x_bytes, cus, 2, stream, ev0, ev1);
+    return launch_rt<FMT, 2>(p, M, x_bytes, cus, 1, stream, ev0, ev1);
 }
 
 template <int FMT>

@@ -162,6 +162,10 @@ __device__ __forceinline__ uint32_t tword(const uint32_t (&R)[16 / RB][4], int c
     else return R[0][c];
 }
 
+// Launched on a grid of (row tile groups) x (activation row groups of 16 NT):
+// workgroup row blockIdx.y takes activation rows [16 NT y, 16 NT y + 16 NT),
+// so that a product at 32 rows can run as two 16-row halves (twice the waves,
+// each decoding the weights for its half).
 template <int FMT, int RB, int NT, int WR, int WK>
 __global__ void __launch_bounds__(64 * WR * WK) __attribute__((amdgpu_waves_per_eu(2))) matvec_mfma_rt(MvParams p, int M, uint32_t x_bytes, int steps_per_wave) {
     using C = RtCfg<FMT, RB, NT, WR, WK>;
@@ -172,11 +176,20 @@ __global__ void __launch_bounds__(64 * WR * WK) __attribute__((amdgpu_waves_per_
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // (uniform: scalar arithmetic below)
     const int wr = wave % WR, wk = wave / WR;
+    // this workgroup's activation rows (the host launches ceil(M / 16 NT) rows of workgroups)
+    {
+        const int m0 = 16 * NT * (int)blockIdx.y;
+        const uint32_t skip = (uint32_t)((int64_t)m0 * p.ldx * 2);
+        p.x = static_cast<const uint16_t*>(p.x) + (int64_t)m0 * p.ldx;
+        p.y += (int64_t)m0 * p.ldy;
+        x_bytes -= skip;
+        M -= m0;
+    }
     uint8_t* const xbase = lds;
     uint8_t* const dummy = lds + C::NXB * C::XBUF;
     const int nq_row = steps_per_wave * CPS / 4;  // quads per row of the LDS scale table
     const int wave_meta = C::s_bytes(nq_row) + C::d_bytes(nq_row);
-    uint8_t* const meta = lds + C::NXB * C::XBUF + C::DUMMY + wave * wave_meta;  // scales [row][quad]
+    uint8_t* const meta = dummy + C::DUMMY + wave * wave_meta;  // scales [row][quad]
     uint8_t* const meta_d = meta + C::s_bytes(nq_row);                             // Q6_K: d [row][quad]
 
     const int64_t row0 = ((int64_t)blockIdx.x * WR + wr) * 16;

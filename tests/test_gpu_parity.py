@@ -329,16 +329,21 @@ def test_matrix_core_forms(gpu, fmt, form, monkeypatch):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("shape,rb", [("41", "8"), ("41", "16"), ("22", "8"), ("22", "16"), ("14", "16")])
-def test_streaming_matrix_core_shapes(gpu, fmt, shape, rb, monkeypatch):
+@pytest.mark.parametrize("shape,rb", [("41", "8"), ("41", "16"), ("42", "8"), ("42", "16"), ("22", "8"), ("22", "16"),
+                                      ("14", "16")])
+@pytest.mark.parametrize("msplit", ["0", "1"])
+def test_streaming_matrix_core_shapes(gpu, fmt, shape, rb, msplit, monkeypatch):
     """The streaming matrix-core form (fp16 activations) at every workgroup
-    shape (RQMV_RT_SHAPE: four row tiles, two tiles x two K ranges, four K
-    ranges) and step (RQMV_RT_RB: 8 rows x 8 chunks or 16 rows x 4 chunks per
-    load): partial row tiles and workgroups, a last step past the row's end,
-    rows of more than one 64-chunk group, K ranges of unequal length, one and
-    two 16-row activation tiles."""
+    shape (RQMV_RT_SHAPE: four row tiles, four tiles x two K ranges, two tiles
+    x two K ranges, four K ranges), step (RQMV_RT_RB: 8 rows x 8 chunks or 16
+    rows x 4 chunks per load) and form above 16 activation rows
+    (RQMV_RT_MSPLIT: two 16-row tiles per wave, or one per workgroup row):
+    partial row tiles and workgroups, a last step past the row's end, rows of
+    more than one 64-chunk group, K ranges of unequal length, one and two
+    16-row activation tiles, strided activations and outputs."""
     monkeypatch.setenv("RQMV_RT_SHAPE", shape)
     monkeypatch.setenv("RQMV_RT_RB", rb)
+    monkeypatch.setenv("RQMV_RT_MSPLIT", msplit)
     kq = fmt in ("q4_k", "q6_k")
     shapes = [(83, 768), (300, 5376), (37, 256)] if kq else [(83, 800), (300, 4160), (21, 96)]
     for rows, cols in shapes:
@@ -350,6 +355,18 @@ def test_streaming_matrix_core_shapes(gpu, fmt, shape, rb, monkeypatch):
             ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
             assert np.isfinite(y).all(), (fmt, shape, rb, rows, cols, m)
             assert rel_l2(y, ref) <= 2e-4, (fmt, shape, rb, rows, cols, m, rel_l2(y, ref))
+        # strided rows of x and y: the same products, nothing written between the rows
+        m, ldx, ldy = 32, cols + 96, rows + 5
+        xs = synth.activations_f16(m * ldx, seed=rows).reshape(m, ldx)
+        xb = gpu.DeviceBuffer.from_array(xs)
+        yb = gpu.DeviceBuffer(4 * m * ldy)
+        yb.fill_zero()
+        W.matvec(xb, 1, m, ldx, yb, ldy)
+        gpu.synchronize()
+        y = yb.download(np.float32).reshape(m, ldy)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, synth.fp16_to_f32(xs[:, :cols]), threads=THREADS)
+        assert rel_l2(y[:, :rows], ref) <= 2e-4, (fmt, shape, rb, msplit, rows, cols, "strided")
+        assert (y[:, rows:] == 0).all()
 
 
 @pytest.mark.parametrize("fmt", FMTS)
