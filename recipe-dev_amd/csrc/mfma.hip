@@ -190,7 +190,11 @@ hipError_t launch_matvec_mfma(int fmt, int xtype, int M, const MvParams& p, int 
     // fit (K ranges longer than it holds) or RQMV_MFMA_RT=0 asks for the
     // staged forms below.
     const char* rt_env = getenv("RQMV_MFMA_RT");
-    if (xtype == X_F16 && !(rt_env && *rt_env == '0')) {
+    // (long rows on few row tiles, at most 16 activation rows: the split-K form,
+    // whose waves read their activation fragments from the caches, measured
+    // faster: Q4_K 14336->4096 at 16 rows 26.4 -> 24.1 us)
+    const bool long_few = M <= 16 && p.K > 8192 && (p.rows + 15) / 16 < (int64_t)2 * cus;
+    if (xtype == X_F16 && !(rt_env && *rt_env == '0') && !(long_few && !(rt_env && *rt_env == '1'))) {
         hipError_t e = hipErrorInvalidValue;
         switch (fmt) {
             case Q4_0: e = launch_rt_fmt<Q4_0>(p, M, (uint32_t)x_bytes, cus, stream, ev0, ev1); break;
