@@ -370,6 +370,34 @@ def test_streaming_matrix_core_shapes(gpu, fmt, shape, rb, msplit, monkeypatch):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+def test_split_k_long_rows(gpu, fmt):
+    """Long rows (K > 8192) on few row tiles: the split-K form up to 16
+    activation rows, the streaming form on two workgroup rows above (one row
+    in the second half at 17): partial row tiles, strided activations and
+    outputs."""
+    for rows, cols in [(83, 9216), (300, 14336)]:
+        w = _weights(fmt, rows, cols, seed=rows + 5)
+        W = gpu.Weight(fmt, rows, cols, w)
+        for m in (3, 16, 17, 32):
+            xh, dt, x32 = _x(m, cols, "f16", seed=m + 17)
+            y = _run_matvec(gpu, W, xh, dt, rows)
+            ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+            assert np.isfinite(y).all(), (fmt, rows, cols, m)
+            assert rel_l2(y, ref) <= 2e-4, (fmt, rows, cols, m, rel_l2(y, ref))
+        m, ldx, ldy = 32, cols + 64, rows + 3
+        xs = synth.activations_f16(m * ldx, seed=rows).reshape(m, ldx)
+        xb = gpu.DeviceBuffer.from_array(xs)
+        yb = gpu.DeviceBuffer(4 * m * ldy)
+        yb.fill_zero()
+        W.matvec(xb, 1, m, ldx, yb, ldy)
+        gpu.synchronize()
+        y = yb.download(np.float32).reshape(m, ldy)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, synth.fp16_to_f32(xs[:, :cols]), threads=THREADS)
+        assert rel_l2(y[:, :rows], ref) <= 2e-4, (fmt, rows, cols, "strided")
+        assert (y[:, rows:] == 0).all()
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 def test_small_m_vector_path(gpu, fmt, monkeypatch):
     """RQMV_MFMA_MIN moves small M back to the vector kernels; both paths agree with the oracle."""
     monkeypatch.setenv("RQMV_MFMA_MIN", "99")
