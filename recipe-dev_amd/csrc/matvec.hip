@@ -155,7 +155,7 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (row0 + r < rows) dot_int<FMT>(d[r], c, xv, bv, acc[r][mm]);
-            if (outliers && wave_has_outlier(bv[0])) {
+            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
                 const uint4 o = xb[(mm * 3 + 2) * nch + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r)
@@ -310,7 +310,7 @@ __global__ void __launch_bounds__(256) matvec_burst(MvParams p, int S) {
                 bv[0] = xb[(mm * 3 + 0) * nch + c];
                 bv[1] = xb[(mm * 3 + 1) * nch + c];
                 dot_int<FMT>(d[u], c, xv, bv, acc[mm]);
-                if (outliers && wave_has_outlier(bv[0]))
+                if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0))
                     dot_outliers<FMT>(d[u], c, xb[(mm * 3 + 2) * nch + c], acc[mm]);
             }
         }

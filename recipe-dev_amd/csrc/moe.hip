@@ -311,7 +311,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
                 bv[1] = xb[nch + c];
                 dot_int<FMT>(dg0, c, xv, bv, ag);
                 dot_int<FMT>(du0, c, xv, bv, au);
-                if (outliers && wave_has_outlier(bv[0])) {
+                if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
                     const uint4 o = xb[2 * nch + c];
                     dot_outliers<FMT>(dg0, c, o, ag);
                     dot_outliers<FMT>(du0, c, o, au);
@@ -339,7 +339,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
             bv[1] = xb[nch + c];
             dot_int<FMT>(dg, c, xv, bv, ag);
             dot_int<FMT>(du, c, xv, bv, au);
-            if (outliers && wave_has_outlier(bv[0])) {
+            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
                 const uint4 o = xb[2 * nch + c];
                 dot_outliers<FMT>(dg, c, o, ag);
                 dot_outliers<FMT>(du, c, o, au);
@@ -418,7 +418,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
                 bv[1] = xb[nch + c];
                 float part = 0.f;
                 dot_int<FMT>(cd0, lc0, xv, bv, part);
-                if (outliers && wave_has_outlier(bv[0])) dot_outliers<FMT>(cd0, lc0, xb[2 * nch + c], part);
+                if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb[2 * nch + c], part);
                 acc = fmaf(w0, part, acc);
             }
             acc = group_sum(acc, G);
@@ -442,7 +442,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
             bv[1] = xb[nch + c];
             float part = 0.f;
             dot_int<FMT>(cd, lc, xv, bv, part);
-            if (outliers && wave_has_outlier(bv[0])) dot_outliers<FMT>(cd, lc, xb[2 * nch + c], part);
+            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd, lc, xb[2 * nch + c], part);
             acc = fmaf(w, part, acc);
         }
         acc = group_sum(acc, G);

@@ -200,18 +200,19 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int K, const StageI
     // A NaN or an infinity anywhere in the block makes the block's scale NaN
     // (its digits are zero), so every product that reads the block is NaN:
     // a non-finite activation is never dropped by the maximum or the rounding.
-    float imax = 0.f;  // this item's largest magnitude
-    int bad = 0;
+    // Magnitudes compared as bit patterns (sign cleared): for finite values
+    // their integer order is their order, and every infinity or NaN pattern
+    // lies above the largest finite one, so one maximum finds both the
+    // block's largest magnitude and whether any value is not finite.
+    uint32_t ibits = 0;  // this item's largest magnitude, as a pattern
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        imax = fmaxf(imax, fabsf(v[k]));
-        bad |= !(fabsf(v[k]) <= 3.402823466e38f);
-    }
-    float amax = imax;
-    amax = fmaxf(amax, dpp_quad_f32<0xB1>(amax));  // quad_perm [1,0,3,2]
-    amax = fmaxf(amax, dpp_quad_f32<0x4E>(amax));  // quad_perm [2,3,0,1]
-    bad |= dpp_i32<0xB1>(bad);
-    bad |= dpp_i32<0x4E>(bad);
+    for (int k = 0; k < 8; ++k) ibits = max(ibits, __builtin_bit_cast(uint32_t, v[k]) & 0x7FFFFFFFu);
+    uint32_t bbits = ibits;
+    bbits = max(bbits, (uint32_t)dpp_i32<0xB1>((int)bbits));  // quad_perm [1,0,3,2]
+    bbits = max(bbits, (uint32_t)dpp_i32<0x4E>((int)bbits));  // quad_perm [2,3,0,1]
+    const int bad = bbits > 0x7F7FFFFFu;
+    const float imax = __builtin_bit_cast(float, ibits);
+    float amax = __builtin_bit_cast(float, bbits);
     if (!live) amax = 0.f;
     // The largest magnitude exceeds kOutlierRatio times the second largest
     // exactly when it is the block's only value at or above amax / 4. When two
@@ -222,7 +223,7 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int K, const StageI
     hi_items += dpp_i32<0xB1>(hi_items);
     hi_items += dpp_i32<0x4E>(hi_items);
     bool outlier = false;
-    if (hi_items == 1 && live && !bad) {
+    if (__builtin_expect(hi_items == 1 && live && !bad, 0)) {
         int big = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) big += fabsf(v[k]) >= thr;
@@ -232,7 +233,7 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int K, const StageI
     }
     float ov = 0.f;
     int gi = 0;
-    if (outlier) {  // (rare: a quad-uniform branch)
+    if (__builtin_expect(outlier, 0)) {  // (rare: a quad-uniform branch)
         // its owner takes the value out; the block is scaled by the rest
         float rest = 0.f;
 #pragma unroll
@@ -252,7 +253,7 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int K, const StageI
         gi += dpp_i32<0x4E>(gi);
         amax = rest;
     }
-    if (bad) {
+    if (__builtin_expect(bad, 0)) {
         amax = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[k] = 0.f;
