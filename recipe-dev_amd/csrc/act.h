@@ -68,4 +68,17 @@ __device__ inline float act_apply(int code, float factor, float x) {
     }
 }
 
+// act_apply with SiLU (llama-style experts) inline and the rest out of the
+// hot path's layout.
+__device__ __forceinline__ float act_apply_likely_silu(int code, float factor, float x) {
+    if (__builtin_expect(code == kActSilu, 1)) return x * act_sigmoid_tanh(x);
+    return act_apply(code, factor, x);
+}
+
+// act_apply with Sigmoid (the usual shared-expert gate) inline.
+__device__ __forceinline__ float act_apply_likely_sigmoid(int code, float factor, float x) {
+    if (__builtin_expect(code == kActSigmoid, 1)) return act_sigmoid_tanh(x);
+    return act_apply(code, factor, x);
+}
+
 }  // namespace rq

@@ -140,16 +140,20 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
     const bool sigmoid = d.scoring != 0, renorm = d.renormalize != 0;
     float v[S];
     uint32_t key[S];
-    float bias[S];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int e = lane + 64 * j;
         v[j] = ws.logits[e < E ? e : E - 1];
-        bias[j] = d.sel_bias ? d.sel_bias[e < E ? e : E - 1] : 0.f;
         key[j] = e < E ? order_key(v[j]) : 0u;  // an absent expert ranks below every score
     }
     const float shared_logit = ws.logits[E];  // read early; used only with a gated shared expert
-    if (d.sel_bias) {
+    if (__builtin_expect(d.sel_bias != nullptr, 0)) {
+        float bias[S];
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int e = lane + 64 * j;
+            bias[j] = d.sel_bias[e < E ? e : E - 1];
+        }
         // probability over every expert, plus the bias
         float am = -INFINITY;
 #pragma unroll
@@ -234,7 +238,7 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
         // The shared expert's weight: its gate's activation (SharedExpert::Gated,
         // recipe.rs:23440-23452), or 1 when it has no gate.
         if (lane == 0 && d.hidden_shared > 0)
-            ws.weights[k] = d.shared_gated ? act_apply(d.shared_gate_act, d.act_factor, shared_logit) : 1.0f;
+            ws.weights[k] = d.shared_gated ? act_apply_likely_sigmoid(d.shared_gate_act, d.act_factor, shared_logit) : 1.0f;
     }
 }
 
@@ -319,7 +323,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
             }
             ag = group_sum(ag, G);
             au = group_sum(au, G);
-            if (r < total_rows && g == G - 1) ws.h[r] = act_apply(d.activation, d.act_factor, ag) * au;
+            if (r < total_rows && g == G - 1) ws.h[r] = act_apply_likely_silu(d.activation, d.act_factor, ag) * au;
         }
         return;
     }
@@ -347,7 +351,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
         }
         ag = group_sum(ag, G);
         au = group_sum(au, G);
-        if (r < total_rows && g == G - 1) ws.h[r] = act_apply(d.activation, d.act_factor, ag) * au;
+        if (r < total_rows && g == G - 1) ws.h[r] = act_apply_likely_silu(d.activation, d.act_factor, ag) * au;
     };
     while (tile < tiles) {
         step(tile, dg0, du0, dg1, du1);
