@@ -271,8 +271,24 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     const int len = min(pos + 1, max_ctx);  // positions past the cache are not read
     if (t0 >= len) return;  // a chunk past the position: nothing to read (the whole workgroup leaves)
 
+    // The position's (cos, sin) pairs for this lane's dims (the table has
+    // max_ctx rows), requested before the keys and values: the rotation then
+    // waits for them alone, and the scores for the keys alone.
+    const bool upper = 8 * b >= HALF;
+    float4 cs4v[ROPE ? 4 : 1];
+    if constexpr (ROPE) {
+        const float4* cs4 =
+            reinterpret_cast<const float4*>(rope + (size_t)min(pos, max_ctx - 1) * HALF + (8 * b - (upper ? HALF : 0)));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cs4v[i] = cs4[i];
+    }
     // keys and values of this lane's positions (clamped into the cache; masked below)
     uint4 kr[NS], vr[NS];
+    // ROPE: the new position's key and value, rounded to fp16, stand in for
+    // sweep jsel's cache entry where they are used (so that no wait for the
+    // cache loads comes before the rotation)
+    uint4 k16 = make_uint4(0, 0, 0, 0), v16 = make_uint4(0, 0, 0, 0);
+    int jsel = -1;
     const size_t head_base = (size_t)kh * max_ctx;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
@@ -285,14 +301,10 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
         vr[j] = *reinterpret_cast<const uint4*>(vc + (head_base + p) * HD + b * 8);
     }
     if constexpr (ROPE) {
-        // the position's (cos, sin) pairs for this lane's dims (the table has max_ctx rows)
-        const bool upper = 8 * b >= HALF;
-        const float4* cs4 =
-            reinterpret_cast<const float4*>(rope + (size_t)min(pos, max_ctx - 1) * HALF + (8 * b - (upper ? HALF : 0)));
         float2 cs[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 v = cs4[i];
+            const float4 v = cs4v[i];
             cs[2 * i] = make_float2(v.x, v.y);
             cs[2 * i + 1] = make_float2(v.z, v.w);
         }
@@ -307,16 +319,12 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
         rotate8(kn, kp, cs, upper);
         // the new position's key and value replace the cache entry in the chunk that holds it
         const int jn = pos - t0 - slot;
+        k16 = pack8(kn);
+        v16 = pack8(vn);
         if (pos < max_ctx && jn >= 0 && jn < kAttnChunk && jn % PPS == 0) {
-            const uint4 k16 = pack8(kn), v16 = pack8(vn);
             *reinterpret_cast<uint4*>(kc + (head_base + pos) * HD + b * 8) = k16;
             *reinterpret_cast<uint4*>(vc + (head_base + pos) * HD + b * 8) = v16;
-#pragma unroll
-            for (int j = 0; j < NS; ++j)
-                if (j == jn / PPS) {
-                    kr[j] = k16;
-                    vr[j] = v16;
-                }
+            jsel = jn / PPS;  // (the sweep whose key and value this lane takes from k16, v16)
         }
     }
 #pragma unroll
@@ -328,7 +336,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         float kv[8];
-        unpack8(kr[j], kv);
+        unpack8(j == jsel ? k16 : kr[j], kv);
         const int pl = slot + j * PPS;
 #pragma unroll
         for (int g = 0; g < MAXG; ++g) {
@@ -365,7 +373,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         float vv[8];
-        unpack8(vr[j], vv);
+        unpack8(j == jsel ? v16 : vr[j], vv);
         const int pl = slot + j * PPS;
         const bool live = t0 + pl < len;
 #pragma unroll
