@@ -25,9 +25,11 @@
 // times, so that no set is copied around the loop.
 //
 // A workgroup is WR row tiles x WK K ranges: tall matrices use WR = 4 (the
-// activation window is shared by four tiles), shorter ones 2 x 2 (split K,
-// the partial sums added in LDS in a fixed order at the end, so results are
-// deterministic).
+// activation window is shared by four tiles), mid-sized ones 4 x 2, shorter
+// ones 2 x 2 or 1 x 4 (split K, the partial sums added in LDS in a fixed
+// order at the end, so results are deterministic). Above 16 activation rows a
+// wave takes two 16-row tiles, or (few row tiles) the launch takes one
+// workgroup row per 16-row half.
 //
 // Each 32-weight block is one v_mfma_f32_16x16x32_f16 per 16 activation rows
 // on exact fp16 weight codes, scaled into fp32 sums per block (Q4_K: minus its
