@@ -531,7 +531,21 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
                            const MoeBatch& b, int cus, hipStream_t stream) {
     constexpr int CW = Traits<FMT>::CW;
     const int nch = (d.top * d.hidden + d.hidden_shared) / CW;
-    const int G = lanes_for(nch);
+    // Lanes per output row, at most 32. Every workgroup stages the whole slot
+    // activation vector, so rows per workgroup amortise it (8 rows at 32
+    // lanes). The same at every batch size, so that a batch stays
+    // bit-identical to one-position calls. Measured on the gguf_moe workload
+    // (6,912 slot values, 2,048 rows), us per step: 1 / 2 / 3 / 4 / 16 / 32
+    // positions 20.5 / 29.6 / 40.2 / 43.2 / 86.5 / 143.0 at 64 lanes, 20.4 /
+    // 28.3 / 35.6 / 37.5 / 81.4 / 133.7 at 32 (16 lanes: 22.6 at one position,
+    // 79.2 at sixteen). RQMV_MOE_DOWN_G overrides it.
+    const char* genv = getenv("RQMV_MOE_DOWN_G");
+    int G = lanes_for(nch);
+    if (G > 32) G = 32;
+    if (genv && *genv) {
+        const int g = atoi(genv);
+        if (g == 8 || g == 16 || g == 32 || g == 64) G = g;
+    }
     const int rows_per_block = 4 * (64 / G);
     int grid = (d.d_model + rows_per_block - 1) / rows_per_block;
     const int cap = batch_grid_cap(cus, b.m);
