@@ -594,6 +594,17 @@ LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu) {
     if (s.block > 512) s.block = 512;
     const int64_t rows_per_wave = (int64_t)(64 / s.G) * s.R;
     const int64_t tiles = (rows + rows_per_wave - 1) / rows_per_wave;
+    // One 512-thread workgroup per CU when the product has the tiles for it:
+    // every workgroup stages (and, with the prologue, normalises) the whole
+    // activation row, so one wide workgroup per CU halves that work against
+    // two of 256. Measured on the 32-layer decode step: 535.2 -> 543.9 tok/s
+    // (1,024 threads: 506.2). (The standalone 4096 -> 14336 product with fp16
+    // x, whose staging is lighter, stays faster at two of 256: 9.8 against
+    // 10.3 us.) RQMV_FUSED_WIDE=0 keeps the matvec plan's shape.
+    if (env_int("RQMV_FUSED_WIDE", 1) && tiles >= (int64_t)8 * cus) {
+        s.block = 512;
+        s.grid = cus;
+    }
     const int wpb = s.block / 64;
     int64_t grid = (tiles + wpb - 1) / wpb;
     if (grid > s.grid) grid = s.grid;
