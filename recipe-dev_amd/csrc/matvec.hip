@@ -425,6 +425,12 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     const int64_t nch = chunks_per_row(fmt, cols);
     int G = 64;
     while (G > 8 && G > nch) G >>= 1;
+    // Q6_K rows of 65-95 chunks (5120 columns: 80) leave a 64-lane group's
+    // second step three-quarters idle, and Q6_K's chunks are the costliest to
+    // decode: 32 lanes per row measured faster (Q6_K 5120->25600 27.6 -> 24.5
+    // us; Q4_K at 5120 columns a tie; Q6_K at 3584, 4096 and 14336 columns
+    // faster at 64: 14.9 / 13.5 / 15.0 against 14.7 / 14.0 / 17.4).
+    if (fmt == Q6_K && G == 64 && nch > 64 && nch < 96) G = 32;
     s.G = G;
     s.R = M <= 2 ? 2 : 1;
     if (xtype == X_F32) s.R = M == 1 ? 2 : 1;
