@@ -452,14 +452,19 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
         s.R = 1;
         s.block = 128;
     }
-    s.G = env_int("RQMV_G", s.G);
-    s.R = env_int("RQMV_R", s.R);
-    s.block = env_int("RQMV_BLOCK", s.block);
+    // tuning overrides, taken only within what the kernels are built for
+    // (lanes per row a power of two from 8 to 64; workgroups of whole waves
+    // up to the kernels' launch bound of 512 threads)
+    const int env_g = env_int("RQMV_G", s.G), env_r = env_int("RQMV_R", s.R), env_b = env_int("RQMV_BLOCK", s.block);
+    if (env_g == 8 || env_g == 16 || env_g == 32 || env_g == 64) s.G = env_g;
+    if (env_r == 1 || env_r == 2 || env_r == 4) s.R = env_r;
+    if (env_b >= 64 && env_b <= 512 && env_b % 64 == 0) s.block = env_b;
     const int64_t rows_per_wave = (int64_t)(64 / s.G) * s.R;
     const int64_t tiles = (rows + rows_per_wave - 1) / rows_per_wave;
     const int wpb = s.block / 64;
     int64_t grid = (tiles + wpb - 1) / wpb;
-    const int64_t cap = (int64_t)cus * env_int("RQMV_BLOCKS_PER_CU", per_cu);
+    const int per_cu_env = env_int("RQMV_BLOCKS_PER_CU", per_cu);
+    const int64_t cap = (int64_t)cus * (per_cu_env >= 1 ? per_cu_env : per_cu);
     if (grid > cap) grid = cap;
     s.grid = env_int("RQMV_GRID", (int)grid);
     if (s.grid < 1) s.grid = 1;
