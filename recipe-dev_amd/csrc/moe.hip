@@ -175,14 +175,19 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
             key[j] = lane + 64 * j < E ? order_key(prob + bias[j]) : 0u;
         }
     }
-    // T = the largest key with at least k keys >= T
+    // T = the largest key with at least k keys >= T. Once exactly k keys are
+    // >= T the kept set is known (it is {key >= T}, as it would be at the
+    // final T), so the remaining bits are skipped.
     uint32_t T = 0;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = T | (1u << bit);
         int cnt = 0;
 #pragma unroll
         for (int j = 0; j < S; ++j) cnt += __popcll(__ballot(key[j] >= cand));
-        if (cnt >= k) T = cand;
+        if (cnt >= k) {
+            T = cand;
+            if (cnt == k) break;
+        }
     }
     int above = 0;
 #pragma unroll
@@ -203,26 +208,27 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
         slot[j] = kept_before + lanes_below(km);
         kept_before += __popcll(km);
     }
-    // Maximum and total over the kept experts (renormalized) or over all.
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < S; ++j)
-        if ((renorm ? kept[j] : lane + 64 * j < E)) m = fmaxf(m, v[j]);
-    float mx = m;
-    {
-        int ii = 0;
-        wave_argmax(mx, ii);
-    }
-    float t = 0.f;
-#pragma unroll
-    for (int j = 0; j < S; ++j)
-        if ((renorm ? kept[j] : lane + 64 * j < E)) t += sigmoid ? sigmoidf_dev(v[j]) : expf(v[j] - mx);
-    const float total = wave_sum_fixed(t);
-    const float denom = (renorm || !sigmoid) ? total : 1.0f;
+    // the slots first: the expert loads wait for them
 #pragma unroll
     for (int j = 0; j < S; ++j)
         if (kept[j]) slot_ids[slot[j]] = lane + 64 * j;
     if (publish) {
+        // maximum and total over the kept experts (renormalized) or over all
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+            if ((renorm ? kept[j] : lane + 64 * j < E)) m = fmaxf(m, v[j]);
+        float mx = m;
+        {
+            int ii = 0;
+            wave_argmax(mx, ii);
+        }
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+            if ((renorm ? kept[j] : lane + 64 * j < E)) t += sigmoid ? sigmoidf_dev(v[j]) : expf(v[j] - mx);
+        const float total = wave_sum_fixed(t);
+        const float denom = (renorm || !sigmoid) ? total : 1.0f;
 #pragma unroll
         for (int j = 0; j < S; ++j) {
             const int e = lane + 64 * j;
@@ -273,6 +279,10 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     // routes for its workgroup and the others read its slots after a barrier.
     // (RING is chosen for exactly the launches of more than two positions.)
     int* const slot_ids = slot_ids_all[RING ? 0 : wave];
+    // the activation loads go out first, so that they land while the position is routed
+    const bool multi = stage_items<FMT>(nch, 1) <= kStageNJ * kMoeThreads;
+    StageItem<XF32> it[kStageNJ];
+    if (multi) stage_multi_issue<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, it);
     if (!RING || wave == 0) route_wave<S>(d, ws, route_dense, blockIdx.x == 0 && wave == 0, slot_ids);
     if constexpr (RING) __syncthreads();
     // Row r of the gate/up stack: hidden row f of routed slot s, or of the shared expert.
@@ -295,7 +305,8 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     ChunkData<FMT> dg0, du0, dg1, du1;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, dg0, du0);
     __shared__ int wave_flags[kMoeThreads / 64];
-    publish_outliers(stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
+    publish_outliers(multi ? stage_multi_finish<FMT, XF32>(nch, d.d_model, 1, kMoeThreads, it, xd, reinterpret_cast<float*>(xb))
+                           : stage_all<FMT, XF32>(nch, d.d_model, x, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, kMoeThreads);
