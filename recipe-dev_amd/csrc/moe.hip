@@ -407,13 +407,19 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
     };
     int tile = blockIdx.x * wpb + wave;
     const int stride = gridDim.x * wpb;
-    // the first tile's weights are requested before the slot activations are staged
+    // The slot activations' loads go out first (they do not depend on the
+    // routing), then the first tile's weights (which wait for the slot ids);
+    // all of them are in flight before any activation is encoded.
+    const bool multi = stage_items<FMT>(nch, 1) <= kStageNJ * kMoeThreads;
+    StageItem<true> it[kStageNJ];
+    if (multi) stage_multi_issue<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, it);
     ChunkData<FMT> cd0, cd1;
     float w0, w1;
     int lc0, lc1;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd0, w0, lc0);
     __shared__ int wave_flags[kMoeThreads / 64];
-    publish_outliers(stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
+    publish_outliers(multi ? stage_multi_finish<FMT, true>(nch, K, 1, kMoeThreads, it, xd, reinterpret_cast<float*>(xb))
+                           : stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, kMoeThreads);
