@@ -373,27 +373,61 @@ __host__ __device__ inline size_t stage_bytes_int(int fmt, int M, int nch) {
     return (size_t)M * nch * (size_t)(xp + 3) * 16;
 }
 
-// F16 weights: fp16 activations as natural pairs, or fp32 activations.
+// F16 weights: fp16 activations as natural pairs, or fp32 activations. Up to
+// kCopyNJ units per thread are all loaded before any is stored, so the copy
+// costs one round trip; larger rows loop.
+constexpr int kCopyNJ = 4;
+
 __device__ __forceinline__ void stage_f16_pairs(int nch, int K, const void* xv, int64_t ldx, int M, int nthreads,
                                                 uint4* xq) {
     const uint16_t* x = static_cast<const uint16_t*>(xv);
     const int total = M * 8 * nch;
-    for (int u = threadIdx.x; u < total; u += nthreads) {
+    auto unit = [&](int u) {
         const int c = u % nch, mj = u / nch, j = mj % 8, m = mj / 8;
         const int k0 = c * 64 + j * 8;
-        xq[u] = k0 < K ? *reinterpret_cast<const uint4*>(x + (int64_t)m * ldx + k0) : make_uint4(0, 0, 0, 0);
+        return k0 < K ? *reinterpret_cast<const uint4*>(x + (int64_t)m * ldx + k0) : make_uint4(0, 0, 0, 0);
+    };
+    if (total <= kCopyNJ * nthreads) {
+        uint4 v[kCopyNJ];
+#pragma unroll
+        for (int j = 0; j < kCopyNJ; ++j) {
+            const int u = (int)threadIdx.x + j * nthreads;
+            if (u < total) v[j] = unit(u);
+        }
+#pragma unroll
+        for (int j = 0; j < kCopyNJ; ++j) {
+            const int u = (int)threadIdx.x + j * nthreads;
+            if (u < total) xq[u] = v[j];
+        }
+        return;
     }
+    for (int u = threadIdx.x; u < total; u += nthreads) xq[u] = unit(u);
 }
 
 __device__ __forceinline__ void stage_f32_quads(int nch, int K, const void* xv, int64_t ldx, int M, int nthreads,
                                                 float4* xf) {
     const float* x = static_cast<const float*>(xv);
     const int total = M * 16 * nch;
-    for (int u = threadIdx.x; u < total; u += nthreads) {
+    auto unit = [&](int u) {
         const int c = u % nch, mj = u / nch, j = mj % 16, m = mj / 16;
         const int k0 = c * 64 + j * 4;
-        xf[u] = k0 < K ? *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        return k0 < K ? *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    if (total <= kCopyNJ * nthreads) {
+        float4 v[kCopyNJ];
+#pragma unroll
+        for (int j = 0; j < kCopyNJ; ++j) {
+            const int u = (int)threadIdx.x + j * nthreads;
+            if (u < total) v[j] = unit(u);
+        }
+#pragma unroll
+        for (int j = 0; j < kCopyNJ; ++j) {
+            const int u = (int)threadIdx.x + j * nthreads;
+            if (u < total) xf[u] = v[j];
+        }
+        return;
     }
+    for (int u = threadIdx.x; u < total; u += nthreads) xf[u] = unit(u);
 }
 
 __host__ __device__ inline size_t stage_bytes_f16w(int xtype_f32, int M, int nch) {
