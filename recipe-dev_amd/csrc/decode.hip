@@ -462,7 +462,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
 #pragma unroll
     for (int k = 0; k < kMlPer; ++k)
         if (t + 256 * k < live) M = fmaxf(M, mlv[k].x);
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    M = wave_max(M);  // (DPP and lane swaps: no LDS round trips)
     if (lane == 0) part[0][wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
@@ -476,7 +476,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
             L += mlv[k].y * e;
         }
     }
-    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+    L = wave_sum(L);
     if (lane == 0) part[1][wave] = L;
     __syncthreads();
     const float inv = 1.0f / ((part[1][0] + part[1][1]) + (part[1][2] + part[1][3]));
