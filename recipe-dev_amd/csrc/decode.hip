@@ -227,11 +227,23 @@ __device__ __forceinline__ void rotate8(float (&x)[8], const float (&xp)[8], con
 }
 
 // The rotation partners of a lane's eight values: in the lane holding the
-// piece HD/2 away in the same position, lane ^ (LPP / 2).
+// piece HD/2 away in the same position, lane ^ (LPP / 2). For 16 lanes per
+// position that is a DPP rotation of each 16-lane row by 8, for 32 a 16-lane
+// swap (no LDS round trip either way); 8 lanes per position shuffle.
 template <int LPP>
 __device__ __forceinline__ void partners8(const float (&x)[8], float (&xp)[8]) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xp[e] = __shfl_xor(x[e], LPP / 2);
+    for (int e = 0; e < 8; ++e) {
+        if constexpr (LPP == 16) {
+            xp[e] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x[e]), 0x128, 0xf,
+                                                                          0xf, false));  // row_ror:8
+        } else if constexpr (LPP == 32) {
+            const LanePair pr = swap16(x[e]);
+            xp[e] = (threadIdx.x & 16) ? pr.lo : pr.hi;
+        } else {
+            xp[e] = __shfl_xor(x[e], LPP / 2);
+        }
+    }
 }
 
 template <int HD, int MAXG, bool ROPE>
