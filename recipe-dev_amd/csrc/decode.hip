@@ -93,10 +93,13 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(float* qkv, const int* pos
 // positions past the end are masked by selection, never by multiplying, so
 // stale cache contents cannot leak in). Pass 1: each query head's score
 // against each position (an eight-value dot per lane, summed over the
-// position's lanes), times 1/sqrt(HD), into LDS. Pass 2: per query head the
-// chunk's maximum m, weights e = exp(s - m) and their sum l. Pass 3: o = sum e
-// v, per lane over its positions, summed over the lanes that hold the same
-// values. The chunk's (m, l, o) go to the workspace.
+// position's lanes), times 1/sqrt(HD), kept in the registers of the
+// position's lanes. Pass 2, per wave: each head's maximum mw over the wave's
+// positions, weights e = exp(s - mw) and their sum lw, through DPP and lane
+// swaps (no LDS, no barrier). Pass 3: o = sum e v, per lane over its
+// positions, summed over the lanes that hold the same values; after the one
+// barrier the waves are merged, m = max mw and each wave's o and lw scaled by
+// e^(mw - m). The chunk's (m, l, o) go to the workspace.
 //
 // ROPE (the decode step's fused form): q and the new key come unrotated in
 // qkv ([q heads | k heads | v heads]) and are turned here with a cos/sin table
@@ -180,6 +183,27 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 __device__ __forceinline__ float wave_sum(float v) { return swap32_sum(swap16_sum(sum_lanes<16>(v))); }
 
+// Maximum and sum over a wave's position slots: the lanes holding the same
+// piece b of different positions (LPP lanes per position: lane bits from
+// log2(LPP) up), every lane getting the result; DPP row rotation by 8 for
+// lane bit 3, the lane swaps for bits 4 and 5.
+template <int LPP>
+__device__ __forceinline__ float slots_max(float v) {
+    if constexpr (LPP <= 8)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false)));
+    if constexpr (LPP <= 16) v = swap16_max(v);
+    if constexpr (LPP <= 32) v = swap32_max(v);
+    return v;
+}
+template <int LPP>
+__device__ __forceinline__ float slots_sum(float v) {
+    if constexpr (LPP <= 8)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+    if constexpr (LPP <= 16) v = swap16_sum(v);
+    if constexpr (LPP <= 32) v = swap32_sum(v);
+    return v;
+}
+
 struct AttnWork {
     float* ml;  // [nq][nchunks][2]
     float* o;   // [nq][nchunks][hd]
@@ -255,8 +279,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     constexpr int PPS = kAttnThreads / LPP;        // positions per sweep
     constexpr int NS = kAttnChunk / PPS;           // sweeps per chunk
     constexpr int HALF = HD / 2;
-    __shared__ float sc[MAXG][kAttnChunk];
-    __shared__ float ml[MAXG][2];
+    __shared__ float wml[kAttnWaves][MAXG][2];  // each wave's (maximum, weight sum) per head
     // the partial outputs: with at most four query heads, one padded row per
     // position slot of the workgroup; with more, one row per wave
     constexpr bool kSlotRows = MAXG <= 4;
@@ -344,36 +367,42 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[g][e] = g < group ? qr[g][e] : 0.f;
 
-    // pass 1: scores
+    // pass 1: each lane's positions' scores (every lane of a position holds them)
+    float s[NS][MAXG];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         float kv[8];
         unpack8(j == jsel ? k16 : kr[j], kv);
-        const int pl = slot + j * PPS;
+        const bool live = t0 + slot + j * PPS < len;
 #pragma unroll
         for (int g = 0; g < MAXG; ++g) {
             float d = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kv[e], d);
             d = sum_lanes<LPP>(d);
-            if (g < group && b == 0) sc[g][pl] = t0 + pl < len ? d * scale : -INFINITY;
+            s[j][g] = live ? d * scale : -INFINITY;
         }
     }
-    __syncthreads();
 
-    // pass 2: per query head, the chunk's maximum, weights and their sum (one position per lane)
-    for (int g = wave; g < group; g += kAttnWaves) {
-        const float s = sc[g][lane];
-        const float m = wave_max(s);
-        const float e = s == -INFINITY ? 0.f : __expf(s - m);
-        sc[g][lane] = e;
-        const float l = wave_sum(e);
-        if (lane == 0) {
-            ml[g][0] = m;
-            ml[g][1] = l;
+    // pass 2, per wave: each head's maximum mw over the wave's positions (the
+    // lane's sweeps, then the wave's position slots across lanes), weights
+    // e = exp(s - mw) and their sum lw, all in registers; the chunk's waves
+    // are merged at the end
+    float mw[MAXG], lw[MAXG];
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+        float m = s[0][g];
+#pragma unroll
+        for (int j = 1; j < NS; ++j) m = fmaxf(m, s[j][g]);
+        mw[g] = slots_max<LPP>(m);
+        float l = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            s[j][g] = s[j][g] == -INFINITY ? 0.f : __expf(s[j][g] - mw[g]);
+            l += s[j][g];
         }
+        lw[g] = slots_sum<LPP>(l);
     }
-    __syncthreads();
 
     // pass 3: o = sum_p e_p v_p over this lane's positions, then over the lanes
     // holding the same eight values (across the wave, then across waves)
@@ -386,13 +415,12 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     for (int j = 0; j < NS; ++j) {
         float vv[8];
         unpack8(j == jsel ? v16 : vr[j], vv);
-        const int pl = slot + j * PPS;
-        const bool live = t0 + pl < len;
+        const bool live = t0 + slot + j * PPS < len;
 #pragma unroll
         for (int e = 0; e < 8; ++e) vv[e] = live ? vv[e] : 0.f;
 #pragma unroll
         for (int g = 0; g < MAXG; ++g) {
-            const float wgt = g < group ? sc[g][pl] : 0.f;
+            const float wgt = g < group ? s[j][g] : 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[g][e] = fmaf(wgt, vv[e], o[g][e]);
         }
@@ -422,17 +450,45 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
                 for (int e = 0; e < 8; ++e) red[wave * kRedStride + g * HD + b * 8 + e] = o[g][e];
         }
     }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) {
+            wml[wave][g][0] = mw[g];
+            wml[wave][g][1] = lw[g];
+        }
+    }
     __syncthreads();
+    // the chunk: m = max over the waves, each wave's sums rescaled by e^(mw - m)
+    constexpr int kRowsPerWave = kRedRows / kAttnWaves;
     for (int i = t; i < group * HD; i += kAttnThreads) {
+        const int g = i / HD, d = i % HD;
+        float m = wml[0][g][0];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; ++w) m = fmaxf(m, wml[w][g][0]);
         float acc = 0.f;
 #pragma unroll
-        for (int r = 0; r < kRedRows; ++r) acc += red[r * kRedStride + i];
-        const int g = i / HD, d = i % HD;
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float mwg = wml[w][g][0];
+            const float f = mwg == -INFINITY ? 0.f : __expf(mwg - m);
+            float part = 0.f;
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) part += red[(w * kRowsPerWave + r) * kRedStride + i];
+            acc = fmaf(f, part, acc);
+        }
         ws.o[((size_t)(kh * group + g) * nchunks + chunk) * HD + d] = acc;
     }
     if (t < group) {
-        ws.ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 0] = ml[t][0];
-        ws.ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 1] = ml[t][1];
+        float m = wml[0][t][0];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; ++w) m = fmaxf(m, wml[w][t][0]);
+        float l = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float mwg = wml[w][t][0];
+            l = fmaf(mwg == -INFINITY ? 0.f : __expf(mwg - m), wml[w][t][1], l);
+        }
+        ws.ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 0] = m;
+        ws.ml[((size_t)(kh * group + t) * nchunks + chunk) * 2 + 1] = l;
     }
 }
 
