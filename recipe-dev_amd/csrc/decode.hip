@@ -494,9 +494,12 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 
 // out[h] = sum_c w_c o_c with w_c = e^(m_c - M) / sum_c l_c e^(m_c - M) over
 // the live chunks of query head h. Each thread takes one 16-byte column of the
-// head and every CLN-th chunk; its first kPre chunks are loaded with the
-// position and the chunk maxima, before anything is known of which are live.
-// The chunk lanes are then summed in order through LDS.
+// head and every CLN-th chunk; its first kPre chunks' partials and maxima are
+// loaded with the position, before anything is known of which are live. Each
+// wave forms the maximum and weight sum of every 256th chunk's (m, l) from
+// its lanes; after one barrier every thread merges the four waves' into M and
+// L, weights its own chunks, and the chunk lanes are summed in order through
+// LDS.
 template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const int* pos_dev, int max_ctx, int nchunks,
                                                            float* out) {
@@ -504,7 +507,6 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
     constexpr int CLN = 256 / COLS4;
     constexpr int kPre = 12;
     constexpr int kMlPer = kAttnMaxChunks / 256;
-    __shared__ float wts[kAttnMaxChunks];
     __shared__ float part[2][4];
     __shared__ float4 cred[256];
     const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -512,10 +514,12 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
     const int col = t % COLS4, cl = t / COLS4;
     const float* po = ws.o + (size_t)h * nchunks * HD + col * 4;
     float4 pre[kPre];
+    float mine[kPre];  // the maxima of the thread's own chunks
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
         const int c = min(cl + k * CLN, nchunks - 1);
         pre[k] = *reinterpret_cast<const float4*>(po + (size_t)c * HD);
+        mine[k] = hml[2 * c];
     }
     float2 mlv[kMlPer];
 #pragma unroll
@@ -525,35 +529,34 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
     }
     const int len = min(*pos_dev + 1, max_ctx);
     const int live = (len + kAttnChunk - 1) / kAttnChunk;
-    // M and L over the live chunks: each thread its strided share, then the waves, then the four waves
-    float M = -INFINITY;
+    // this wave's maximum and weight sum over its lanes' live chunks
+    float Mw = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kMlPer; ++k)
-        if (t + 256 * k < live) M = fmaxf(M, mlv[k].x);
-    M = wave_max(M);  // (DPP and lane swaps: no LDS round trips)
-    if (lane == 0) part[0][wave] = M;
+        if (t + 256 * k < live) Mw = fmaxf(Mw, mlv[k].x);
+    Mw = wave_max(Mw);  // (DPP and lane swaps: no LDS round trips)
+    float Lw = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMlPer; ++k)
+        if (t + 256 * k < live) Lw = fmaf(mlv[k].y, __expf(mlv[k].x - Mw), Lw);
+    Lw = wave_sum(Lw);
+    if (lane == 0) {
+        part[0][wave] = Mw;
+        part[1][wave] = Lw;
+    }
     __syncthreads();
-    M = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
+    const float M = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
     float L = 0.f;
 #pragma unroll
-    for (int k = 0; k < kMlPer; ++k) {
-        const int c = t + 256 * k;
-        if (c < live) {
-            const float e = __expf(mlv[k].x - M);
-            wts[c] = e;
-            L += mlv[k].y * e;
-        }
-    }
-    L = wave_sum(L);
-    if (lane == 0) part[1][wave] = L;
-    __syncthreads();
-    const float inv = 1.0f / ((part[1][0] + part[1][1]) + (part[1][2] + part[1][3]));
+    for (int w = 0; w < 4; ++w)
+        if (part[0][w] != -INFINITY) L = fmaf(part[1][w], __expf(part[0][w] - M), L);
+    const float inv = 1.0f / L;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
         const int c = cl + k * CLN;
         if (c < live) {
-            const float w = wts[c];
+            const float w = __expf(mine[k] - M);
             acc.x = fmaf(w, pre[k].x, acc.x);
             acc.y = fmaf(w, pre[k].y, acc.y);
             acc.z = fmaf(w, pre[k].z, acc.z);
@@ -562,7 +565,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
     }
     for (int c = cl + kPre * CLN; c < live; c += CLN) {
         const float4 v = *reinterpret_cast<const float4*>(po + (size_t)c * HD);
-        const float w = wts[c];
+        const float w = __expf(hml[2 * c] - M);
         acc.x = fmaf(w, v.x, acc.x);
         acc.y = fmaf(w, v.y, acc.y);
         acc.z = fmaf(w, v.z, acc.z);
