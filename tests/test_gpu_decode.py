@@ -269,7 +269,8 @@ def _mv_ref(fmt, w, rows, cols, x):
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 6144, 4096), ("q8_0", 4096, 4096), ("q6_k", 512, 1024),
                                            ("q4_0", 300, 4096), ("q4_k", 256, 14336), ("q8_0", 1001, 544),
-                                           ("q8_0", 3, 32)])
+                                           ("q8_0", 3, 32), ("q4_k", 6143, 4096), ("q6_k", 6145, 1024),
+                                           ("q4_0", 6142, 512)])
 @pytest.mark.parametrize("with_delta", [False, True])
 def test_fused_norm_prologue(gpu, fmt, rows, cols, with_delta):
     w = synth.weights(fmt, rows, cols, seed=rows + cols)
@@ -313,7 +314,8 @@ def test_fused_glu_epilogue(gpu, fmt, n, cols):
     assert rel_err(z[1::2], _mv_ref(fmt, u, n, cols, x)) < 1e-3
 
 
-@pytest.mark.parametrize("fmt,rows,cols", [("q8_0", 1001, 544), ("q8_0", 4096, 4096), ("q4_0", 77, 128)])
+@pytest.mark.parametrize("fmt,rows,cols", [("q8_0", 1001, 544), ("q8_0", 4096, 4096), ("q4_0", 77, 128),
+                                           ("q4_k", 6143, 4096)])
 def test_fused_plain_without_norm(gpu, fmt, rows, cols):
     """The fused entry point with neither prologue nor epilogue equals the plain
     product bit for bit (one launch shape per format and row count)."""
