@@ -285,7 +285,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     constexpr bool kSlotRows = MAXG <= 4;
     constexpr int kRedRows = kSlotRows ? kAttnThreads / (HD / 8) : kAttnWaves;
     constexpr int kRedStride = MAXG * HD + (kSlotRows ? 4 : 0);
-    __shared__ float red[kRedRows * kRedStride];
+    __shared__ __align__(16) float red[kRedRows * kRedStride];
     const int kh = blockIdx.x, chunk = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int b = t % LPP, slot = t / LPP;
@@ -438,16 +438,14 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
 #pragma unroll
         for (int g = 0; g < MAXG; ++g)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if constexpr (LPP <= 8) o[g][e] += __shfl_xor(o[g][e], 8);
-                if constexpr (LPP <= 16) o[g][e] = swap16_sum(o[g][e]);
-                o[g][e] = swap32_sum(o[g][e]);
-            }
+            for (int e = 0; e < 8; ++e) o[g][e] = slots_sum<LPP>(o[g][e]);
         if (lane < LPP) {
+            float* row = red + wave * kRedStride + b * 8;
 #pragma unroll
-            for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) red[wave * kRedStride + g * HD + b * 8 + e] = o[g][e];
+            for (int g = 0; g < MAXG; ++g) {
+                *reinterpret_cast<float4*>(row + g * HD) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+                *reinterpret_cast<float4*>(row + g * HD + 4) = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+            }
         }
     }
     if (lane == 0) {
