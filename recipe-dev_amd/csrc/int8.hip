@@ -13,7 +13,7 @@
 // recipe's GPU backends run 32 lanes per output (NVIDIA warps, gfx11/gfx12
 // wave32). Here each wave64 runs two outputs on its two 32-lane halves: lane l
 // of a half holds exactly the partial sums recipe's lane l holds, and
-// __shfl_xor within the half repeats recipe's butterfly.
+// lane exchanges within the half (lane_xor) repeat recipe's butterfly.
 //
 // fp32 order per output (this file is built with -ffp-contract=off, and fmaf
 // stands where recipe's state madd is):
@@ -315,6 +315,31 @@ __device__ __forceinline__ int quad_sum(int v) {
     return v + __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);  // lane ^ 2
 }
 __device__ __forceinline__ int lane_int(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+// The value of lane ^ OFF (OFF < 32, within the lane's 32-lane half), through
+// DPP and the 16-lane swap rather than the LDS crossbar: quad permutations
+// for 1 and 2, row shifts by 4 either way for 4, a row rotation by 8 for 8,
+// v_permlane16_swap for 16. Each lane then adds exactly the partner
+// __shfl_xor would give it, so the butterflies keep their bits.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int iv = __builtin_bit_cast(int, v);
+    if constexpr (OFF == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xf, 0xf, false));
+    if constexpr (OFF == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xf, 0xf, false));
+    if constexpr (OFF == 4) {
+        const int up = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xf, 0xf, false);    // row_shr:4 (lane - 4)
+        const int down = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xf, 0xf, false);  // row_shl:4 (lane + 4)
+        return __builtin_bit_cast(float, (threadIdx.x & 4) ? up : down);
+    }
+    if constexpr (OFF == 8) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xf, 0xf, false));
+    if constexpr (OFF == 16) {
+        float a = v, b = v;
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        return (threadIdx.x & 16) ? a : b;
+    }
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16, "lane_xor: 1, 2, 4, 8 or 16");
+    return v;
+}
+
 __device__ __forceinline__ float lane_float(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
@@ -391,8 +416,11 @@ __global__ __launch_bounds__(kI8Threads) void int8_slices_kernel(I8Launch p) {
         }
         __builtin_amdgcn_wave_barrier();
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 32);
+    acc = acc + lane_xor<16>(acc);
+    acc = acc + lane_xor<8>(acc);
+    acc = acc + lane_xor<4>(acc);
+    acc = acc + lane_xor<2>(acc);
+    acc = acc + lane_xor<1>(acc);
     if ((lane & 31) == 0 && (mine == 0 || two)) p.y[(int64_t)blockIdx.y * p.ldy + row0 + mine] = acc;
 }
 
@@ -466,7 +494,7 @@ __global__ __launch_bounds__(kI8Threads) void int8_q4k256_kernel(I8Launch p) {
         }
         __builtin_amdgcn_wave_barrier();
     }
-    const float other = __shfl_xor(acc, 1);
+    const float other = lane_xor<1>(acc);
     if (lane == 0) p.y[(int64_t)m * p.ldy + row0] = acc - other;
     if (lane == 32 && two) p.y[(int64_t)m * p.ldy + row0 + 1] = acc - other;
 }
@@ -544,9 +572,9 @@ __global__ __launch_bounds__(kI8Threads) void int8_q6k256_kernel(I8Launch p) {
         }
         __builtin_amdgcn_wave_barrier();
     }
-    const float t = f + __shfl_xor(f, 4);
-    const float u = t + __shfl_xor(t, 2);
-    const float total = u + __shfl_xor(u, 1);
+    const float t = f + lane_xor<4>(f);
+    const float u = t + lane_xor<2>(t);
+    const float total = u + lane_xor<1>(u);
     if (lane == 0) p.y[(int64_t)blockIdx.y * p.ldy + row0] = total;
     if (lane == 32 && two) p.y[(int64_t)blockIdx.y * p.ldy + row0 + 1] = total;
 }
