@@ -130,7 +130,11 @@ __device__ __forceinline__ float sum_lanes(float v) {
     if constexpr (LPP >= 16)
         v += __builtin_bit_cast(float,
                                 __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
-    if constexpr (LPP >= 32) v += __shfl_xor(v, 16);
+    if constexpr (LPP >= 32) {  // lane ^ 16 through v_permlane16_swap (see swap16 below)
+        float a = v, b = v;
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        v = a + b;
+    }
     return v;
 }
 
@@ -253,7 +257,7 @@ __device__ __forceinline__ void rotate8(float (&x)[8], const float (&xp)[8], con
 // The rotation partners of a lane's eight values: in the lane holding the
 // piece HD/2 away in the same position, lane ^ (LPP / 2). For 16 lanes per
 // position that is a DPP rotation of each 16-lane row by 8, for 32 a 16-lane
-// swap (no LDS round trip either way); 8 lanes per position shuffle.
+// swap, for 8 a row shift by 4 (no LDS round trip in any case).
 template <int LPP>
 __device__ __forceinline__ void partners8(const float (&x)[8], float (&xp)[8]) {
 #pragma unroll
@@ -264,8 +268,11 @@ __device__ __forceinline__ void partners8(const float (&x)[8], float (&xp)[8]) {
         } else if constexpr (LPP == 32) {
             const LanePair pr = swap16(x[e]);
             xp[e] = (threadIdx.x & 16) ? pr.lo : pr.hi;
-        } else {
-            xp[e] = __shfl_xor(x[e], LPP / 2);
+        } else {  // 8 lanes per position: lane ^ 4, a row shift by 4 one way or the other
+            const int iv = __builtin_bit_cast(int, x[e]);
+            const int up = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xf, 0xf, false);    // row_shr:4 (lane - 4)
+            const int down = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xf, 0xf, false);  // row_shl:4 (lane + 4)
+            xp[e] = __builtin_bit_cast(float, (threadIdx.x & 4) ? up : down);
         }
     }
 }
