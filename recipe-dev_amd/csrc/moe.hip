@@ -28,6 +28,10 @@ constexpr int kMoeThreads = 256;  // workgroup size of the MoE kernels (four wav
 constexpr int kMoeOwnRouteMax = 2;  // positions per launch up to which every wave routes on its own
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
+static bool env_flag(const char* name, bool fallback) {
+    const char* v = getenv(name);
+    return v && *v ? *v != '0' : fallback;
+}
 
 // Workgroups per position of a launch: at most eight per CU over the whole
 // batch (each workgroup routes or stages its position once, so a batch of
@@ -373,8 +377,8 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     }
 }
 
-template <int FMT, bool RING>
-__global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
+template <int FMT, bool RING, int BT = kMoeThreads>
+__global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
                                                         float* y, int G, MoeBatch batch) {
     constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
     ws = position_ws(ws, batch.ws_stride, (int)blockIdx.y);
@@ -387,7 +391,7 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
     const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
-    const int wpb = kMoeThreads >> 6, wave = threadIdx.x >> 6;
+    const int wpb = BT >> 6, wave = threadIdx.x >> 6;
     const int rows_per_wave = 64 / G;
     const int tiles = (d.d_model + rows_per_wave - 1) / rows_per_wave;
     // Chunk c of output row n: chunk lc of slot s's expert down row, or of the shared expert's.
@@ -410,19 +414,19 @@ __global__ void __launch_bounds__(kMoeThreads) moe_down_kernel(MoeDims d, MoeBan
     // The slot activations' loads go out first (they do not depend on the
     // routing), then the first tile's weights (which wait for the slot ids);
     // all of them are in flight before any activation is encoded.
-    const bool multi = stage_items<FMT>(nch, 1) <= kStageNJ * kMoeThreads;
+    const bool multi = stage_items<FMT>(nch, 1) <= kStageNJ * BT;
     StageItem<true> it[kStageNJ];
-    if (multi) stage_multi_issue<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, it);
+    if (multi) stage_multi_issue<FMT, true>(nch, K, ws.h, 0, 1, BT, it);
     ChunkData<FMT> cd0, cd1;
     float w0, w1;
     int lc0, lc1;
     fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd0, w0, lc0);
-    __shared__ int wave_flags[kMoeThreads / 64];
-    publish_outliers(multi ? stage_multi_finish<FMT, true>(nch, K, 1, kMoeThreads, it, xd, reinterpret_cast<float*>(xb))
-                           : stage_all<FMT, true>(nch, K, ws.h, 0, 1, kMoeThreads, xd, reinterpret_cast<float*>(xb)),
+    __shared__ int wave_flags[BT / 64];
+    publish_outliers(multi ? stage_multi_finish<FMT, true>(nch, K, 1, BT, it, xd, reinterpret_cast<float*>(xb))
+                           : stage_all<FMT, true>(nch, K, ws.h, 0, 1, BT, xd, reinterpret_cast<float*>(xb)),
                      wave_flags);
     __syncthreads();
-    const bool outliers = read_outliers(wave_flags, kMoeThreads);
+    const bool outliers = read_outliers(wave_flags, BT);
     if constexpr (!RING) {
         bool fetched = true;
         for (; tile < tiles; tile += stride) {
@@ -575,18 +579,27 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
         const int g = atoi(genv);
         if (g == 8 || g == 16 || g == 32 || g == 64) G = g;
     }
-    const int rows_per_block = 4 * (64 / G);
+    // Two positions: 512-thread workgroups, each staging the slot activations
+    // once for twice the rows (the gguf_moe workload 21.5 -> 20.3 us per step;
+    // at one position 18.1 -> 18.4, so it keeps 256). Each row's sum is the
+    // same either way. RQMV_MOE_DOWN_WIDE=0/1 forces it off or on (one or two
+    // positions).
+    const bool wide = b.m <= kMoeOwnRouteMax && env_flag("RQMV_MOE_DOWN_WIDE", b.m == 2);
+    const int threads = wide ? 512 : kMoeThreads;
+    const int rows_per_block = threads / 64 * (64 / G);
     int grid = (d.d_model + rows_per_block - 1) / rows_per_block;
     const int cap = batch_grid_cap(cus, b.m);
     if (grid > cap) grid = cap;
     const size_t lds = stage_bytes_int(FMT, 1, nch);
-    auto kernel = b.m > kMoeOwnRouteMax ? moe_down_kernel<FMT, true> : moe_down_kernel<FMT, false>;
+    auto kernel = b.m > kMoeOwnRouteMax ? moe_down_kernel<FMT, true>
+                  : wide                ? moe_down_kernel<FMT, false, 512>
+                                        : moe_down_kernel<FMT, false>;
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid, b.m), dim3(kMoeThreads), lds, stream, d, down, down_sh, ws, y, G, b);
+    hipLaunchKernelGGL(kernel, dim3(grid, b.m), dim3(threads), lds, stream, d, down, down_sh, ws, y, G, b);
     return hipGetLastError();
 }
 
