@@ -377,7 +377,12 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     }
 }
 
-template <int FMT, bool RING, int BT = kMoeThreads>
+// SPLIT (one or two positions, G = 32): one row per wave, its lanes taking
+// chunks lane, lane + 64, ... as 64 lanes would, with the sums formed in the
+// order of 32 lanes per row (lane g adds chunk g + 64 s, then lane g + 32's
+// chunk g + 32 + 64 s, through a 32-lane swap), so that every row carries the
+// bits of the 32-lane form with twice the waves.
+template <int FMT, bool RING, int BT = kMoeThreads, bool SPLIT = false>
 __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
                                                         float* y, int G, MoeBatch batch) {
     constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
@@ -390,9 +395,10 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
     const int routed_ch = d.top * cps;
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
-    const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
+    static_assert(!(SPLIT && RING), "the split form is for one or two positions");
+    const int lane = threadIdx.x & 63, g = SPLIT ? lane : lane & (G - 1), sub = SPLIT ? 0 : lane / G;
     const int wpb = BT >> 6, wave = threadIdx.x >> 6;
-    const int rows_per_wave = 64 / G;
+    const int rows_per_wave = SPLIT ? 1 : 64 / G;
     const int tiles = (d.d_model + rows_per_wave - 1) / rows_per_wave;
     // Chunk c of output row n: chunk lc of slot s's expert down row, or of the shared expert's.
     auto fetch = [&](int n, int c, ChunkData<FMT>& cd, float& w, int& lc) {
@@ -427,6 +433,40 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, BT);
+    if constexpr (SPLIT) {
+        bool fetched = true;
+        for (; tile < tiles; tile += stride) {
+            const int n = tile;
+            float acc = 0.f;
+            for (int c0 = 0; c0 < nch; c0 += 64) {
+                const int c = c0 + lane;
+                if (!fetched) fetch(n, c, cd0, w0, lc0);
+                fetched = false;
+                float part = 0.f;
+                if (c < nch) {
+                    uint4 xv[XP];
+                    uint4 bv[2];
+#pragma unroll
+                    for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+                    bv[0] = xb[c];
+                    bv[1] = xb[nch + c];
+                    dot_int<FMT>(cd0, lc0, xv, bv, part);
+                    if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb[2 * nch + c], part);
+                }
+                // lane + 32's chunk and weight, in every lane below 32
+                float pu = part, wu = w0, pl = part, wl = w0;
+                asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(pl), "+v"(pu));
+                asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(wl), "+v"(wu));
+                if (lane < 32) {
+                    if (c < nch) acc = fmaf(w0, part, acc);
+                    if (c + 32 < nch) acc = fmaf(wu, pu, acc);
+                }
+            }
+            acc = group_sum(acc, 32);
+            if (n < d.d_model && lane == 31) y[n] = acc;
+        }
+        return;
+    }
     if constexpr (!RING) {
         bool fetched = true;
         for (; tile < tiles; tile += stride) {
@@ -564,14 +604,11 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
                            const MoeBatch& b, int cus, hipStream_t stream) {
     constexpr int CW = Traits<FMT>::CW;
     const int nch = (d.top * d.hidden + d.hidden_shared) / CW;
-    // Lanes per output row, at most 32. Every workgroup stages the whole slot
-    // activation vector, so rows per workgroup amortise it (8 rows at 32
-    // lanes). The same at every batch size, so that a batch stays
-    // bit-identical to one-position calls. Measured on the gguf_moe workload
-    // (6,912 slot values, 2,048 rows), us per step: 1 / 2 / 3 / 4 / 16 / 32
-    // positions 20.5 / 29.6 / 40.2 / 43.2 / 86.5 / 143.0 at 64 lanes, 20.4 /
-    // 28.3 / 35.6 / 37.5 / 81.4 / 133.7 at 32 (16 lanes: 22.6 at one position,
-    // 79.2 at sixteen). RQMV_MOE_DOWN_G overrides it.
+    // Lanes per output row (the order of each row's sum), at most 32. Every
+    // workgroup stages the whole slot activation vector, so rows per
+    // workgroup amortise it. The same at every batch size, so that a batch
+    // stays bit-identical to one-position calls (16 lanes measured slower at
+    // one position, 64 from two). RQMV_MOE_DOWN_G overrides it.
     const char* genv = getenv("RQMV_MOE_DOWN_G");
     int G = lanes_for(nch);
     if (G > 32) G = 32;
@@ -579,21 +616,43 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
         const int g = atoi(genv);
         if (g == 8 || g == 16 || g == 32 || g == 64) G = g;
     }
-    // Two positions: 512-thread workgroups, each staging the slot activations
-    // once for twice the rows (the gguf_moe workload 21.5 -> 20.3 us per step;
-    // at one position 18.1 -> 18.4, so it keeps 256). Each row's sum is the
-    // same either way. RQMV_MOE_DOWN_WIDE=0/1 forces it off or on (one or two
-    // positions).
-    const bool wide = b.m <= kMoeOwnRouteMax && env_flag("RQMV_MOE_DOWN_WIDE", b.m == 2);
-    const int threads = wide ? 512 : kMoeThreads;
+    // From two positions, 512-thread workgroups, each staging the slot
+    // activations once for twice the rows; at one position, the split form
+    // below. Each row's sum is the same in every form, so batches stay
+    // bit-identical to one-position calls. Measured on the gguf_moe workload,
+    // us per step at 1 / 2 / 3 / 4 / 8 / 16 / 32 positions: 256 threads 18.2 /
+    // 21.5 / 27.5 / 30.8 / 50.5 / 76.6 / 129.3, 512 threads 18.4 / 20.3 / 27.2 /
+    // 29.2 / 48.3 / 75.0 / 127.7, the split form 17.1 / 20.9. 64 lanes per row
+    // (other sums) were faster at one position only (17.0-17.3) and slower from
+    // two (21.1 / 29.0 / 33.6 / 50.6 / 79.0 / 135.3). RQMV_MOE_DOWN_WIDE=0/1 and
+    // RQMV_MOE_DOWN_THREADS override the workgroup size, RQMV_MOE_DOWN_SPLIT=0/1
+    // the split form (one or two positions, 32 lanes).
+    int threads = env_flag("RQMV_MOE_DOWN_WIDE", b.m >= 2) ? 512 : kMoeThreads;
+    const char* tenv = getenv("RQMV_MOE_DOWN_THREADS");
+    if (tenv && *tenv) {
+        const int v = atoi(tenv);
+        if (v == 256 || v == 512 || v == 1024) threads = v;
+    }
     const int rows_per_block = threads / 64 * (64 / G);
     int grid = (d.d_model + rows_per_block - 1) / rows_per_block;
-    const int cap = batch_grid_cap(cus, b.m);
+    const int cap = (batch_grid_cap(cus, b.m) * kMoeThreads + threads - 1) / threads;
     if (grid > cap) grid = cap;
     const size_t lds = stage_bytes_int(FMT, 1, nch);
-    auto kernel = b.m > kMoeOwnRouteMax ? moe_down_kernel<FMT, true>
-                  : wide                ? moe_down_kernel<FMT, false, 512>
-                                        : moe_down_kernel<FMT, false>;
+    const bool ring = b.m > kMoeOwnRouteMax;
+    auto kernel = ring ? (threads == 1024 ? moe_down_kernel<FMT, true, 1024>
+                          : threads == 512 ? moe_down_kernel<FMT, true, 512>
+                                           : moe_down_kernel<FMT, true>)
+                       : (threads == 1024 ? moe_down_kernel<FMT, false, 1024>
+                          : threads == 512 ? moe_down_kernel<FMT, false, 512>
+                                           : moe_down_kernel<FMT, false>);
+    // the split form: one row per wave on 512-thread workgroups
+    if (!ring && G == 32 && env_flag("RQMV_MOE_DOWN_SPLIT", b.m == 1)) {
+        threads = 512;
+        grid = (d.d_model + threads / 64 - 1) / (threads / 64);
+        const int scap = (batch_grid_cap(cus, b.m) * kMoeThreads + threads - 1) / threads;
+        if (grid > scap) grid = scap;
+        kernel = moe_down_kernel<FMT, false, 512, true>;
+    }
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
