@@ -41,6 +41,19 @@ __device__ __forceinline__ int stage_items(int nch, int M) {
     return M * nch * Traits<FMT>::BLK * 4;
 }
 
+// Item u's row m, chunk c, block b and quarter q. At one activation row (M a
+// constant 1 after inlining) no division by the chunk count is needed.
+struct StagePos {
+    int m, c, b, q;
+};
+template <int FMT>
+__device__ __forceinline__ StagePos stage_pos(int u, int nch, int M) {
+    constexpr int BLK = Traits<FMT>::BLK;
+    const int cb = u >> 2, mc = cb / BLK;
+    const int m = M == 1 ? 0 : mc / nch;
+    return StagePos{m, mc - m * nch, cb % BLK, u & 3};
+}
+
 inline int stage_items_host(int fmt, int64_t nch, int M) {
     return (int)(M * nch * (fmt == Q8_0 ? 1 : 2) * 4);
 }
@@ -62,10 +75,10 @@ struct NormIn {
 };
 
 template <int FMT, bool XF32, bool NORM = false>
-__device__ __forceinline__ void stage_issue(int u, int nch, int K, const void* xv, int64_t ldx,
+__device__ __forceinline__ void stage_issue(int u, int nch, int M, int K, const void* xv, int64_t ldx,
                                             StageItem<XF32, NORM>& it, const NormIn& nin = NormIn{}) {
-    constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK;
-    const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
+    constexpr int CW = Traits<FMT>::CW;
+    const auto [m, c, b, q] = stage_pos<FMT>(u, nch, M);
     int k0 = c * CW + b * 32 + q * 8;
     k0 = k0 < K ? k0 : K - 8;
     if constexpr (XF32) {
@@ -120,7 +133,9 @@ __device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* ou
 // the integer sum of the eight in `sum`; returns the block scale amax / 30583.
 template <int FMT>
 __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, uint32_t (&w4)[4], int& sum) {
-    const float inv = amax > 0.f ? kXMax / amax : 0.f;
+    // the hardware reciprocal (within one ulp): x moves by at most 30583 *
+    // 2^-22 of a step against a correctly rounded quotient
+    const float inv = amax > 0.f ? kXMax * __builtin_amdgcn_rcpf(amax) : 0.f;
     int xi[8];
     sum = 0;
 #pragma unroll
@@ -152,10 +167,11 @@ __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, ui
 // run it together (the block maximum and sums move through DPP).
 // Returns whether the item's block holds an outlier.
 template <int FMT, bool XF32, bool NORM = false>
-__device__ __forceinline__ bool stage_finish(int u, int nch, int K, const StageItem<XF32, NORM>& it, uint4* xd,
-                                             float* xbf, const NormIn& nin = NormIn{}, float* ss = nullptr) {
+__device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const StageItem<XF32, NORM>& it,
+                                             uint4* xd, float* xbf, const NormIn& nin = NormIn{},
+                                             float* ss = nullptr) {
     constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP;
-    const int q = u & 3, cb = u >> 2, b = cb % BLK, mc = cb / BLK, c = mc % nch, m = mc / nch;
+    const auto [m, c, b, q] = stage_pos<FMT>(u, nch, M);
     const bool live = c * CW + b * 32 < K;
     float v[8];
     if constexpr (XF32) {
@@ -334,7 +350,7 @@ __device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x,
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
         const int u = (int)threadIdx.x + j * nthreads;
-        stage_issue<FMT, XF32, NORM>(u < total ? u : (int)threadIdx.x % 4, nch, K, x, ldx, it[j], nin);
+        stage_issue<FMT, XF32, NORM>(u < total ? u : (int)threadIdx.x % 4, nch, M, K, x, ldx, it[j], nin);
     }
 }
 
@@ -347,7 +363,7 @@ __device__ __forceinline__ bool stage_multi_finish(int nch, int K, int M, int nt
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
         const int u = (int)threadIdx.x + j * nthreads;
-        if (u < total) out |= stage_finish<FMT, XF32, NORM>(u, nch, K, it[j], xd, xbf, nin, ss);
+        if (u < total) out |= stage_finish<FMT, XF32, NORM>(u, nch, M, K, it[j], xd, xbf, nin, ss);
     }
     return out;
 }
@@ -360,8 +376,8 @@ __device__ __forceinline__ bool stage_all(int nch, int K, const void* x, int64_t
     bool out = false;
     for (int u = threadIdx.x; u < total; u += nthreads) {
         StageItem<XF32, NORM> it;
-        stage_issue<FMT, XF32, NORM>(u, nch, K, x, ldx, it, nin);
-        out |= stage_finish<FMT, XF32, NORM>(u, nch, K, it, xd, xbf, nin, ss);
+        stage_issue<FMT, XF32, NORM>(u, nch, M, K, x, ldx, it, nin);
+        out |= stage_finish<FMT, XF32, NORM>(u, nch, M, K, it, xd, xbf, nin, ss);
     }
     return out;
 }

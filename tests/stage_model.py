@@ -3,7 +3,8 @@ kernels (recipe-dev_amd/csrc/stage.h), test infrastructure.
 
 Every 32-value block of an activation row becomes 16-bit integers
 x_i = clamp(rint(v_i * (30583 / amax)), -30583, 30583) with the block scale
-s = amax * fp32(1 / 30583); the kernels' products are exact integer dots of
+s = amax * fp32(1 / 30583) (the kernels form 30583 / amax as 30583 times the
+hardware reciprocal, within one ulp of 1 / amax; the model divides); the kernels' products are exact integer dots of
 these against the weights' integer codes, scaled per block in fp32, so the
 activation a kernel multiplies is s * x_i. With outlier extraction, a block
 whose largest magnitude exceeds `threshold` times its second largest has that
@@ -13,7 +14,8 @@ itself is multiplied exactly (in fp32) with its weight.
 
 The functions return the effective activations and the error bound they
 obey: |v_i - s x_i| <= 0.51 s for every encoded value (half a step, plus the
-fp32 roundings of v * inv and of s, each below 2^-23 * 30583 steps), i.e.
+fp32 roundings of v * inv and of s, and the reciprocal's error, each below
+2^-22 * 30583 steps), i.e.
 about (the block's scaling magnitude) / 60000.
 """
 from __future__ import annotations
