@@ -1,9 +1,9 @@
 // Activation staging into LDS, shared by the matvec and MoE kernels.
 //
 // Quantized weights (integer kernels). Each 32-value block b of an activation
-// row becomes 16-bit integers x = rint(v * 30583 / max|v|) with scale
-// s_b = max|v| / 30583, so every value is within s_b / 2 (1.64e-5 of the
-// block's largest magnitude) of s_b x. A block whose largest magnitude is more
+// row becomes 16-bit integers x = rint(v / s_b) with scale s_b = max|v| / 30583,
+// so every value is within s_b / 2 (1.64e-5 of the block's largest magnitude)
+// of s_b x. A block whose largest magnitude is more
 // than kOutlierRatio times its second largest has that one value taken out
 // (encoded as 0, the block scaled by the second largest): it goes to the
 // block's outlier slot and the kernels multiply it exactly in fp32 with its
@@ -127,29 +127,42 @@ __device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* ou
     out[3] = __builtin_amdgcn_perm(D, C, 0x07050301u);
 }
 
-// Encodes eight values of a 32-value block whose maximum magnitude is amax:
-// x = rint(v * 30583 / amax) as digit words (nibble formats: four words, one
-// per balanced hex digit; Q8_0: two low-byte words, then two high-byte words),
-// the integer sum of the eight in `sum`; returns the block scale amax / 30583.
+// Encodes eight values of a 32-value block whose maximum magnitude is amax
+// (the values finite, |v| <= amax): x = rint(v / s) with the block scale
+// s = amax / 30583, as digit words (nibble formats: four words, one per
+// balanced hex digit; Q8_0: two low-byte words, then two high-byte words), the
+// integer sum of the eight in `sum`; returns s. 1 / s is the hardware
+// reciprocal (within one ulp), so |v / s| stays below 30583.5 and needs no
+// clamp. A block whose step would fall below the smallest normal float (amax
+// under 30583 * 2^-126) takes the step 2^-126. The rounding is one fma with
+// 1.5 * 2^23, whose sum holds 2^23 + 2^22 + rint(v / s) (to nearest even) in
+// its low bits; x's low 16 bits are those of the sum's bit pattern, and the
+// digit split only uses those.
 template <int FMT>
 __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, uint32_t (&w4)[4], int& sum) {
-    // the hardware reciprocal (within one ulp): x moves by at most 30583 *
-    // 2^-22 of a step against a correctly rounded quotient
-    const float inv = amax > 0.f ? kXMax * __builtin_amdgcn_rcpf(amax) : 0.f;
-    int xi[8];
-    sum = 0;
+    constexpr uint32_t kMagicBits = 0x4B400000u;  // 1.5 * 2^23
+    float s = amax * (1.0f / kXMax);
+    float inv;
+    if (__builtin_expect(s < 0x1p-126f, 0)) {  // (zero or tiny blocks)
+        inv = amax > 0.f ? 0x1p126f : 0.f;
+        s = amax > 0.f ? 0x1p-126f : 0.f;
+    } else {
+        inv = __builtin_amdgcn_rcpf(s);
+    }
+    uint32_t xb[8];
+    uint32_t usum = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const int t = (int)__builtin_rintf(v[k] * inv);
-        xi[k] = t < -30583 ? -30583 : (t > 30583 ? 30583 : t);
-        sum += xi[k];
+        xb[k] = __builtin_bit_cast(uint32_t, fmaf(v[k], inv, 12582912.0f));
+        usum += xb[k];
     }
+    sum = (int)(usum - 8u * kMagicBits);
     if constexpr (FMT == Q8_0) {
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             uint32_t uu[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) uu[e] = ((uint32_t)(xi[4 * w + e] + 0x8080) ^ 0x8080u) & 0xffffu;
+            for (int e = 0; e < 4; ++e) uu[e] = ((xb[4 * w + e] + 0x8080u) ^ 0x8080u) & 0xffffu;
             const uint32_t pa = uu[0] | (uu[1] << 16), pb = uu[2] | (uu[3] << 16);
             w4[w] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
             w4[2 + w] = __builtin_amdgcn_perm(pb, pa, 0x07050301u);
@@ -157,10 +170,10 @@ __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, ui
     } else {
         uint32_t uu[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) uu[e] = (uint32_t)(xi[e] + 0x8888) ^ 0x8888u;
+        for (int e = 0; e < 8; ++e) uu[e] = (xb[e] + 0x8888u) ^ 0x8888u;
         nibble_transpose(uu, w4);
     }
-    return amax * (1.0f / kXMax);
+    return s;
 }
 
 // Encodes item u and stores it into LDS. Every lane of the item's quad must

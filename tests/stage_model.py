@@ -2,9 +2,10 @@
 kernels (recipe-dev_amd/csrc/stage.h), test infrastructure.
 
 Every 32-value block of an activation row becomes 16-bit integers
-x_i = clamp(rint(v_i * (30583 / amax)), -30583, 30583) with the block scale
-s = amax * fp32(1 / 30583) (the kernels form 30583 / amax as 30583 times the
-hardware reciprocal, within one ulp of 1 / amax; the model divides); the kernels' products are exact integer dots of
+x_i = rint(v_i / s) with the block scale s = amax * fp32(1 / 30583) (2^-126 for
+blocks whose step would fall below the smallest normal float), rounded once
+from the exact product of v_i and 1 / s (the kernels form 1 / s with the
+hardware reciprocal, within one ulp; the model divides); the kernels' products are exact integer dots of
 these against the weights' integer codes, scaled per block in fp32, so the
 activation a kernel multiplies is s * x_i. With outlier extraction, a block
 whose largest magnitude exceeds `threshold` times its second largest has that
@@ -45,9 +46,13 @@ def encode_block(v: np.ndarray, threshold: float | None = None):
             amax = amax2
     if not np.isfinite(amax) or not np.isfinite(v).all():
         return np.full(v.shape, np.nan, np.float32), np.float32(np.nan), -1, np.float32(0)
-    inv = XMAX / amax if amax > 0 else np.float32(0)
-    x = np.clip(np.rint(v * np.float32(inv)), -30583, 30583).astype(np.float32)
     s = np.float32(amax * INV_XMAX)
+    if s < np.float32(2.0 ** -126):  # zero or tiny blocks: the step 2^-126
+        s = np.float32(2.0 ** -126) if amax > 0 else np.float32(0)
+    inv = np.float32(1) / s if s > 0 else np.float32(0)
+    # one rounding of the exact product (the kernel's fma); no clamp is needed
+    x = np.rint(v.astype(np.float64) * np.float64(inv)).astype(np.float32)
+    assert np.abs(x).max(initial=0) <= 30583
     eff = (s * x).astype(np.float32)
     if out_i >= 0:
         eff[out_i] = out_v
