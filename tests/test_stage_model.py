@@ -74,3 +74,22 @@ def test_ties_and_single_values():
     x[17] = -3.25
     eff, s, i, v = sm.encode_block(x, 4.0)
     assert i == 17 and v == np.float32(-3.25) and np.array_equal(eff, x)
+
+
+def test_extreme_block_magnitudes():
+    """Blocks at the ends of the fp32 range. The largest keep the half-step
+    bound (the reciprocal of their step stays a normal float); blocks whose
+    step would fall below the smallest normal float take the step 2^-126,
+    so their values keep an absolute error of at most 2^-127."""
+    for scale in (1e37, 7.5e37):
+        x = (RNG.uniform(-1, 1, 32) * scale).astype(np.float32)
+        eff, s, _, _ = sm.encode_block(x)
+        assert np.isfinite(s) and s > 0
+        assert np.all(np.abs(eff.astype(np.float64) - x) <= 0.51 * float(s))
+    for scale in (1e-35, 1e-38, 1e-44):
+        x = (RNG.uniform(-1, 1, 32) * scale).astype(np.float32)
+        eff, s, _, _ = sm.encode_block(x)
+        assert s == np.float32(2.0 ** -126)
+        assert np.all(np.abs(eff.astype(np.float64) - x) <= 2.0 ** -127)
+    eff, s, _, _ = sm.encode_block(np.zeros(32, np.float32))
+    assert s == 0 and not eff.any()
