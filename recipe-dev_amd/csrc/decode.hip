@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "decode.h"
 #include "stage.h"
 
@@ -369,69 +371,77 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
             jsel = jn / PPS;  // (the sweep whose key and value this lane takes from k16, v16)
         }
     }
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qr[g][e] = g < group ? qr[g][e] : 0.f;
+    // Query heads past the group (g >= group) compute on a copy of the group's
+    // last head; their results are never written.
 
-    // pass 1: each lane's positions' scores (every lane of a position holds them)
-    float s[NS][MAXG];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        float kv[8];
-        unpack8(j == jsel ? k16 : kr[j], kv);
-        const bool live = t0 + slot + j * PPS < len;
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kv[e], d);
-            d = sum_lanes<LPP>(d);
-            s[j][g] = live ? d * scale : -INFINITY;
-        }
-    }
-
-    // pass 2, per wave: each head's maximum mw over the wave's positions (the
-    // lane's sweeps, then the wave's position slots across lanes), weights
-    // e = exp(s - mw) and their sum lw, all in registers; the chunk's waves
-    // are merged at the end
-    float mw[MAXG], lw[MAXG];
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g) {
-        float m = s[0][g];
-#pragma unroll
-        for (int j = 1; j < NS; ++j) m = fmaxf(m, s[j][g]);
-        mw[g] = slots_max<LPP>(m);
-        float l = 0.f;
+    // The passes, in two forms: a chunk wholly before the new position (every
+    // position live, none replaced by the new key and value) needs none of the
+    // selections that mask dead positions or substitute the new entry; the
+    // chunk holding the position, or past the cache's end, takes them. The
+    // results are the same either way.
+    float s[NS][MAXG], mw[MAXG], lw[MAXG], o[MAXG][8];
+    auto passes = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        // pass 1: each lane's positions' scores (every lane of a position holds them)
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            s[j][g] = s[j][g] == -INFINITY ? 0.f : __expf(s[j][g] - mw[g]);
-            l += s[j][g];
+            float kv[8];
+            unpack8(!FULL && j == jsel ? k16 : kr[j], kv);
+            const bool live = FULL || t0 + slot + j * PPS < len;
+#pragma unroll
+            for (int g = 0; g < MAXG; ++g) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kv[e], d);
+                d = sum_lanes<LPP>(d);
+                s[j][g] = live ? d * scale : -INFINITY;
+            }
         }
-        lw[g] = slots_sum<LPP>(l);
-    }
 
-    // pass 3: o = sum_p e_p v_p over this lane's positions, then over the lanes
-    // holding the same eight values (across the wave, then across waves)
-    float o[MAXG][8];
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        float vv[8];
-        unpack8(j == jsel ? v16 : vr[j], vv);
-        const bool live = t0 + slot + j * PPS < len;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vv[e] = live ? vv[e] : 0.f;
+        // pass 2, per wave: each head's maximum mw over the wave's positions (the
+        // lane's sweeps, then the wave's position slots across lanes), weights
+        // e = exp(s - mw) and their sum lw, all in registers; the chunk's waves
+        // are merged at the end
 #pragma unroll
         for (int g = 0; g < MAXG; ++g) {
-            const float wgt = g < group ? s[j][g] : 0.f;
+            float m = s[0][g];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[g][e] = fmaf(wgt, vv[e], o[g][e]);
+            for (int j = 1; j < NS; ++j) m = fmaxf(m, s[j][g]);
+            mw[g] = slots_max<LPP>(m);
+            float l = 0.f;
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                s[j][g] = !FULL && s[j][g] == -INFINITY ? 0.f : __expf(s[j][g] - mw[g]);
+                l += s[j][g];
+            }
+            lw[g] = slots_sum<LPP>(l);
         }
-    }
+
+        // pass 3: o = sum_p e_p v_p over this lane's positions, then over the lanes
+        // holding the same eight values (across the wave, then across waves)
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            float vv[8];
+            unpack8(!FULL && j == jsel ? v16 : vr[j], vv);
+            if constexpr (!FULL) {
+                const bool live = t0 + slot + j * PPS < len;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vv[e] = live ? vv[e] : 0.f;
+            }
+#pragma unroll
+            for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[g][e] = fmaf(s[j][g], vv[e], o[g][e]);
+        }
+    };
+    // (wholly inside the live length and, under ROPE, wholly before the new
+    // position)
+    if (t0 + kAttnChunk <= (ROPE ? min(pos, len) : len)) passes(std::true_type{});
+    else passes(std::false_type{});
     if constexpr (kSlotRows) {
         // every lane's sums go to its slot's row; each output then adds the
         // rows in slot order (fewer instructions than lane exchanges)
