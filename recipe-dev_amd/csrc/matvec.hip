@@ -443,6 +443,15 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     const bool long_rows = nch > 128;
     s.block = long_rows ? 512 : 256;
     int per_cu = long_rows ? 1 : 2;
+    // Long Q4_K rows at one fp16 activation row: 32 lanes per row and one row
+    // per lane group (two rows per wave, seven steps each at 14336 columns)
+    // measured faster than 64 lanes and two rows per group: Q4_K 14336->4096
+    // kernel 10.37 -> 10.00 us (three alternating pairs). With fp32 rows (the
+    // decode step's down product) it was slower: 568 -> 548 tok/s.
+    if (fmt == Q4_K && M == 1 && long_rows && xtype == X_F16) {
+        s.G = 32;
+        s.R = 1;
+    }
     // Small products at one or two activation rows, whose tiles would not give
     // every CU a workgroup, spread them over smaller workgroups of one row per
     // lane group (the MoE router, 257 x 2048 F16: 17 -> 65 workgroups; the MoE
