@@ -250,6 +250,40 @@ def test_wide_dynamic_range_f32(gpu, fmt, m):
         assert err <= 2e-4, (r, err)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_block_magnitude_extremes_f32(gpu, fmt, m):
+    """fp32 blocks at the ends of the float range among N(0,1) blocks: one
+    whose two largest magnitudes are 1e38 and 9e37 (its step is 3.3e33, whose
+    reciprocal is a normal float, while the reciprocal of 1e38 itself would
+    not be), and one of magnitudes near 1e-36 (below 3.6e-34, where the
+    integer kernels take the smallest normal step 2^-126)."""
+    rows, cols = 200, 2048
+    w = _weights(fmt, rows, cols, seed=150 + m).copy()
+    # a small scale (fp16 2^-10; Q6_K 2^-14) on the GGUF block holding the
+    # huge columns, so that every product, and recipe's own sum, stays finite
+    bv, bb = synth.BLOCK[fmt]
+    blk = w.reshape(rows, cols // bv, bb)[:, 165 // bv]
+    small = np.array([0x0400 if fmt == "q6_k" else 0x1400], dtype=np.uint16).view(np.uint8)
+    at = 208 if fmt == "q6_k" else 0
+    blk[:, at:at + 2] = small
+    if fmt == "q4_k":
+        blk[:, 2:4] = small  # dmin
+    W = gpu.Weight(fmt, rows, cols, w)
+    rng = np.random.default_rng(151 + m)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    x[:, 96:128] *= np.float32(1e-36)
+    x[:, 165] = np.float32(1e38)
+    x[:, 170] = np.float32(-9e37)
+    y = _run_matvec(gpu, W, x, 0, rows)
+    ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x, threads=THREADS)
+    assert np.isfinite(ref).all()
+    for r in range(m):
+        err = rel_l2(y[r], ref[r])
+        print(f"block extremes {fmt} m={m} row {r}: rel-L2 {err:.2e}", flush=True)
+        assert err <= 2e-4, (r, err)
+
+
 @pytest.mark.parametrize("m", [3, 16, 32])
 @pytest.mark.parametrize("scale", [1e-6, 1e5])
 def test_matrix_cores_f32_extreme_scales(gpu, m, scale):
