@@ -301,8 +301,8 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     const int t0 = chunk * kAttnChunk;
     // Every load is issued before the first wait. The queries and, under ROPE,
     // the new key and value do not depend on the position, so they go out
-    // while it is read; slots past the group read the group's last head and
-    // are zeroed below.
+    // while it is read; slots past the group read the group's last head (their
+    // results are never written).
     float qr[MAXG][8];
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) load8(q + (size_t)(kh * group + min(g, group - 1)) * HD + b * 8, qr[g]);
@@ -371,9 +371,6 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
             jsel = jn / PPS;  // (the sweep whose key and value this lane takes from k16, v16)
         }
     }
-    // Query heads past the group (g >= group) compute on a copy of the group's
-    // last head; their results are never written.
-
     // The passes, in two forms: a chunk wholly before the new position (every
     // position live, none replaced by the new key and value) needs none of the
     // selections that mask dead positions or substitute the new entry; the
