@@ -616,18 +616,21 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
         const int g = atoi(genv);
         if (g == 8 || g == 16 || g == 32 || g == 64) G = g;
     }
-    // From two positions, 512-thread workgroups, each staging the slot
-    // activations once for twice the rows; at one position, the split form
-    // below. Each row's sum is the same in every form, so batches stay
-    // bit-identical to one-position calls. Measured on the gguf_moe workload,
-    // us per step at 1 / 2 / 3 / 4 / 8 / 16 / 32 positions: 256 threads 18.2 /
-    // 21.5 / 27.5 / 30.8 / 50.5 / 76.6 / 129.3, 512 threads 18.4 / 20.3 / 27.2 /
-    // 29.2 / 48.3 / 75.0 / 127.7, the split form 17.1 / 20.9. 64 lanes per row
-    // (other sums) were faster at one position only (17.0-17.3) and slower from
-    // two (21.1 / 29.0 / 33.6 / 50.6 / 79.0 / 135.3). RQMV_MOE_DOWN_WIDE=0/1 and
-    // RQMV_MOE_DOWN_THREADS override the workgroup size, RQMV_MOE_DOWN_SPLIT=0/1
-    // the split form (one or two positions, 32 lanes).
-    int threads = env_flag("RQMV_MOE_DOWN_WIDE", b.m >= 2) ? 512 : kMoeThreads;
+    // At two positions 512-thread workgroups, from three 1024-thread ones,
+    // each staging the slot activations once for more rows; at one position,
+    // the split form below. Each row's sum is the same in every form, so
+    // batches stay bit-identical to one-position calls. Measured on the
+    // gguf_moe workload, us per step at 1 / 2 / 3 / 4 / 8 / 16 / 32 positions:
+    // 256 threads 18.2 / 21.5 / 27.5 / 30.8 / 50.5 / 76.6 / 129.3, 512 threads
+    // 18.4 / 20.3 / 27.2 / 29.2 / 48.3 / 75.0 / 127.7, the split form 17.1 /
+    // 20.9; after cheaper staging, 512 against 1024 threads from two
+    // positions: 19.8 / 26.7 / 28.6 / 47.0 / 73.7 / 126.6 against 21.1 / 25.9
+    // / 27.8 / 46.0 / 73.3 / 126.5. 64 lanes per row (other sums) were faster
+    // at one position only (17.0-17.3) and slower from two (21.1 / 29.0 / 33.6
+    // / 50.6 / 79.0 / 135.3). RQMV_MOE_DOWN_WIDE=0/1 and RQMV_MOE_DOWN_THREADS
+    // override the workgroup size, RQMV_MOE_DOWN_SPLIT=0/1 the split form (one
+    // or two positions, 32 lanes).
+    int threads = env_flag("RQMV_MOE_DOWN_WIDE", b.m >= 2) ? (b.m >= 3 ? 1024 : 512) : kMoeThreads;
     const char* tenv = getenv("RQMV_MOE_DOWN_THREADS");
     if (tenv && *tenv) {
         const int v = atoi(tenv);
