@@ -255,7 +255,14 @@ __device__ __forceinline__ void route_wave(const MoeDims& d, const MoeWorkspace&
 // RING (batches): two buffers of weights, the next tile's requested before
 // the current one is computed. One or two positions run one tile per wave,
 // where the single buffer holds fewer registers and measured faster.
-template <int FMT, bool XF32, int S, bool RING>
+//
+// Each row's gate and up sums add one partial per chunk (each chunk's dot
+// formed from zero), in the chunk order of G lanes per row pair (lane g:
+// chunks g, g + G, ...). GSPLIT (one position) runs 2G lanes per row pair with
+// those sums: lane g < G adds its chunk's partials and then, through a lane
+// swap, those of lane g + G (chunk g + G), so every row carries the bits of
+// the G-lane form with twice the lanes.
+template <int FMT, bool XF32, int S, bool RING, bool GSPLIT = false>
 __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank gate, MoeBank up, MoeBank gate_sh,
                                                        MoeBank up_sh, const void* x, MoeWorkspace ws, float* route_dense,
                                                        int G, MoeBatch batch) {
@@ -314,6 +321,62 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, kMoeThreads);
+    // one chunk's gate and up partials, each formed from zero
+    auto partials = [&](int c, const ChunkData<FMT>& dg, const ChunkData<FMT>& du, float& pg, float& pu) {
+        uint4 xv[XP];
+        uint4 bv[2];
+#pragma unroll
+        for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+        bv[0] = xb[c];
+        bv[1] = xb[nch + c];
+        pg = 0.f;
+        pu = 0.f;
+        dot_int<FMT>(dg, c, xv, bv, pg);
+        dot_int<FMT>(du, c, xv, bv, pu);
+        if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
+            const uint4 o = xb[2 * nch + c];
+            dot_outliers<FMT>(dg, c, o, pg);
+            dot_outliers<FMT>(du, c, o, pu);
+        }
+    };
+    if constexpr (GSPLIT) {
+        const int GE = G >> 1;  // the lanes whose sums every row carries
+        bool fetched = true;
+        for (; tile < tiles; tile += stride) {
+            const int r = tile * rows_per_wave + sub;
+            float ag = 0.f, au = 0.f;
+            for (int c0 = 0; c0 < nch; c0 += G) {
+                const int c = c0 + g;
+                if (!fetched) fetch(r, c, dg0, du0);
+                fetched = false;
+                float pg = 0.f, pu = 0.f;
+                if (c < nch) partials(c, dg0, du0, pg, pu);
+                // (lo, hi): lane g's and lane g + GE's partials, in every lane g < GE
+                float gl = pg, gh = pg, ul = pu, uh = pu;
+                if (GE == 16) {
+                    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(gl), "+v"(gh));
+                    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(ul), "+v"(uh));
+                } else {
+                    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(gl), "+v"(gh));
+                    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(ul), "+v"(uh));
+                }
+                if (g < GE) {
+                    if (c < nch) {
+                        ag += gl;
+                        au += ul;
+                    }
+                    if (c + GE < nch) {
+                        ag += gh;
+                        au += uh;
+                    }
+                }
+            }
+            ag = group_sum(ag, GE);
+            au = group_sum(au, GE);
+            if (r < total_rows && g == GE - 1) ws.h[r] = act_apply_likely_silu(d.activation, d.act_factor, ag) * au;
+        }
+        return;
+    }
     if constexpr (!RING) {
         bool fetched = true;
         for (; tile < tiles; tile += stride) {
@@ -322,19 +385,10 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
             for (int c = g; c < nch; c += G) {
                 if (!fetched) fetch(r, c, dg0, du0);
                 fetched = false;
-                uint4 xv[XP];
-                uint4 bv[2];
-#pragma unroll
-                for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
-                bv[0] = xb[c];
-                bv[1] = xb[nch + c];
-                dot_int<FMT>(dg0, c, xv, bv, ag);
-                dot_int<FMT>(du0, c, xv, bv, au);
-                if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
-                    const uint4 o = xb[2 * nch + c];
-                    dot_outliers<FMT>(dg0, c, o, ag);
-                    dot_outliers<FMT>(du0, c, o, au);
-                }
+                float pg, pu;
+                partials(c, dg0, du0, pg, pu);
+                ag += pg;
+                au += pu;
             }
             ag = group_sum(ag, G);
             au = group_sum(au, G);
@@ -350,19 +404,10 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
         float ag = 0.f, au = 0.f;
         for (int c = g; c < nch; c += G) {
             if (c != g) fetch(r, c, dg, du);  // a row longer than one chunk per lane
-            uint4 xv[XP];
-            uint4 bv[2];
-#pragma unroll
-            for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
-            bv[0] = xb[c];
-            bv[1] = xb[nch + c];
-            dot_int<FMT>(dg, c, xv, bv, ag);
-            dot_int<FMT>(du, c, xv, bv, au);
-            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
-                const uint4 o = xb[2 * nch + c];
-                dot_outliers<FMT>(dg, c, o, ag);
-                dot_outliers<FMT>(du, c, o, au);
-            }
+            float pg, pu;
+            partials(c, dg, du, pg, pu);
+            ag += pg;
+            au += pu;
         }
         ag = group_sum(ag, G);
         au = group_sum(au, G);
@@ -546,20 +591,28 @@ static hipError_t glu_launch(const MoeDims& d, const MoeBank& gate, const MoeBan
         const int g = atoi(glu_genv);
         if (g == 8 || g == 16 || g == 32 || g == 64) G = g;
     }
+    // At one position, twice the lanes with the same sums (GSPLIT): 32 lanes
+    // per row pair in the 16-lane sum order, 16.78 -> 16.43 us per step (two
+    // alternating pairs; two and four positions unchanged with the partial
+    // sums). RQMV_MOE_GLU_SPLIT=0/1 overrides it.
+    const bool split = (G == 16 || G == 32) && env_flag("RQMV_MOE_GLU_SPLIT", b.m == 1) && b.m <= kMoeOwnRouteMax;
+    const int GL = split ? 2 * G : G;  // lanes per row pair in the launch
     const int total_rows = d.top * d.hidden + d.hidden_shared;
-    const int rows_per_block = 4 * (64 / G);
+    const int rows_per_block = 4 * (64 / GL);
     int grid = (total_rows + rows_per_block - 1) / rows_per_block;
     const int cap = batch_grid_cap(cus, b.m);
     if (grid > cap) grid = cap;
     const size_t lds = stage_bytes_int(FMT, 1, nch);
-    auto kernel = b.m > kMoeOwnRouteMax ? moe_glu_kernel<FMT, XF32, S, true> : moe_glu_kernel<FMT, XF32, S, false>;
+    auto kernel = b.m > kMoeOwnRouteMax ? moe_glu_kernel<FMT, XF32, S, true>
+                  : split                ? moe_glu_kernel<FMT, XF32, S, false, true>
+                                         : moe_glu_kernel<FMT, XF32, S, false>;
     if (lds > 60000) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(kernel, dim3(grid, b.m), dim3(kMoeThreads), lds, stream, d, gate, up, gate_sh, up_sh, x, ws,
-                       route_dense, G, b);
+                       route_dense, GL, b);
     return hipGetLastError();
 }
 
