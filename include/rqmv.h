@@ -152,9 +152,13 @@ typedef struct {
     int renormalize;    /* divide the kept weights by their total */
     float scale;        /* routed weight scale (1 = none) */
     int activation;     /* rqmv_activation of every expert: act(gate x) * (up x) (lower_gated,
-                           recipe.rs:23279-23286); RQMV_ACT_SILU for llama-style experts */
+                           recipe.rs:23279-23286); RQMV_ACT_SILU for llama-style experts.
+                           Code 0 is RQMV_ACT_LINEAR: a zero-initialised struct gets linear
+                           experts and a linear shared gate, so set both codes explicitly
+                           (RQMV_ACT_SILU and RQMV_ACT_SIGMOID for llama-style blocks) */
     int shared_gate_activation; /* rqmv_activation of the shared gate (SharedExpert::Gated's gate) */
-    float activation_factor;    /* RQMV_ACT_SCALE's constant, RQMV_ACT_PRELU's slope (else unused) */
+    float activation_factor;    /* RQMV_ACT_SCALE's constant, RQMV_ACT_PRELU's slope (else unused);
+                                   must be finite when either code uses it, else RQMV_EINVAL */
     const float* selection_bias; /* device, experts fp32 values (exp_probs_b.bias) or NULL: the top-k
                                     key becomes the expert's probability plus its bias, the weights
                                     stay those of the unbiased scores (topk_key, amd-nv-cpu.ll:4653-4660) */

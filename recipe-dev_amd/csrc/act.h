@@ -6,8 +6,7 @@
 // scale sqrt(2/pi) and cubic 0.044715, Huber threshold 1. Codes are
 // Activation::code() (recipe.rs:13925-13950); kActGeluFp16 is Gelu as the
 // llama.cpp profile's gelu table runs it (the input and the result rounded to
-// fp16 inside (-10, 10), the input itself at 10 and above, zero at -10 and
-// below). `factor` is Scale's constant and PReLU's slope.
+// fp16 inside [-10, 10], the input itself above 10, zero below -10). `factor` is Scale's constant and PReLU's slope.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -62,12 +62,13 @@ __device__ __forceinline__ int sbfe(uint32_t v, uint32_t off, uint32_t width) {
 //   CW  weights per chunk          QP  16-byte code parts per chunk
 //   XP  16-byte activation parts per chunk (digit words, or fp16 pairs for F16)
 //   BLK 32-value activation blocks per chunk
+//   XR  16-byte rows of staged block data per chunk (2 + one outlier row per block)
 template <int FMT> struct Traits;
-template <> struct Traits<Q8_0> { static constexpr int CW = 32, QP = 2, XP = 4, BLK = 1; };
-template <> struct Traits<Q4_0> { static constexpr int CW = 64, QP = 2, XP = 8, BLK = 2; };
-template <> struct Traits<Q4_K> { static constexpr int CW = 64, QP = 2, XP = 8, BLK = 2; };
-template <> struct Traits<Q6_K> { static constexpr int CW = 64, QP = 3, XP = 8, BLK = 2; };
-template <> struct Traits<F16> { static constexpr int CW = 64, QP = 8, XP = 8, BLK = 2; };
+template <> struct Traits<Q8_0> { static constexpr int CW = 32, QP = 2, XP = 4, BLK = 1, XR = 3; };
+template <> struct Traits<Q4_0> { static constexpr int CW = 64, QP = 2, XP = 8, BLK = 2, XR = 4; };
+template <> struct Traits<Q4_K> { static constexpr int CW = 64, QP = 2, XP = 8, BLK = 2, XR = 4; };
+template <> struct Traits<Q6_K> { static constexpr int CW = 64, QP = 3, XP = 8, BLK = 2, XR = 4; };
+template <> struct Traits<F16> { static constexpr int CW = 64, QP = 8, XP = 8, BLK = 2, XR = 0; };
 
 // One chunk's weight data as loaded from HBM.
 template <int FMT> struct ChunkData {
@@ -211,8 +212,8 @@ __device__ __forceinline__ int dot_nibbles4(const uint4& W, const uint4* xd, int
 // -------------------------------------------------------------------------
 // Integer dot of one chunk for one activation row. xd[] holds the chunk's
 // activation digit words as staged (Traits::XP parts), xb[] its block data:
-// xb[0] = (s_0, s_1, sx_0, sx_1), xb[1] = (sx_2, sx_3, 0, 0), where s_b is
-// block b's scale (its sign bit set when the chunk holds an outlier) and sx
+// xb[0] = (s_0, s_1, sx_0, sx_1), xb[1] = (sx_2, sx_3, idx_0, idx_1), where s_b is
+// block b's scale (its sign bit set when the block has extracted values) and sx
 // the scaled activation sums (per 32-block for Q4_K, per 16-value scale group
 // for Q6_K). Accumulates sum_j w_j x_j into acc, the outliers' terms aside
 // (dot_outliers).
@@ -303,46 +304,57 @@ __device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const ui
     }
 }
 
-// The outliers' terms of one chunk: o = (v_0, v_1, i_0, i_1), each block's
-// extracted activation (0 if none) and its index; adds w_{i_b} v_b with the
-// weight decoded exactly (w = d sc q - dmin m for Q4_K, d (q - 8) for Q4_0,
-// d q for Q8_0, d sc (q - 32) for Q6_K). Run when wave_has_outlier says some
-// lane of the wave needs it.
+// The extracted activations' terms of one chunk. `xo` points at the chunk's
+// staged block data (row 0 of its XR rows, `nch` 16-byte units apart): row 1
+// holds in words 2 + b the slot indices of block b (five bits per slot, slot j
+// at bits 5j), row 2 + b block b's four slot values (0 in unused slots). Adds
+// w_i v for every slot, with the weight decoded exactly (w = d sc q - dmin m
+// for Q4_K, d (q - 8) for Q4_0, d q for Q8_0, d sc (q - 32) for Q6_K). Run
+// when wave_has_outlier says some lane of the wave needs it.
 template <int FMT>
-__device__ __forceinline__ void dot_outliers(const ChunkData<FMT>& d, int c, const uint4& o, float& acc) {
+__device__ __forceinline__ void dot_outliers(const ChunkData<FMT>& d, int c, const uint4* xo, int nch, float& acc) {
+    constexpr int BLK = Traits<FMT>::BLK;
+    const uint4 ix = xo[nch];
     float y = acc;
+    float sc[2], k[2] = {0.f, 0.f};
     if constexpr (FMT == Q4_K) {
         uint32_t sc0, m0, sc1, m1;
         q4k_scales(d.meta, c & 3, sc0, m0, sc1, m1);
         const float dd = half_lo(d.meta.x), dmin = half_hi(d.meta.x);
-        const float s0 = dd * (float)sc0, s1 = dd * (float)sc1;
-        const float k0 = fmaf(8.f, s0, -dmin * (float)m0), k1 = fmaf(8.f, s1, -dmin * (float)m1);
-        const int j0 = (int)o.z, j1 = (int)o.w;
-        const int q0 = sbfe(word_at(d.q[0], j0 >> 3), 4 * (j0 & 7), 4);
-        const int q1 = sbfe(word_at(d.q[1], j1 >> 3), 4 * (j1 & 7), 4);
-        y = fmaf(fmaf(s0, (float)q0, k0), wordf(o, 0), y);
-        y = fmaf(fmaf(s1, (float)q1, k1), wordf(o, 1), y);
+        sc[0] = dd * (float)sc0;
+        sc[1] = dd * (float)sc1;
+        k[0] = fmaf(8.f, sc[0], -dmin * (float)m0);
+        k[1] = fmaf(8.f, sc[1], -dmin * (float)m1);
     } else if constexpr (FMT == Q4_0) {
-        const int j0 = (int)o.z, j1 = (int)o.w;
-        const int q0 = sbfe(word_at(d.q[0], j0 >> 3), 4 * (j0 & 7), 4);
-        const int q1 = sbfe(word_at(d.q[1], j1 >> 3), 4 * (j1 & 7), 4);
-        y = fmaf((float)q0 * half_lo(d.meta.x), wordf(o, 0), y);
-        y = fmaf((float)q1 * half_hi(d.meta.x), wordf(o, 1), y);
-    } else if constexpr (FMT == Q8_0) {
-        const int j = (int)o.z;
-        const uint32_t w0 = word_at(d.q[0], (j >> 2) & 3), w1 = word_at(d.q[1], (j >> 2) & 3);
-        const uint32_t wd = j < 16 ? w0 : w1;  // (selecting the part first would index registers at run time)
-        y = fmaf(half_lo(d.meta.x) * (float)sbfe(wd, 8 * (j & 3), 8), wordf(o, 0), y);
-    } else if constexpr (FMT == Q6_K) {
-        // the outlier at position e = 32 b + i_b of the chunk, in scale group e / 16
-        const float dd = half_lo(d.meta.y);
+        sc[0] = half_lo(d.meta.x);
+        sc[1] = half_hi(d.meta.x);
+    }
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int e = 32 * b + (int)word(o, 2 + b), g = e >> 4, j = e & 15;
-            const int l = sbfe(word_at(d.q[b], (e >> 3) & 3), 4 * (e & 7), 4) + 8;
-            const int h = (int)bfe(word_at(d.q[2], g), j < 8 ? 4 * j : 4 * (j - 8) + 2, 2);
-            const float dsc = dd * (float)(int8_t)((d.meta.x >> (8 * g)) & 0xffu);
-            y = fmaf(dsc * (float)(l + 16 * h - 32), wordf(o, b), y);
+    for (int b = 0; b < BLK; ++b) {
+        const uint4 ov = xo[(2 + b) * nch];
+        const uint32_t idx = word(ix, 2 + b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = (int)bfe(idx, 5 * j, 5);
+            const float v = wordf(ov, j);
+            if constexpr (FMT == Q4_K) {
+                const int q = sbfe(word_at(d.q[b], i >> 3), 4 * (i & 7), 4);
+                y = fmaf(fmaf(sc[b], (float)q, k[b]), v, y);
+            } else if constexpr (FMT == Q4_0) {
+                const int q = sbfe(word_at(d.q[b], i >> 3), 4 * (i & 7), 4);
+                y = fmaf((float)q * sc[b], v, y);
+            } else if constexpr (FMT == Q8_0) {
+                const uint32_t w0 = word_at(d.q[0], (i >> 2) & 3), w1 = word_at(d.q[1], (i >> 2) & 3);
+                const uint32_t wd = i < 16 ? w0 : w1;  // (selecting the part first would index registers at run time)
+                y = fmaf(half_lo(d.meta.x) * (float)sbfe(wd, 8 * (i & 3), 8), v, y);
+            } else if constexpr (FMT == Q6_K) {
+                // position e = 32 b + i of the chunk, in scale group e / 16
+                const int e = 32 * b + i, g = e >> 4, jj = e & 15;
+                const int l = sbfe(word_at(d.q[b], (e >> 3) & 3), 4 * (e & 7), 4) + 8;
+                const int h = (int)bfe(word_at(d.q[2], g), jj < 8 ? 4 * jj : 4 * (jj - 8) + 2, 2);
+                const float dsc = half_lo(d.meta.y) * (float)(int8_t)((d.meta.x >> (8 * g)) & 0xffu);
+                y = fmaf(dsc * (float)(l + 16 * h - 32), v, y);
+            }
         }
     }
     acc = y;

@@ -138,7 +138,7 @@ template <int FMT, int M, int R, bool NORM = false>
 __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, int sub, int g, const ChunkData<FMT> (&d)[R],
                                          float (&acc)[R][M], const uint4* xd, const uint4* xb, bool outliers,
                                          float norm_scale = 1.f) {
-    constexpr int XP = Traits<FMT>::XP;
+    constexpr int XP = Traits<FMT>::XP, XR = Traits<FMT>::XR;
     const int nch = p.P.nch;
     const int c = w.chunk();
     const int row0 = w.tile * w.rows_per_wave + sub * R, rows = (int)p.rows;
@@ -150,16 +150,15 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
             uint4 bv[2];
 #pragma unroll
             for (int j = 0; j < XP; ++j) xv[j] = xd[(mm * XP + j) * nch + c];
-            bv[0] = xb[(mm * 3 + 0) * nch + c];
-            bv[1] = xb[(mm * 3 + 1) * nch + c];
+            bv[0] = xb[(mm * XR + 0) * nch + c];
+            bv[1] = xb[(mm * XR + 1) * nch + c];
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (row0 + r < rows) dot_int<FMT>(d[r], c, xv, bv, acc[r][mm]);
             if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
-                const uint4 o = xb[(mm * 3 + 2) * nch + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    if (row0 + r < rows) dot_outliers<FMT>(d[r], c, o, acc[r][mm]);
+                    if (row0 + r < rows) dot_outliers<FMT>(d[r], c, xb + mm * XR * nch + c, nch, acc[r][mm]);
             }
         }
     }
@@ -265,7 +264,7 @@ done:
 // steps per row, U / S rows per wave.
 template <int FMT, int M, int U, bool XF32>
 __global__ void __launch_bounds__(256) matvec_burst(MvParams p, int S) {
-    constexpr int XP = Traits<FMT>::XP;
+    constexpr int XP = Traits<FMT>::XP, XR = Traits<FMT>::XR;
     extern __shared__ uint4 smem[];
     const int nch = p.P.nch;
     uint4* xd = smem;
@@ -307,11 +306,11 @@ __global__ void __launch_bounds__(256) matvec_burst(MvParams p, int S) {
                 uint4 bv[2];
 #pragma unroll
                 for (int j = 0; j < XP; ++j) xv[j] = xd[(mm * XP + j) * nch + c];
-                bv[0] = xb[(mm * 3 + 0) * nch + c];
-                bv[1] = xb[(mm * 3 + 1) * nch + c];
+                bv[0] = xb[(mm * XR + 0) * nch + c];
+                bv[1] = xb[(mm * XR + 1) * nch + c];
                 dot_int<FMT>(d[u], c, xv, bv, acc[mm]);
                 if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0))
-                    dot_outliers<FMT>(d[u], c, xb[(mm * 3 + 2) * nch + c], acc[mm]);
+                    dot_outliers<FMT>(d[u], c, xb + mm * XR * nch + c, nch, acc[mm]);
             }
         }
         if (st == S - 1) {

@@ -334,9 +334,8 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
         dot_int<FMT>(dg, c, xv, bv, pg);
         dot_int<FMT>(du, c, xv, bv, pu);
         if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
-            const uint4 o = xb[2 * nch + c];
-            dot_outliers<FMT>(dg, c, o, pg);
-            dot_outliers<FMT>(du, c, o, pu);
+            dot_outliers<FMT>(dg, c, xb + c, nch, pg);
+            dot_outliers<FMT>(du, c, xb + c, nch, pu);
         }
     };
     if constexpr (GSPLIT) {
@@ -496,7 +495,7 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
                     bv[0] = xb[c];
                     bv[1] = xb[nch + c];
                     dot_int<FMT>(cd0, lc0, xv, bv, part);
-                    if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb[2 * nch + c], part);
+                    if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb + c, nch, part);
                 }
                 // lane + 32's chunk and weight, in every lane below 32
                 float pu = part, wu = w0, pl = part, wl = w0;
@@ -528,7 +527,7 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
                 bv[1] = xb[nch + c];
                 float part = 0.f;
                 dot_int<FMT>(cd0, lc0, xv, bv, part);
-                if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb[2 * nch + c], part);
+                if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb + c, nch, part);
                 acc = fmaf(w0, part, acc);
             }
             acc = group_sum(acc, G);
@@ -552,7 +551,7 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
             bv[1] = xb[nch + c];
             float part = 0.f;
             dot_int<FMT>(cd, lc, xv, bv, part);
-            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd, lc, xb[2 * nch + c], part);
+            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd, lc, xb + c, nch, part);
             acc = fmaf(w, part, acc);
         }
         acc = group_sum(acc, G);

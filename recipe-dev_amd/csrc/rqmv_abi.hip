@@ -502,6 +502,12 @@ int moe_dims(const rqmv_moe_params* p, rq::MoeDims* d, const DeviceInfo& info) {
     if (p->scoring != RQMV_SCORE_SOFTMAX && p->scoring != RQMV_SCORE_SIGMOID) return fail(RQMV_EINVAL, "bad scoring");
     if (!rq::act_known(p->activation) || !rq::act_known(p->shared_gate_activation))
         return fail(RQMV_EINVAL, "unknown activation code (rqmv_activation)");
+    // Scale's constant and PReLU's slope must be finite (lower_activation's
+    // Scale arm, recipe.rs:22717-22721)
+    const bool uses_factor = p->activation == rq::kActScale || p->activation == rq::kActPrelu ||
+                             p->shared_gate_activation == rq::kActScale || p->shared_gate_activation == rq::kActPrelu;
+    if (uses_factor && !(p->activation_factor - p->activation_factor == 0.f))
+        return fail(RQMV_EINVAL, "scale factor must be finite");
     if (!(p->scale == p->scale) || p->scale - p->scale != 0.f) return fail(RQMV_EINVAL, "moe routed scale must be finite");
     if (reinterpret_cast<uintptr_t>(p->selection_bias) % 4 != 0)
         return fail(RQMV_EINVAL, "selection_bias must be 4-byte aligned");

@@ -1,25 +1,31 @@
 // Activation staging into LDS, shared by the matvec and MoE kernels.
 //
 // Quantized weights (integer kernels). Each 32-value block b of an activation
-// row becomes 16-bit integers x = rint(v / s_b) with scale s_b = max|v| / 30583,
-// so every value is within s_b / 2 (1.64e-5 of the block's largest magnitude)
-// of s_b x. A block whose largest magnitude is more
-// than kOutlierRatio times its second largest has that one value taken out
-// (encoded as 0, the block scaled by the second largest): it goes to the
-// block's outlier slot and the kernels multiply it exactly in fp32 with its
-// weight, so one outlier per block does not coarsen the others. For 4-bit formats each x is split into four balanced
-// hex digits (x + 0x8888 has hex digits d_i + 8, so (x + 0x8888) ^ 0x8888 holds
-// every d_i as a signed nibble) and the digits are transposed into words of
-// eight values per digit, the weights' nibble order. For Q8_0 x is split into
-// two balanced bytes ((x + 0x8080) ^ 0x8080) and transposed into words of four.
+// row becomes 16-bit integers x = rint(v / s_b) with scale s_b = amax / 30583,
+// amax the largest magnitude of the values the block encodes, so every such
+// value is within s_b / 2 (1.64e-5 of amax) of s_b x. Large values are taken
+// out first: when at most kOutlierSlots values of a block are at or above
+// amax / kOutlierRatio, they go to the block's slots (encoded as 0) and the
+// kernels multiply them exactly in fp32 with their weights; the test repeats
+// on the rest with its own largest magnitude until the slots are used up or
+// the rest has more large values than slots are left. So a block's step is at
+// most kOutlierRatio / 30583 of its (kOutlierSlots + 1)-th largest magnitude:
+// a few outliers per block (on columns whose weights are small or zero) do not
+// coarsen the block's other values. For 4-bit formats each x is split into
+// four balanced hex digits (x + 0x8888 has hex digits d_i + 8, so
+// (x + 0x8888) ^ 0x8888 holds every d_i as a signed nibble) and the digits are
+// transposed into words of eight values per digit, the weights' nibble order.
+// For Q8_0 x is split into two balanced bytes ((x + 0x8080) ^ 0x8080) and
+// transposed into words of four.
 //   LDS: xd [m][part][chunk] 16-byte digit words (Traits::XP parts per chunk:
 //        nibble formats: part 2i + b holds digit i of the chunk's block b;
 //        Q8_0: parts 0-1 low bytes, parts 2-3 high bytes),
-//        xb [m][3][chunk] block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -),
-//        sx = s * sum x over the block (Q4_K) or the 16-value group (Q6_K),
-//        and the outlier slot (v_0, v_1, i_0, i_1): each block's extracted
-//        value (0 if none) and its index in the block; a chunk with an
-//        outlier stores its s_0 (or s_1) with the sign bit set.
+//        xb [m][XR][chunk] block data: row 0 (s_0, s_1, sx_0, sx_1), row 1
+//        (sx_2, sx_3, idx_0, idx_1), row 2 + b block b's four slot values
+//        (0 where unused); sx = s * sum x over the block (Q4_K) or the
+//        16-value group (Q6_K); idx_b the slots' indices within block b,
+//        five bits each (slot j at bits 5j); s_b carries its sign bit set
+//        when block b has values taken out.
 // F16 weights: fp16 activations as [m][part][chunk] 16-byte units of natural
 // pairs, or fp32 activations as [m][part][chunk] units of four floats.
 // Columns at or beyond K read as zero; lanes on consecutive chunks read
@@ -31,7 +37,8 @@
 namespace rq {
 
 constexpr float kXMax = 30583.f;  // 7 * (1 + 16 + 256 + 4096): four balanced hex digits
-constexpr float kOutlierRatio = 4.f;  // largest / second largest magnitude beyond which the largest is exact
+constexpr float kOutlierRatio = 4.f;  // a value at or above amax / kOutlierRatio is large
+constexpr int kOutlierSlots = 4;      // values of a block that can be taken out and multiplied exactly
 
 // Work item u = ((m * nch + c) * BLK + b) * 4 + q stages the eight values
 // 8q..8q+7 of block b of chunk c of row m. The four items of a block sit in an
@@ -178,12 +185,12 @@ __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, ui
 
 // Encodes item u and stores it into LDS. Every lane of the item's quad must
 // run it together (the block maximum and sums move through DPP).
-// Returns whether the item's block holds an outlier.
+// Returns whether the item's block has values taken out.
 template <int FMT, bool XF32, bool NORM = false>
 __device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const StageItem<XF32, NORM>& it,
                                              uint4* xd, float* xbf, const NormIn& nin = NormIn{},
                                              float* ss = nullptr) {
-    constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP;
+    constexpr int CW = Traits<FMT>::CW, BLK = Traits<FMT>::BLK, XP = Traits<FMT>::XP, XR = Traits<FMT>::XR;
     const auto [m, c, b, q] = stage_pos<FMT>(u, nch, M);
     const bool live = c * CW + b * 32 < K;
     float v[8];
@@ -233,54 +240,79 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const
     // their integer order is their order, and every infinity or NaN pattern
     // lies above the largest finite one, so one maximum finds both the
     // block's largest magnitude and whether any value is not finite.
-    uint32_t ibits = 0;  // this item's largest magnitude, as a pattern
+    uint32_t mb[8];
+    uint32_t i1 = 0, i2 = 0;  // this item's largest and second largest magnitudes, as patterns
 #pragma unroll
-    for (int k = 0; k < 8; ++k) ibits = max(ibits, __builtin_bit_cast(uint32_t, v[k]) & 0x7FFFFFFFu);
-    uint32_t bbits = ibits;
+    for (int k = 0; k < 8; ++k) {
+        mb[k] = __builtin_bit_cast(uint32_t, v[k]) & 0x7FFFFFFFu;
+        i2 = max(i2, min(i1, mb[k]));
+        i1 = max(i1, mb[k]);
+    }
+    uint32_t bbits = i1;
     bbits = max(bbits, (uint32_t)dpp_i32<0xB1>((int)bbits));  // quad_perm [1,0,3,2]
     bbits = max(bbits, (uint32_t)dpp_i32<0x4E>((int)bbits));  // quad_perm [2,3,0,1]
     const int bad = bbits > 0x7F7FFFFFu;
-    const float imax = __builtin_bit_cast(float, ibits);
     float amax = __builtin_bit_cast(float, bbits);
     if (!live) amax = 0.f;
-    // The largest magnitude exceeds kOutlierRatio times the second largest
-    // exactly when it is the block's only value at or above amax / 4. When two
-    // of the quad's items reach amax / 4 (ordinary activations, always) there
-    // is none; otherwise the values are counted (a rare, quad-uniform branch).
-    const float thr = amax * (1.0f / kOutlierRatio);
-    int hi_items = imax >= thr;
-    hi_items += dpp_i32<0xB1>(hi_items);
-    hi_items += dpp_i32<0x4E>(hi_items);
+    // Values are taken out only when at most kOutlierSlots of the block are
+    // at or above amax / kOutlierRatio. Each item's two largest count at most
+    // the large values; when they already exceed kOutlierSlots (ordinary
+    // activations, always) nothing is taken out. Otherwise the values are
+    // counted and taken out in rounds (a rare, quad-uniform branch).
+    const uint32_t thr0 = __builtin_bit_cast(uint32_t, amax * (1.0f / kOutlierRatio));
+    int seen = (int)(i1 >= thr0) + (int)(i2 >= thr0);
+    seen += dpp_i32<0xB1>(seen);
+    seen += dpp_i32<0x4E>(seen);
     bool outlier = false;
-    if (__builtin_expect(hi_items == 1 && live && !bad, 0)) {
-        int big = 0;
+    float slot[4] = {0.f, 0.f, 0.f, 0.f};  // the block's slot values (each set by its owner's lane)
+    uint32_t sidx = 0;                      // their indices in the block, five bits per slot
+    if (__builtin_expect(seen <= kOutlierSlots && live && !bad, 0)) {
+        uint32_t cur = bbits;  // the largest magnitude not taken out
+        int used = 0;
+        uint32_t taken = 0;  // bit k: v[k] is taken out
+        for (int round = 0; round < kOutlierSlots && cur != 0; ++round) {
+            const uint32_t thr = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, cur) * (1.0f / kOutlierRatio));
+            int n = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) big += fabsf(v[k]) >= thr;
-        big += dpp_i32<0xB1>(big);
-        big += dpp_i32<0x4E>(big);
-        outlier = big == 1;
-    }
-    float ov = 0.f;
-    int gi = 0;
-    if (__builtin_expect(outlier, 0)) {  // (rare: a quad-uniform branch)
-        // its owner takes the value out; the block is scaled by the rest
-        float rest = 0.f;
+            for (int k = 0; k < 8; ++k) n += !((taken >> k) & 1u) && mb[k] >= thr;
+            int tot = n + dpp_i32<0xB1>(n);
+            tot += dpp_i32<0x4E>(tot);
+            if (tot > kOutlierSlots - used) break;
+            // this lane's first slot: the slots used so far plus the lower lanes' counts
+            const int n0 = dpp_i32<0x00>(n), n1 = dpp_i32<0x55>(n), n2 = dpp_i32<0xAA>(n);
+            int pos = used + (q > 0 ? n0 : 0) + (q > 1 ? n1 : 0) + (q > 2 ? n2 : 0);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (fabsf(v[k]) >= amax * (1.0f / kOutlierRatio)) {
-                ov = v[k];
-                gi = q * 8 + k;
-                v[k] = 0.f;
+            for (int k = 0; k < 8; ++k) {
+                if (!((taken >> k) & 1u) && mb[k] >= thr) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) slot[j] = pos == j ? v[k] : slot[j];
+                    sidx |= (uint32_t)(q * 8 + k) << (5 * pos);
+                    taken |= 1u << k;
+                    ++pos;
+                }
             }
-            rest = fmaxf(rest, fabsf(v[k]));
+            used += tot;
+            uint32_t rest = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) rest = ((taken >> k) & 1u) ? rest : max(rest, mb[k]);
+            rest = max(rest, (uint32_t)dpp_i32<0xB1>((int)rest));
+            rest = max(rest, (uint32_t)dpp_i32<0x4E>((int)rest));
+            cur = rest;
         }
-        rest = fmaxf(rest, dpp_quad_f32<0xB1>(rest));
-        rest = fmaxf(rest, dpp_quad_f32<0x4E>(rest));
-        ov += dpp_quad_f32<0xB1>(ov);  // the value and its index, in every lane of the quad
-        ov += dpp_quad_f32<0x4E>(ov);
-        gi += dpp_i32<0xB1>(gi);
-        gi += dpp_i32<0x4E>(gi);
-        amax = rest;
+        if (used > 0) {  // (quad-uniform) the block is scaled by what is left
+            outlier = true;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = ((taken >> k) & 1u) ? 0.f : v[k];
+            amax = __builtin_bit_cast(float, cur);
+            // every slot has one owner and zeros elsewhere: the quad's sum is its value
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                slot[j] += dpp_quad_f32<0xB1>(slot[j]);
+                slot[j] += dpp_quad_f32<0x4E>(slot[j]);
+            }
+            sidx += (uint32_t)dpp_i32<0xB1>((int)sidx);
+            sidx += (uint32_t)dpp_i32<0x4E>((int)sidx);
+        }
     }
     if (__builtin_expect(bad, 0)) {
         amax = 0.f;
@@ -306,20 +338,19 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const
 #pragma unroll
         for (int i = 0; i < 4; ++i) xdw[((m * XP + 2 * i + b) * nch + c) * 4 + q] = w4[i];
     }
-    // block data (s_0, s_1, sx_0, sx_1), (sx_2, sx_3, -, -), outlier slot (v_0, v_1, i_0, i_1)
+    // block data rows 0 (s_0, s_1, sx_0, sx_1) and 1 (sx_2, sx_3, idx_0, idx_1), slot row 2 + b
     const int pair = sum + dpp_i32<0xB1>(sum);   // this half block (16 values)
     const int whole = pair + dpp_i32<0x4E>(pair);  // the block
-    float* b0 = xbf + ((m * 3 + 0) * nch + c) * 4;
-    float* b1 = xbf + ((m * 3 + 1) * nch + c) * 4;
-    float* bo = xbf + ((m * 3 + 2) * nch + c) * 4;
+    float* b0 = xbf + ((m * XR + 0) * nch + c) * 4;
+    float* b1 = xbf + ((m * XR + 1) * nch + c) * 4;
     if (q == 0) {
-        b0[b] = outlier ? -s : s;  // the sign bit marks a chunk with an outlier (s >= 0 otherwise)
-        bo[b] = ov;
-        reinterpret_cast<int*>(bo)[2 + b] = outlier ? gi : 0;
+        b0[b] = outlier ? -s : s;  // the sign bit marks a block with values taken out (s >= 0 otherwise)
+        reinterpret_cast<uint32_t*>(b1)[2 + b] = sidx;
+        *reinterpret_cast<float4*>(xbf + ((m * XR + 2 + b) * nch + c) * 4) =
+            make_float4(slot[0], slot[1], slot[2], slot[3]);
         if constexpr (BLK == 1) {
             b0[1] = 0.f;  // (read with s_0 for the outlier mark)
-            bo[1] = 0.f;
-            reinterpret_cast<int*>(bo)[3] = 0;
+            reinterpret_cast<uint32_t*>(b1)[3] = 0u;
         }
     }
     if constexpr (FMT == Q4_K) {
@@ -396,10 +427,10 @@ __device__ __forceinline__ bool stage_all(int nch, int K, const void* x, int64_t
 }
 
 // LDS bytes of a staged activation block for the integer kernels: digit
-// words, then xb [m][3][chunk] (block data and the outlier slot).
+// words, then xb [m][XR][chunk] (block data and the slot rows).
 __host__ __device__ inline size_t stage_bytes_int(int fmt, int M, int nch) {
-    const int xp = fmt == Q8_0 ? 4 : 8;
-    return (size_t)M * nch * (size_t)(xp + 3) * 16;
+    const int xp = fmt == Q8_0 ? 4 : 8, xr = fmt == Q8_0 ? 3 : 4;
+    return (size_t)M * nch * (size_t)(xp + xr) * 16;
 }
 
 // F16 weights: fp16 activations as natural pairs, or fp32 activations. Up to

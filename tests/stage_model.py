@@ -7,11 +7,13 @@ blocks whose step would fall below the smallest normal float), rounded once
 from the exact product of v_i and 1 / s (the kernels form 1 / s with the
 hardware reciprocal, within one ulp; the model divides); the kernels' products are exact integer dots of
 these against the weights' integer codes, scaled per block in fp32, so the
-activation a kernel multiplies is s * x_i. With outlier extraction, a block
-whose largest magnitude exceeds `threshold` times its second largest has that
-one value (the lowest index among equal magnitudes) taken out: it is encoded
-as 0, the block is scaled by the second largest magnitude, and the value
-itself is multiplied exactly (in fp32) with its weight.
+activation a kernel multiplies is s * x_i. With outlier extraction, a block takes out its large values before it is
+scaled: when at most `slots` (4) of its values are at or above amax / threshold
+(amax its largest magnitude; threshold 4), they go to the block's slots
+(encoded as 0) and are multiplied exactly (in fp32) with their weights; the
+test repeats on the values left, with their own largest magnitude, until the
+slots are used up or more large values remain than slots are left. So the
+block's scale is at most threshold / 30583 of its fifth largest magnitude.
 
 The functions return the effective activations and the error bound they
 obey: |v_i - s x_i| <= 0.51 s for every encoded value (half a step, plus the
@@ -25,27 +27,35 @@ import numpy as np
 
 XMAX = np.float32(30583.0)
 INV_XMAX = np.float32(1.0) / XMAX
+SLOTS = 4
 
 
-def encode_block(v: np.ndarray, threshold: float | None = None):
-    """One block (32 fp32 values) -> (effective values, scale s, outlier index
-    or -1, outlier value). Arithmetic in fp32 as the kernel does it."""
-    v = np.asarray(v, dtype=np.float32)
+def encode_block(v: np.ndarray, threshold: float | None = None, slots: int = SLOTS):
+    """One block (32 fp32 values) -> (effective values, scale s, indices taken
+    out, their values). Arithmetic in fp32 as the kernel does it; the slots
+    are filled round by round, each round's values in index order."""
+    v = np.asarray(v, dtype=np.float32).copy()
     a = np.abs(v)
     amax = np.float32(a.max()) if a.size else np.float32(0)
-    out_i, out_v = -1, np.float32(0)
-    if threshold is not None and amax > 0:
-        i = int(np.argmax(a))  # lowest index among the largest
-        rest = a.copy()
-        rest[i] = 0
-        amax2 = np.float32(rest.max())
-        if amax > np.float32(threshold) * amax2:
-            out_i, out_v = i, v[i]
-            v = v.copy()
-            v[i] = 0
-            amax = amax2
+    taken_i, taken_v = [], []
+    if threshold is not None and np.isfinite(v).all():
+        mask = np.zeros(v.size, bool)
+        cur = amax
+        ratio = np.float32(1.0) / np.float32(threshold)
+        while len(taken_i) < slots and cur > 0:
+            big = ~mask & (a >= np.float32(cur * ratio))
+            if int(big.sum()) > slots - len(taken_i):
+                break
+            for i in np.nonzero(big)[0]:
+                taken_i.append(int(i))
+                taken_v.append(v[i])
+            mask |= big
+            cur = np.float32(np.where(mask, np.float32(0), a).max())
+        if taken_i:
+            v[mask] = 0
+            amax = cur
     if not np.isfinite(amax) or not np.isfinite(v).all():
-        return np.full(v.shape, np.nan, np.float32), np.float32(np.nan), -1, np.float32(0)
+        return np.full(v.shape, np.nan, np.float32), np.float32(np.nan), [], []
     s = np.float32(amax * INV_XMAX)
     if s < np.float32(2.0 ** -126):  # zero or tiny blocks: the step 2^-126
         s = np.float32(2.0 ** -126) if amax > 0 else np.float32(0)
@@ -54,9 +64,9 @@ def encode_block(v: np.ndarray, threshold: float | None = None):
     x = np.rint(v.astype(np.float64) * np.float64(inv)).astype(np.float32)
     assert np.abs(x).max(initial=0) <= 30583
     eff = (s * x).astype(np.float32)
-    if out_i >= 0:
-        eff[out_i] = out_v
-    return eff, s, out_i, out_v
+    for i, tv in zip(taken_i, taken_v):
+        eff[i] = tv
+    return eff, s, taken_i, taken_v
 
 
 def effective_row(x: np.ndarray, threshold: float | None = None) -> np.ndarray:
@@ -71,13 +81,13 @@ def effective_row(x: np.ndarray, threshold: float | None = None) -> np.ndarray:
 
 def block_bound(x: np.ndarray, threshold: float | None = None) -> np.ndarray:
     """Per-value error bound |v - eff|: 0.51 s (s the block's scale), 0 for
-    an extracted outlier."""
+    a value taken out."""
     x = np.asarray(x, dtype=np.float32)
     out = np.empty(x.size, np.float64)
     for b in range(0, x.size, 32):
         blk = x[b:b + 32]
-        eff, s, oi, _ = encode_block(blk, threshold)
+        eff, s, taken, _ = encode_block(blk, threshold)
         out[b:b + 32] = 0.51 * float(s) + 1e-45
-        if oi >= 0:
-            out[b + oi] = 0.0
+        for i in taken:
+            out[b + i] = 0.0
     return out

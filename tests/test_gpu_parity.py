@@ -178,10 +178,13 @@ def _zero_column(fmt, w, rows, cols, col):
     return b.reshape(-1)
 
 
-def _outlier_x(m, k, factor, seed, dtype):
+def _outlier_x(m, k, factor, seed, dtype, per_block=1):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    cols = np.arange(0, k, 32) + rng.integers(0, 32, k // 32)
+    if per_block == 1:
+        cols = np.arange(0, k, 32) + rng.integers(0, 32, k // 32)
+    else:
+        cols = np.concatenate([b + np.sort(rng.choice(32, per_block, replace=False)) for b in range(0, k, 32)])
     x[:, cols] *= factor
     if dtype == "f16":
         bits = x.astype(np.float16).view(np.uint16)
@@ -228,6 +231,66 @@ def test_outliers_on_zero_weight_columns(gpu, fmt, xdt, m):
     ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
     err = rel_l2(y, ref)
     print(f"zero-column outliers {fmt} {xdt} m={m}: rel-L2 {err:.2e}", flush=True)
+    assert err <= 2e-4, err
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("per_block,factor", [(2, 1000.0), (3, 100.0), (4, 1000.0)])
+def test_several_outliers_on_zero_weight_columns(gpu, fmt, xdt, m, per_block, factor):
+    """Two to four outliers (x100 or x1000) in every 32-value block, each on
+    a column whose weights are all zero: the integer kernels (M <= 2) take up
+    to four values per block out of its scaling, in rounds, and multiply
+    them exactly, so the block's other values keep a step set by their own
+    magnitude (the matrix cores, M >= 3, use x as is)."""
+    rows, cols = 256, 4096
+    w = _weights(fmt, rows, cols, seed=150 + m + 7 * per_block)
+    xh, dt, x32, oc = _outlier_x(m, cols, factor, seed=151 + m + 7 * per_block, dtype=xdt, per_block=per_block)
+    for c in oc:
+        w = _zero_column(fmt, w, rows, cols, int(c))
+    deq = oracle.dequant_rows(fmt, w, rows, cols).reshape(rows, cols)
+    assert not deq[:, oc].any() and deq.any()
+    W = gpu.Weight(fmt, rows, cols, w)
+    y = _run_matvec(gpu, W, xh, dt, rows)
+    ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+    err = rel_l2(y, ref)
+    print(f"{per_block} zero-column outliers x{factor:g} {fmt} {xdt} m={m}: rel-L2 {err:.2e}", flush=True)
+    assert err <= 2e-4, err
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("per_block", [1, 3])
+def test_moe_outliers_on_zero_weight_columns(gpu, fmt, per_block):
+    """gguf_moe's gate/up staging with outliers in every block of x on
+    columns that every router, gate, up and shared row ignores (zero
+    weights), so the logits stay ordinary and the routed and shared
+    products are made of the other values alone: they must keep the bar."""
+    d, E, top, H, HS = 1024, 16, 4, 256, 256
+    router, gate, up, down, shared = _moe_case(fmt, d, E, top, H, HS, True, seed=61 + per_block)
+    sg, gs, us, ds = shared
+    xh, dt, x32, oc = _outlier_x(1, d, 1000.0, seed=62 + per_block, dtype="f16", per_block=per_block)
+    router = np.array(router.view(np.uint16).reshape(E, d), copy=True)
+    router[:, oc] = 0
+    sg = np.array(sg.view(np.uint16).reshape(1, d), copy=True)
+    sg[:, oc] = 0
+    router, sg = router.reshape(-1), sg.reshape(-1)
+    for c in oc:
+        gate = _zero_column(fmt, gate, E * H, d, int(c))
+        up = _zero_column(fmt, up, E * H, d, int(c))
+        gs = _zero_column(fmt, gs, HS, d, int(c))
+        us = _zero_column(fmt, us, HS, d, int(c))
+    moe = gpu.Moe(gpu.Weight("f16", E, d, router), gpu.Weight(fmt, H, d, gate, experts=E),
+                  gpu.Weight(fmt, H, d, up, experts=E), gpu.Weight(fmt, d, H, down, experts=E), top,
+                  shared_gate_inp=gpu.Weight("f16", 1, d, sg), gate_sh=gpu.Weight(fmt, HS, d, gs),
+                  up_sh=gpu.Weight(fmt, HS, d, us), down_sh=gpu.Weight(fmt, d, HS, ds))
+    y, route = moe(xh[0])
+    y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
+                                   x32[0].astype(np.float64), hidden_shared=HS, shared_gate_bits=sg.view(np.uint16),
+                                   gate_sh=gs, up_sh=us, down_sh=ds)
+    assert np.array_equal(route != 0, rw_ref != 0), "routed experts differ"
+    err = rel_l2(y, y_ref)
+    print(f"moe {fmt} {per_block} zero-column outliers per block: rel-L2 {err:.2e}", flush=True)
     assert err <= 2e-4, err
 
 
@@ -604,6 +667,39 @@ def test_moe_activation_and_selection_bias(gpu, act, gate_act, biased, scoring, 
     err = rel_l2(y, y_ref)
     print(f"moe {act}/{gate_act} bias={biased} {fmt} d={d} E={E}: rel-L2 {err:.3e}", flush=True)
     assert err <= REL_L2
+
+
+@pytest.mark.parametrize("scoring,renorm", [(0, True), (1, False)])
+def test_moe_selection_bias_flips_a_choice(gpu, scoring, renorm):
+    """A bias built to change the selection: zero everywhere except the best
+    expert the plain scores leave out, which gets +1 (more than any score's
+    spread), so the biased key must take it in and drop the weakest plain
+    choice. The device must follow the oracle, and differ from the unbiased
+    selection: a path that ignored the bias fails here."""
+    fmt, d, E, top, H = "q4_k", 2048, 256, 8, 512
+    router, gate, up, down, _ = _moe_case(fmt, d, E, top, H, 0, False, seed=41)
+    xh, dt, x32 = _x(1, d, "f16", seed=42)
+    x64 = x32[0].astype(np.float64)
+    _, plain = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down, x64,
+                              scoring=scoring, renormalize=renorm)
+    logits = synth.fp16_to_f32(router.view(np.uint16)).reshape(E, d).astype(np.float64) @ x64
+    order = np.argsort(-logits, kind="stable")
+    outside = int(order[top])  # the best expert the plain selection leaves out
+    assert plain[outside] == 0
+    bias = np.zeros(E, np.float32)
+    bias[outside] = 1.0
+    B = gpu.DeviceBuffer.from_array(bias)
+    moe = gpu.Moe(gpu.Weight("f16", E, d, router), gpu.Weight(fmt, H, d, gate, experts=E),
+                  gpu.Weight(fmt, H, d, up, experts=E), gpu.Weight(fmt, d, H, down, experts=E), top,
+                  scoring=scoring, renormalize=renorm, selection_bias=B)
+    y, route = moe(xh[0])
+    y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down, x64,
+                                   scoring=scoring, renormalize=renorm, selection_bias=bias.astype(np.float64))
+    assert rw_ref[outside] != 0 and int(np.sum((plain != 0) != (rw_ref != 0))) == 2
+    assert np.array_equal(route != 0, rw_ref != 0), "routed experts differ"
+    assert not np.array_equal(route != 0, plain != 0), "the bias moved no selection"
+    assert np.allclose(route, rw_ref, rtol=1e-5, atol=1e-7)
+    assert rel_l2(y, y_ref) <= REL_L2
 
 
 @pytest.mark.parametrize("scoring,renorm", [(0, True), (1, False), (1, True)])
