@@ -21,6 +21,14 @@ struct MvParams {
     int64_t ldy;
     int G;  // lanes that share one row (power of two, 8..64)
     int block = 256;  // threads per workgroup (the launch's block size)
+    // The row-tile walk of the vector kernels, set by the launcher from the
+    // launch shape (so that no wave divides before its first load): log2 G,
+    // rows per wave tile ((64 / G) * R), row tiles, and steps per tile
+    // (ceil(chunks / G)).
+    int g_shift = 6;
+    int rows_per_wave = 1;
+    int tiles = 0;
+    int steps = 1;
     // F16 weights only: rows at or past `split` come from P2 (row - split), so
     // that two weights of one width run as one launch (an MoE router and its
     // shared-expert gate). split >= rows: P alone.

@@ -49,17 +49,29 @@ struct StepWalk {
 
 __device__ __forceinline__ StepWalk make_walk(const MvParams& p, int R, int g) {
     StepWalk w;
+    (void)R;
     const int wpb = p.block >> 6, wave = threadIdx.x >> 6;
-    w.rows_per_wave = (64 / p.G) * R;
-    w.tiles = (int)((p.rows + w.rows_per_wave - 1) / w.rows_per_wave);
+    w.rows_per_wave = p.rows_per_wave;
+    w.tiles = p.tiles;
     w.tile = (int)blockIdx.x * wpb + wave;
     w.tile_stride = (int)gridDim.x * wpb;
     w.s = 0;
-    w.steps = (p.P.nch + p.G - 1) / p.G;
+    w.steps = p.steps;
     w.g = g;
     w.G = p.G;
     w.nch = p.P.nch;
     return w;
+}
+
+// The walk's launch-shape constants (MvParams::g_shift .. steps) for G lanes
+// per row and R rows per lane group.
+static void set_walk(MvParams& p, int G, int R) {
+    int sh = 0;
+    while ((1 << sh) < G) ++sh;
+    p.g_shift = sh;
+    p.rows_per_wave = (64 >> sh) * R;
+    p.tiles = (int)((p.rows + p.rows_per_wave - 1) / p.rows_per_wave);
+    p.steps = (p.P.nch + G - 1) / G;
 }
 
 // Loads step `w` for the lane's R rows. Rows or chunks past the end (and the
@@ -186,7 +198,7 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     const int nch = p.P.nch;
     uint4* xd = smem;
     uint4* xb = smem + M * XP * nch;
-    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane / p.G;
+    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane >> p.g_shift;
     const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
     StepWalk w[NB];
     w[0] = make_walk(p, R, g);
@@ -330,7 +342,7 @@ template <int M, int R, bool XF32>
 __global__ void __launch_bounds__(512) matvec_f16w(MvParams p) {
     extern __shared__ uint4 smem[];
     const int nch = p.P.nch;
-    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane / p.G;
+    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane >> p.g_shift;
     StepWalk w = make_walk(p, R, g);
     ChunkData<F16> cur[R];
     load_rows<F16, R>(p, w, sub, cur);
@@ -484,6 +496,8 @@ static hipError_t launch_kernel(K kernel, const MvParams& p_in, const LaunchShap
                                 hipEvent_t ev0, hipEvent_t ev1) {
     MvParams p = p_in;
     p.block = s.block;
+    p.G = s.G;
+    set_walk(p, s.G, s.R);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);

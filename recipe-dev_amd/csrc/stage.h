@@ -393,6 +393,9 @@ __device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x,
     const int total = stage_items<FMT>(nch, M);
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
+        // (rounds past the last item are skipped by the whole workgroup; a
+        // thread past it in the last round loads an item of its own quad)
+        if (j * nthreads >= total) break;
         const int u = (int)threadIdx.x + j * nthreads;
         stage_issue<FMT, XF32, NORM>(u < total ? u : (int)threadIdx.x % 4, nch, M, K, x, ldx, it[j], nin);
     }
@@ -406,6 +409,7 @@ __device__ __forceinline__ bool stage_multi_finish(int nch, int K, int M, int nt
     bool out = false;
 #pragma unroll
     for (int j = 0; j < kStageNJ; ++j) {
+        if (j * nthreads >= total) break;
         const int u = (int)threadIdx.x + j * nthreads;
         if (u < total) out |= stage_finish<FMT, XF32, NORM>(u, nch, M, K, it[j], xd, xbf, nin, ss);
     }
