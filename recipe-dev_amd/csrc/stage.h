@@ -107,6 +107,8 @@ __device__ __forceinline__ void stage_issue(int u, int nch, int M, int K, const 
     }
 }
 
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
 template <int CTRL>
 __device__ __forceinline__ int dpp_i32(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
@@ -116,22 +118,30 @@ __device__ __forceinline__ float dpp_quad_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
-// Four signed-nibble digit words (one per digit) from eight 16-bit patterns.
-__device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* out) {
-    uint32_t t[4], v[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t p = (u[2 * k] & 0xffffu) | (u[2 * k + 1] << 16);
-        const uint32_t q = p & 0x0F0F0F0Fu, r = (p >> 4) & 0x0F0F0F0Fu;
-        t[k] = q | (q >> 12);  // byte 0: digit 0 pair, byte 1: digit 2 pair
-        v[k] = r | (r >> 12);  // byte 0: digit 1 pair, byte 1: digit 3 pair
-    }
-    const uint32_t A = __builtin_amdgcn_perm(t[1], t[0], 0x05040100u), B = __builtin_amdgcn_perm(t[3], t[2], 0x05040100u);
-    const uint32_t C = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u), D = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
-    out[0] = __builtin_amdgcn_perm(B, A, 0x06040200u);
-    out[2] = __builtin_amdgcn_perm(B, A, 0x07050301u);
-    out[1] = __builtin_amdgcn_perm(D, C, 0x06040200u);
-    out[3] = __builtin_amdgcn_perm(D, C, 0x07050301u);
+// The four signed-nibble digit words of eight values from their 16-bit
+// patterns offset by 0x8888: P[j] holds (x_2j + 0x8888) in its low half and
+// (x_2j+1 + 0x8888) in its high half, so every byte of P is a pair of digits
+// d_i + 8 and each byte XOR 0x88 a pair of signed digits. Word i of the
+// result holds digit i of x_0..x_7 in nibbles 0..7.
+__device__ __forceinline__ void digit_words(const uint32_t (&P)[4], uint32_t (&out)[4]) {
+    // bytes of x_1, x_0, x_3, x_2 (and x_5, x_4, x_7, x_6): low bytes (digits
+    // 0, 1) in A, B; high bytes (digits 2, 3) in C, D
+    const uint32_t A = __builtin_amdgcn_perm(P[1], P[0], 0x04060002u), C = __builtin_amdgcn_perm(P[1], P[0], 0x05070103u);
+    const uint32_t B = __builtin_amdgcn_perm(P[3], P[2], 0x04060002u), D = __builtin_amdgcn_perm(P[3], P[2], 0x05070103u);
+    // Z's low nibbles (signed: ^ 8) z_1, z_0, z_3, z_2 per byte; z | z << 12
+    // puts z_0 | z_1 << 4 in byte 1 and z_2 | z_3 << 4 in byte 3
+    auto lo = [](uint32_t Z) {
+        const uint32_t z = (Z & 0x0F0F0F0Fu) ^ 0x08080808u;
+        return z | (z << 12);
+    };
+    auto hi = [](uint32_t Z) {
+        const uint32_t z = ((Z >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+        return z | (z << 12);
+    };
+    out[0] = __builtin_amdgcn_perm(lo(B), lo(A), 0x07050301u);
+    out[1] = __builtin_amdgcn_perm(hi(B), hi(A), 0x07050301u);
+    out[2] = __builtin_amdgcn_perm(lo(D), lo(C), 0x07050301u);
+    out[3] = __builtin_amdgcn_perm(hi(D), hi(C), 0x07050301u);
 }
 
 // Encodes eight values of a 32-value block whose maximum magnitude is amax
@@ -142,43 +152,40 @@ __device__ __forceinline__ void nibble_transpose(const uint32_t* u, uint32_t* ou
 // reciprocal (within one ulp), so |v / s| stays below 30583.5 and needs no
 // clamp. A block whose step would fall below the smallest normal float (amax
 // under 30583 * 2^-126) takes the step 2^-126. The rounding is one fma with
-// 1.5 * 2^23, whose sum holds 2^23 + 2^22 + rint(v / s) (to nearest even) in
-// its low bits; x's low 16 bits are those of the sum's bit pattern, and the
-// digit split only uses those.
+// 1.5 * 2^23 + c, c = 0x8888 (nibble formats) or 0x8080 (Q8_0): the sum lies
+// in [2^23, 2^24), where a float's pattern is 0x4B000000 plus its value
+// minus 2^23, so it is rint(v / s) + c (to nearest even: c is even) in the
+// pattern's low bits and the offset digits come out of the low 16 bits as
+// they are.
 template <int FMT>
 __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, uint32_t (&w4)[4], int& sum) {
-    constexpr uint32_t kMagicBits = 0x4B400000u;  // 1.5 * 2^23
+    constexpr float kOffset = FMT == Q8_0 ? 32896.f : 34952.f;  // 0x8080, 0x8888
+    constexpr float kMagic = 12582912.0f + kOffset;              // 1.5 * 2^23 + c
+    constexpr uint32_t kMagicBits = 0x4B400000u + (uint32_t)kOffset;
     float s = amax * (1.0f / kXMax);
-    float inv;
-    if (__builtin_expect(s < 0x1p-126f, 0)) {  // (zero or tiny blocks)
-        inv = amax > 0.f ? 0x1p126f : 0.f;
-        s = amax > 0.f ? 0x1p-126f : 0.f;
-    } else {
-        inv = __builtin_amdgcn_rcpf(s);
-    }
+    const bool tiny = s < 0x1p-126f;  // (zero or tiny blocks)
+    float inv = __builtin_amdgcn_rcpf(s);
+    inv = tiny ? (amax > 0.f ? 0x1p126f : 0.f) : inv;
+    s = tiny ? (amax > 0.f ? 0x1p-126f : 0.f) : s;
     uint32_t xb[8];
     uint32_t usum = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        xb[k] = __builtin_bit_cast(uint32_t, fmaf(v[k], inv, 12582912.0f));
+        xb[k] = __builtin_bit_cast(uint32_t, fmaf(v[k], inv, kMagic));
         usum += xb[k];
     }
     sum = (int)(usum - 8u * kMagicBits);
+    uint32_t P[4];  // (x_2j + c) | (x_2j+1 + c) << 16
+#pragma unroll
+    for (int j = 0; j < 4; ++j) P[j] = __builtin_amdgcn_perm(xb[2 * j + 1], xb[2 * j], 0x05040100u);
     if constexpr (FMT == Q8_0) {
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            uint32_t uu[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) uu[e] = ((xb[4 * w + e] + 0x8080u) ^ 0x8080u) & 0xffffu;
-            const uint32_t pa = uu[0] | (uu[1] << 16), pb = uu[2] | (uu[3] << 16);
-            w4[w] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
-            w4[2 + w] = __builtin_amdgcn_perm(pb, pa, 0x07050301u);
-        }
+        // low bytes of x_0..x_3 (x_4..x_7), then the high bytes; ^ 0x80 per byte
+        w4[0] = __builtin_amdgcn_perm(P[1], P[0], 0x06040200u) ^ 0x80808080u;
+        w4[1] = __builtin_amdgcn_perm(P[3], P[2], 0x06040200u) ^ 0x80808080u;
+        w4[2] = __builtin_amdgcn_perm(P[1], P[0], 0x07050301u) ^ 0x80808080u;
+        w4[3] = __builtin_amdgcn_perm(P[3], P[2], 0x07050301u) ^ 0x80808080u;
     } else {
-        uint32_t uu[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) uu[e] = (xb[e] + 0x8888u) ^ 0x8888u;
-        nibble_transpose(uu, w4);
+        digit_words(P, w4);
     }
     return s;
 }
@@ -240,13 +247,34 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const
     // their integer order is their order, and every infinity or NaN pattern
     // lies above the largest finite one, so one maximum finds both the
     // block's largest magnitude and whether any value is not finite.
-    uint32_t mb[8];
-    uint32_t i1 = 0, i2 = 0;  // this item's largest and second largest magnitudes, as patterns
+    uint32_t i1 = 0, i2 = 0;  // this item's largest and second largest magnitudes, as fp32 patterns
+    if constexpr (XF32) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        mb[k] = __builtin_bit_cast(uint32_t, v[k]) & 0x7FFFFFFFu;
-        i2 = max(i2, min(i1, mb[k]));
-        i1 = max(i1, mb[k]);
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t mk = __builtin_bit_cast(uint32_t, v[k]) & 0x7FFFFFFFu;
+            i2 = max(i2, min(i1, mk));
+            i1 = max(i1, mk);
+        }
+    } else {
+        // fp16 patterns order the same way, two to a word (packed 16-bit
+        // maxima); the two largest then convert exactly to fp32
+        u16x2_t hi, lo;
+        {
+            const u16x2_t m0 = __builtin_bit_cast(u16x2_t, word(it.raw[0], 0) & 0x7FFF7FFFu);
+            const u16x2_t m1 = __builtin_bit_cast(u16x2_t, word(it.raw[0], 1) & 0x7FFF7FFFu);
+            const u16x2_t m2 = __builtin_bit_cast(u16x2_t, word(it.raw[0], 2) & 0x7FFF7FFFu);
+            const u16x2_t m3 = __builtin_bit_cast(u16x2_t, word(it.raw[0], 3) & 0x7FFF7FFFu);
+            hi = __builtin_elementwise_max(m0, m1);
+            lo = __builtin_elementwise_min(m0, m1);
+            lo = __builtin_elementwise_max(lo, __builtin_elementwise_min(hi, m2));
+            hi = __builtin_elementwise_max(hi, m2);
+            lo = __builtin_elementwise_max(lo, __builtin_elementwise_min(hi, m3));
+            hi = __builtin_elementwise_max(hi, m3);
+        }
+        const uint32_t h1 = max((uint32_t)hi.x, (uint32_t)hi.y);
+        const uint32_t h2 = max(min((uint32_t)hi.x, (uint32_t)hi.y), max((uint32_t)lo.x, (uint32_t)lo.y));
+        i1 = __builtin_bit_cast(uint32_t, half_lo(h1));
+        i2 = __builtin_bit_cast(uint32_t, half_lo(h2));
     }
     uint32_t bbits = i1;
     bbits = max(bbits, (uint32_t)dpp_i32<0xB1>((int)bbits));  // quad_perm [1,0,3,2]
@@ -267,6 +295,9 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const
     float slot[4] = {0.f, 0.f, 0.f, 0.f};  // the block's slot values (each set by its owner's lane)
     uint32_t sidx = 0;                      // their indices in the block, five bits per slot
     if (__builtin_expect(seen <= kOutlierSlots && live && !bad, 0)) {
+        uint32_t mb[8];  // the magnitudes, as fp32 patterns
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mb[k] = __builtin_bit_cast(uint32_t, v[k]) & 0x7FFFFFFFu;
         uint32_t cur = bbits;  // the largest magnitude not taken out
         int used = 0;
         uint32_t taken = 0;  // bit k: v[k] is taken out
