@@ -569,12 +569,102 @@ def int8_bench(args):
     graph.close()
 
 
+def grid_table(args):
+    """The headline product beside a plain read of the same bytes, at the same
+    grids, in one process: for each grid G in --grids, `args.steps` plain
+    reads of 33 MB (a rotating window of a buffer >= 2x the Infinity Cache,
+    256 threads per workgroup, --inflight loads in flight per thread;
+    libmeasure.so) and `args.steps` Q4_K 4096->14336 products at one fp16
+    activation row with RQMV_GRID = G (rotating weight copies), each
+    dispatch timed by events it records itself. Prints one JSON line with a
+    row per (kernel, grid); profile the same command with rocprofv3 to read
+    counters per dispatch."""
+    import ctypes
+
+    import rqmv
+    from rqmv import synth
+
+    fmt, rows, cols, _, desc = WORKLOADS["q4_k_up"]
+    rqmv.init(0)
+    w = synth.weights(fmt, rows, cols)
+    nbytes = (w.nbytes + 15) // 16 * 16
+    copies = args.copies or max(2, -(-2 * MALL_BYTES // nbytes) + 1)
+    Ws = [rqmv.Weight(fmt, rows, cols, w) for _ in range(copies)]
+    xb = rqmv.DeviceBuffer.from_array(synth.activations_f16(cols))
+    yb = rqmv.DeviceBuffer(4 * rows)
+    big = rqmv.DeviceBuffer(nbytes * copies)
+    big.fill_zero()
+    grids = [int(g) for g in args.grids.split(",")]
+    sink = rqmv.DeviceBuffer(4 * 256 * max(grids))
+    stream = rqmv.Stream()
+    meas = ctypes.CDLL(os.path.join(ROOT, "recipe-dev_amd", "libmeasure.so"))
+    meas.measure_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_void_p]
+    alg = w.nbytes + 2 * cols + 4 * rows
+
+    def timed(launch):
+        for i in range(args.warmup):
+            launch(i, None, None)
+        stream.synchronize()
+        ev = [(rqmv.Event(), rqmv.Event()) for _ in range(args.steps)]
+        for i in range(args.steps):
+            launch(i, ev[i][0].handle, ev[i][1].handle)
+        stream.synchronize()
+        d = np.array([a.elapsed_ms(b) for a, b in ev]) * 1e3
+        for a, b in ev:
+            a.close()
+            b.close()
+        return {"mean_us": round(float(d.mean()), 3), "median_us": round(float(np.median(d)), 3),
+                "p10_us": round(float(np.percentile(d, 10)), 3), "p90_us": round(float(np.percentile(d, 90)), 3)}
+
+    table = []
+    for g in grids:
+        def read(i, e0, e1, g=g):
+            rc = meas.measure_stream_read(big.ptr + (i % copies) * nbytes, nbytes, g, args.inflight, 0x9E3779B9,
+                                          sink.ptr, stream.handle, e0, e1)
+            if rc:
+                raise RuntimeError(f"measure_stream_read: HIP error {rc}")
+
+        r = timed(read)
+        r.update({"kernel": "plain read", "grid": g, "bytes": nbytes,
+                  "gbs": round(nbytes / (r["mean_us"] * 1e-6) / 1e9, 1)})
+        log(f"bench: plain read grid {g}: {r}")
+        table.append(r)
+        os.environ["RQMV_GRID"] = str(g)
+
+        def mv(i, e0, e1):
+            if e0 is None:
+                Ws[i % copies].matvec(xb, rqmv.DTYPE_F16, 1, cols, yb, rows, stream)
+            else:
+                _check_mv(rqmv, Ws[i % copies], xb, yb, rows, cols, stream, e0, e1)
+
+        r = timed(mv)
+        r.update({"kernel": "matvec_int Q4_K 4096->14336 M=1", "grid": g, "bytes": alg,
+                  "gbs": round(alg / (r["mean_us"] * 1e-6) / 1e9, 1)})
+        log(f"bench: matvec grid {g}: {r}")
+        table.append(r)
+        del os.environ["RQMV_GRID"]
+    print(json.dumps({"grid_table": table, "inflight": args.inflight, "copies": copies, "steps": args.steps}),
+          flush=True)
+
+
+def _check_mv(rqmv, W, xb, yb, rows, cols, stream, e0, e1):
+    rc = rqmv.lib().lib.rqmv_matvec_timed(W.handle, xb.ptr, rqmv.DTYPE_F16, 1, cols, yb.ptr, rows, stream.handle,
+                                          e0, e1)
+    if rc:
+        raise RuntimeError(f"rqmv_matvec_timed: {rc}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="q4_k_up", choices=sorted(WORKLOADS) + ["moe_c4", "decode_c5"])
+    ap.add_argument("--workload", default="q4_k_up",
+                    choices=sorted(WORKLOADS) + ["moe_c4", "decode_c5", "grid_table"])
+    ap.add_argument("--grids", default="512,1024,2048", help="grid_table: workgroup counts")
+    ap.add_argument("--inflight", type=int, default=4, choices=[1, 2, 4, 8], help="grid_table: plain read loads in flight")
     ap.add_argument("--m", type=int, default=1, help="activation rows")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -599,6 +689,9 @@ def main():
         return
     if args.workload == "decode_c5":
         decode_bench(args)
+        return
+    if args.workload == "grid_table":
+        grid_table(args)
         return
 
     if args.int8:
