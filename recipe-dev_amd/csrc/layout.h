@@ -11,7 +11,7 @@
 // so the 64 lanes of a wave that take 64 consecutive chunks read one
 // contiguous 1 KiB run per load instruction (16 bytes per lane), and a row is
 // one contiguous stream with its scales beside its codes. Rows start 16-byte
-// aligned (a row's bytes round up to a multiple of 16).
+// aligned (a row's bytes round up to a multiple of 16, or of 128 from 4 KiB).
 //
 // Per format (GGML type id, recipe.rs:9925-9961; block sizes recipe.rs:15811-15826).
 // Four-bit codes are stored in natural weight order, two per byte (weight 2j
@@ -82,13 +82,19 @@ RQ_HD int64_t group_bytes(const FormatInfo& f, int64_t nb) {
     return nb * f.code_parts * 16 + (nb * f.meta_quad + 3) / 4;
 }
 
-// Bytes of one row (rounded up to 16) and of a full 64-chunk group.
+// Bytes of one row: its groups rounded up to 16, and rows of 4 KiB or more
+// to whole 128-byte lines, so that no cache line holds the end of one such
+// row and the start of the next (different workgroups read the two rows at
+// different times, and the line would come from HBM twice: Q6_K rows of 5120
+// weights, 4,200 bytes, read 15 % of their bytes twice); shorter rows keep
+// the 16-byte rounding, where a line's padding would be a larger share.
 RQ_HD int64_t row_bytes(int fmt, int64_t cols) {
     const FormatInfo f = format_info(fmt);
     const int64_t nch = chunks_per_row(fmt, cols);
     const int64_t full = nch / 64, rest = nch % 64;
     const int64_t b = full * group_bytes(f, 64) + (rest ? group_bytes(f, rest) : 0);
-    return (b + 15) / 16 * 16;
+    const int64_t b16 = (b + 15) / 16 * 16;
+    return b16 >= 4096 ? (b16 + 127) / 128 * 128 : b16;
 }
 
 // Where chunk c of a row of nch chunks lives: its group's start, the group's
