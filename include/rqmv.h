@@ -31,13 +31,15 @@
  *     of one or two activation rows (and the gguf_moe and decode-step
  *     products) encode each 32-value block of x as 16-bit integers at a step
  *     of (the block's scaling magnitude) / 30583; first, up to four large
- *     values per block (those at or above a quarter of the largest, taken in
+ *     values per block (those at or above 1/16 of the largest, taken in
  *     rounds) are set aside and multiplied exactly in fp32. Every other value
- *     is then within 1/60000 of the scaling magnitude, which is at most 4x the
- *     block's fifth largest magnitude: about 2^-14 of it. Only a block with
- *     five or more comparable outliers on columns whose weights are near zero
- *     can lose accuracy against recipe's fp32 sums. Products of 3 to 32 rows
- *     take fp16 x exactly and fp32 x as an exact-to-2^-22 fp16 pair.
+ *     is then within 1/60000 of the scaling magnitude, which is at most 16x
+ *     the block's fifth largest magnitude: about 2^-12 of it (and 2^-16 of
+ *     the block's largest magnitude where nothing is set aside, as for
+ *     Gaussian or heavy-tailed activations). Only a block with five or more
+ *     outliers on columns whose weights are near zero can lose accuracy
+ *     against recipe's fp32 sums. Products of 3 to 32 rows take fp16 x
+ *     exactly and fp32 x as an exact-to-2^-22 fp16 pair.
  */
 #ifndef RQMV_H
 #define RQMV_H

@@ -37,7 +37,7 @@
 namespace rq {
 
 constexpr float kXMax = 30583.f;  // 7 * (1 + 16 + 256 + 4096): four balanced hex digits
-constexpr float kOutlierRatio = 4.f;  // a value at or above amax / kOutlierRatio is large
+constexpr float kOutlierRatio = 16.f;  // a value at or above amax / kOutlierRatio is large
 constexpr int kOutlierSlots = 4;      // values of a block that can be taken out and multiplied exactly
 
 // Work item u = ((m * nch + c) * BLK + b) * 4 + q stages the eight values

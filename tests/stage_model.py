@@ -9,11 +9,14 @@ hardware reciprocal, within one ulp; the model divides); the kernels' products a
 these against the weights' integer codes, scaled per block in fp32, so the
 activation a kernel multiplies is s * x_i. With outlier extraction, a block takes out its large values before it is
 scaled: when at most `slots` (4) of its values are at or above amax / threshold
-(amax its largest magnitude; threshold 4), they go to the block's slots
+(amax its largest magnitude; threshold RATIO = 16), they go to the block's slots
 (encoded as 0) and are multiplied exactly (in fp32) with their weights; the
 test repeats on the values left, with their own largest magnitude, until the
 slots are used up or more large values remain than slots are left. So the
 block's scale is at most threshold / 30583 of its fifth largest magnitude.
+The ratio is wide enough that heavy-tailed activations (a SiLU-gated product,
+Student-t) almost never have values taken out (under 1 % of blocks), and
+narrow enough that outliers 100x the rest always are.
 
 The functions return the effective activations and the error bound they
 obey: |v_i - s x_i| <= 0.51 s for every encoded value (half a step, plus the
@@ -28,6 +31,7 @@ import numpy as np
 XMAX = np.float32(30583.0)
 INV_XMAX = np.float32(1.0) / XMAX
 SLOTS = 4
+RATIO = 16.0
 
 
 def encode_block(v: np.ndarray, threshold: float | None = None, slots: int = SLOTS):
