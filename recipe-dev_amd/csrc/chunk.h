@@ -178,35 +178,43 @@ __device__ __forceinline__ void load_chunk_rs(__amdgpu_buffer_rsrc_t rs, const P
 }
 
 // Q4_K scale/min of the two sub-blocks 2p and 2p+1 of a chunk, from the
-// superblock's 12 scale bytes s[] held as words m1 = s[0..3], m2 = s[4..7],
-// m3 = s[8..11]; the k_scale packing of recipe.rs:15204-15210.
+// superblock's meta words (x = d, dmin; y, z, w = the 96-bit scale fields):
+// chunk p's 24-bit field at bit 24p holds scale(2p), min(2p), scale(2p+1),
+// min(2p+1), six bits each (the repack's form of the k_scale bytes,
+// recipe.rs:15204-15210). A 64-bit shift of (z:y) or (w:z) brings the field
+// to bit 0: a selection between those pairs, as in word_at (a run-time choice
+// between meta's members reads as an index into the register array, which
+// the compiler would place in scratch memory).
+__device__ __forceinline__ uint32_t q4k_field(const uint4& meta, int p) {
+    const uint64_t lo = ((uint64_t)meta.z << 32) | meta.y, hi = ((uint64_t)meta.w << 32) | meta.z;
+    const uint32_t sh = (uint32_t)(24 * p) - (p < 2 ? 0u : 32u);  // 0, 24, 16, 40
+    return (uint32_t)((p < 2 ? lo : hi) >> sh);
+}
 __device__ __forceinline__ void q4k_scales(const uint4& meta, int p, uint32_t& sc0, uint32_t& m0, uint32_t& sc1,
                                            uint32_t& m1) {
-    const uint32_t o = 16u * (uint32_t)(p & 1);
-    const bool hi = p >= 2;
-    const uint32_t X = hi ? meta.w : meta.y;  // low 4 bits of the scale
-    const uint32_t Y = hi ? meta.w : meta.z;  // low 4 bits of the minimum
-    const uint32_t yo = hi ? 4u : 0u;
-    const uint32_t top = hi ? 6u : 4u;
-    sc0 = bfe(X, o, 4) | (bfe(meta.y, o + top, 2) << 4);
-    sc1 = bfe(X, o + 8, 4) | (bfe(meta.y, o + 8 + top, 2) << 4);
-    m0 = bfe(Y, o + yo, 4) | (bfe(meta.z, o + top, 2) << 4);
-    m1 = bfe(Y, o + 8 + yo, 4) | (bfe(meta.z, o + 8 + top, 2) << 4);
+    const uint32_t f = q4k_field(meta, p);
+    sc0 = f & 63u;
+    m0 = bfe(f, 6, 6);
+    sc1 = bfe(f, 12, 6);
+    m1 = bfe(f, 18, 6);
 }
 
 // sum_i 16^i sum_w dot8(W_w, D_i,w) over four weight words and the four digit
-// words of each digit (digit i's words are xd[2i + half]).
+// words of each digit (digit i's words are xd[2i + half]), as one chain from
+// digit 3 down (the running sum times 16 before each digit's dots): no
+// accumulator starts from zero but the first, and no partial sums are combined
+// afterwards. The sum is exact (|x| <= 30583, |q - 8| <= 8: below 2^24).
 __device__ __forceinline__ int dot_nibbles4(const uint4& W, const uint4* xd, int half) {
-    int a[4];
+    int t = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 3; i >= 0; --i) {
         const uint4 D = xd[2 * i + half];
-        int t = sdot8(W.x, D.x, 0);
+        t = sdot8(W.x, D.x, t * 16);
         t = sdot8(W.y, D.y, t);
         t = sdot8(W.z, D.z, t);
-        a[i] = sdot8(W.w, D.w, t);
+        t = sdot8(W.w, D.w, t);
     }
-    return ((a[3] * 16 + a[2]) * 16 + a[1]) * 16 + a[0];
+    return t;
 }
 
 // -------------------------------------------------------------------------
@@ -260,21 +268,28 @@ __device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const ui
         acc = y;
     } else if constexpr (FMT == Q8_0) {
         const float dd = half_lo(d.meta.x);
-        // digit planes: xd[0..1] low bytes, xd[2..3] high bytes (words 0-3, 4-7)
-        int lo = 0, hi = 0;
+        // digit planes: xd[0..1] low bytes, xd[2..3] high bytes (words 0-3,
+        // 4-7); the high bytes' sum times 256, then the low bytes' dots, in
+        // one chain (exact: |sum q x| <= 32 * 128 * 30583 < 2^31)
+        int t = 0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint4 W = d.q[h], L = xd[h], H = xd[2 + h];
-            lo = sdot4(W.x, L.x, lo);
-            lo = sdot4(W.y, L.y, lo);
-            lo = sdot4(W.z, L.z, lo);
-            lo = sdot4(W.w, L.w, lo);
-            hi = sdot4(W.x, H.x, hi);
-            hi = sdot4(W.y, H.y, hi);
-            hi = sdot4(W.z, H.z, hi);
-            hi = sdot4(W.w, H.w, hi);
+            const uint4 W = d.q[h], H = xd[2 + h];
+            t = sdot4(W.x, H.x, t);
+            t = sdot4(W.y, H.y, t);
+            t = sdot4(W.z, H.z, t);
+            t = sdot4(W.w, H.w, t);
         }
-        acc = fmaf(dd * sb0, (float)hi * 256.f + (float)lo, acc);
+        t *= 256;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 W = d.q[h], L = xd[h];
+            t = sdot4(W.x, L.x, t);
+            t = sdot4(W.y, L.y, t);
+            t = sdot4(W.z, L.z, t);
+            t = sdot4(W.w, L.w, t);
+        }
+        acc = fmaf(dd * sb0, (float)t, acc);
     } else if constexpr (FMT == Q6_K) {
         const float dd = half_lo(d.meta.y);
         float y = acc;
@@ -284,17 +299,17 @@ __device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const ui
             const uint32_t H = word(d.q[2], g);
             const uint32_t He = H & 0x33333333u, Ho = (H >> 2) & 0x33333333u;
             const float dsc = dd * (float)(int8_t)((d.meta.x >> (8 * g)) & 0xffu);
-            int al[4], ah[4];
+            // the low fields' and the high fields' sums over the digits, each
+            // one chain from digit 3 down (as dot_nibbles4)
+            int l = 0, h = 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 3; i >= 0; --i) {
                 // words 2g, 2g+1 of digit i: part 2i + g/2, components (g&1)*2, (g&1)*2+1
                 const uint4 D = xd[2 * i + (g >> 1)];
                 const uint32_t D0 = word(D, (g & 1) * 2), D1 = word(D, (g & 1) * 2 + 1);
-                al[i] = sdot8(L1, D1, sdot8(L0, D0, 0));
-                ah[i] = sdot8(Ho, D1, sdot8(He, D0, 0));
+                l = sdot8(L1, D1, sdot8(L0, D0, l * 16));
+                h = sdot8(Ho, D1, sdot8(He, D0, h * 16));
             }
-            const int l = ((al[3] * 16 + al[2]) * 16 + al[1]) * 16 + al[0];
-            const int h = ((ah[3] * 16 + ah[2]) * 16 + ah[1]) * 16 + ah[0];
             const float s = g < 2 ? sb0 : sb1;
             const float sx = g < 2 ? wordf(xb[0], 2 + g) : wordf(xb[1], g - 2);
             y = fmaf(dsc * s, (float)(h * 16 + l), y);

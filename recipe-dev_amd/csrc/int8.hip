@@ -181,16 +181,12 @@ __device__ __forceinline__ int dot4w(uint32_t q0, uint32_t q1, uint32_t q2, uint
     return sdot4(q3, c.w, s);
 }
 
-// get_scale_min_k4 of sub-block g from the superblock's meta words.
+// get_scale_min_k4 of sub-block g from the superblock's meta words (the
+// chunk fields of q4k_field).
 __device__ __forceinline__ void q4k_scale_min(const uint4& meta, int g, int& sc, int& m) {
-    if (g < 4) {
-        sc = (int)bfe(meta.y, 8 * g, 6);
-        m = (int)bfe(meta.z, 8 * g, 6);
-    } else {
-        const int o = 8 * (g - 4);
-        sc = (int)(bfe(meta.w, o, 4) | (bfe(meta.y, o + 6, 2) << 4));
-        m = (int)(bfe(meta.w, o + 4, 4) | (bfe(meta.z, o + 6, 2) << 4));
-    }
+    const uint32_t f = q4k_field(meta, g >> 1);
+    sc = (int)bfe(f, 12 * (g & 1), 6);
+    m = (int)bfe(f, 12 * (g & 1) + 6, 6);
 }
 
 // The dot of 16 stored nibbles (two words, XOR 8) with a slice's record bytes.

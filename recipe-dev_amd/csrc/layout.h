@@ -24,8 +24,10 @@
 //              meta0 = the two fp16 d per chunk (4 B). A row with an odd block
 //              count gets one zero block (d = 0) at its end.
 //   Q4_K (12)  chunk = the sub-block pair 2p, 2p+1 of a superblock (64 w); part j =
-//              sub-block 2p+j's 32 codes as above. meta0 = the superblock's first
-//              16 bytes (d, dmin, 12 bytes of 6-bit scales/mins), unchanged.
+//              sub-block 2p+j's 32 codes as above. meta0 = the superblock's d and
+//              dmin, then its 16 six-bit scales and minimums as four 24-bit
+//              fields, chunk p's at bit 24p (scale 2p, min 2p, scale 2p+1,
+//              min 2p+1): the k_scale bytes' 96 bits, reordered (repack.cpp).
 //   Q6_K (14)  chunk = a quarter superblock (64 w), 3 parts: parts 0-1 hold the
 //              64 low nibbles l as above; part 2 holds one word per 16-weight
 //              scale group g whose bits 4j..4j+1 are the high field h of weight

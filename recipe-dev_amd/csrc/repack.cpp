@@ -54,6 +54,60 @@ static uint32_t q6_high_word(const uint8_t* q6) {
     return w;
 }
 
+// Q4_K scales: the 12 k_scale bytes of a superblock (bytes 4..15 of the
+// block; get_scale_min_k4, recipe.rs:15204-15210: sub-block j < 4 has scale
+// s[j] & 63 and minimum s[j + 4] & 63, j >= 4 has scale (s[j + 4] & 15) |
+// (s[j - 4] >> 6) << 4 and minimum (s[j + 4] >> 4) | (s[j] >> 6) << 4) <->
+// the layout's four 24-bit fields, one per chunk p (sub-blocks 2p, 2p + 1):
+// bits 24p.. of the 96-bit little-endian value hold scale(2p), min(2p),
+// scale(2p + 1), min(2p + 1), six bits each. Both hold the same 96 bits.
+static void q4k_fields_from_kscale(const uint8_t* s, uint8_t* out12) {
+    uint8_t sc[8], mn[8];
+    for (int j = 0; j < 4; ++j) {
+        sc[j] = s[j] & 63;
+        mn[j] = s[j + 4] & 63;
+        sc[j + 4] = (uint8_t)((s[j + 8] & 15) | ((s[j] >> 6) << 4));
+        mn[j + 4] = (uint8_t)((s[j + 8] >> 4) | ((s[j + 4] >> 6) << 4));
+    }
+    uint64_t lo = 0, hi = 0;  // the 96 bits: lo = bits 0..63, hi = bits 64..95
+    for (int p = 0; p < 4; ++p) {
+        const uint64_t f = (uint64_t)sc[2 * p] | (uint64_t)mn[2 * p] << 6 | (uint64_t)sc[2 * p + 1] << 12 |
+                           (uint64_t)mn[2 * p + 1] << 18;
+        const int at = 24 * p;
+        if (at + 24 <= 64) lo |= f << at;
+        else if (at >= 64) hi |= f << (at - 64);
+        else {
+            lo |= f << at;
+            hi |= f >> (64 - at);
+        }
+    }
+    for (int i = 0; i < 8; ++i) out12[i] = (uint8_t)(lo >> (8 * i));
+    for (int i = 0; i < 4; ++i) out12[8 + i] = (uint8_t)(hi >> (8 * i));
+}
+
+static void q4k_kscale_from_fields(const uint8_t* in12, uint8_t* s) {
+    uint64_t lo = 0, hi = 0;
+    for (int i = 0; i < 8; ++i) lo |= (uint64_t)in12[i] << (8 * i);
+    for (int i = 0; i < 4; ++i) hi |= (uint64_t)in12[8 + i] << (8 * i);
+    uint8_t sc[8], mn[8];
+    for (int p = 0; p < 4; ++p) {
+        const int at = 24 * p;
+        uint64_t f;
+        if (at + 24 <= 64) f = lo >> at;
+        else if (at >= 64) f = hi >> (at - 64);
+        else f = (lo >> at) | (hi << (64 - at));
+        sc[2 * p] = f & 63;
+        mn[2 * p] = (f >> 6) & 63;
+        sc[2 * p + 1] = (f >> 12) & 63;
+        mn[2 * p + 1] = (f >> 18) & 63;
+    }
+    for (int j = 0; j < 4; ++j) {
+        s[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        s[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+        s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+    }
+}
+
 // Shapes the kernels take: rows below 2^31 (their row indices are 32-bit)
 // and cols at most 2^30, a whole number of blocks; both products below are
 // then checked for overflow, so that a shape read from an untrusted file
@@ -139,7 +193,10 @@ static void chunk_copy(int fmt, const uint8_t* src_blocks, uint8_t* dst_blocks, 
             const int64_t m_at = meta + (pl.within / 4) * 16;
             if (TO_LAYOUT) {
                 const uint8_t* blk = src_blocks + sb * 144;
-                if (p == 0) memcpy(dst_row + m_at, blk, 16);
+                if (p == 0) {
+                    memcpy(dst_row + m_at, blk, 4);  // d, dmin
+                    q4k_fields_from_kscale(blk + 4, dst_row + m_at + 4);
+                }
                 for (int h = 0; h < 2; ++h) {  // sub-block 2p + h: low or high nibbles of bytes 32p..32p+31
                     uint8_t q[32];
                     for (int i = 0; i < 32; ++i) q[i] = (blk[16 + 32 * p + i] >> (4 * h)) & 15;
@@ -147,7 +204,10 @@ static void chunk_copy(int fmt, const uint8_t* src_blocks, uint8_t* dst_blocks, 
                 }
             } else {
                 uint8_t* blk = dst_blocks + sb * 144;
-                if (p == 0) memcpy(blk, src_row + m_at, 16);
+                if (p == 0) {
+                    memcpy(blk, src_row + m_at, 4);
+                    q4k_kscale_from_fields(src_row + m_at + 4, blk + 4);
+                }
                 uint8_t lo[32], hi[32];
                 unpack_nibbles(src_row + part(0), lo);
                 unpack_nibbles(src_row + part(1), hi);

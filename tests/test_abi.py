@@ -95,7 +95,9 @@ def _nibbles(b16):
 
 def test_layout_parts_are_contiguous_per_wave():
     """Part h of 64 consecutive chunks forms one contiguous 1 KiB run; part h of
-    Q4_K chunk c holds sub-block 2(c % 4) + h's codes in order."""
+    Q4_K chunk c holds sub-block 2(c % 4) + h's codes in order; each
+    superblock's 16 scale bytes carry its 6-bit scales and minimums as one
+    24-bit field per chunk."""
     rows, cols = 1, 4096  # Q4_K: 64 chunks of 64 weights, 2 parts each
     w = synth.q4_k(rows, cols, seed=5)
     code = rqmv.repack_host("q4_k", rows, cols, w)
@@ -106,8 +108,22 @@ def test_layout_parts_are_contiguous_per_wave():
             got = _nibbles(code[(h * 64 + c) * 16:(h * 64 + c) * 16 + 16])
             want = (blk[sb, 16 + 32 * p:16 + 32 * p + 32].astype(np.int64) >> (4 * h)) & 15
             assert np.array_equal(got, want), (c, h)
-    # the group's scale bytes follow its two code parts
-    assert np.array_equal(code[2048:2304].reshape(16, 16), blk[:, :16])
+    # the group's scale bytes follow its two code parts: d and dmin as stored,
+    # then chunk p's 24-bit field at bit 24p holding scale(2p), min(2p),
+    # scale(2p+1), min(2p+1), against get_scale_min_k4 of the block's 12 bytes
+    meta = code[2048:2304].reshape(16, 16)
+    assert np.array_equal(meta[:, :4], blk[:, :4])
+    for sb in range(16):
+        s = blk[sb, 4:16].astype(np.int64)
+        want = []
+        for j in range(8):
+            if j < 4:
+                want += [s[j] & 63, s[j + 4] & 63]
+            else:
+                want += [(s[j + 4] & 15) | ((s[j - 4] >> 6) << 4), (s[j + 4] >> 4) | ((s[j] >> 6) << 4)]
+        v = int.from_bytes(bytes(meta[sb, 4:16]), "little")
+        got = [(v >> (6 * i)) & 63 for i in range(16)]  # fields back to back: sc, m per sub-block
+        assert got == want, sb
 
 
 def test_q6k_layout_decodes_each_code():
