@@ -421,12 +421,14 @@ __global__ void __launch_bounds__(kMoeThreads) moe_glu_kernel(MoeDims d, MoeBank
     }
 }
 
+// TAIL (with SPLIT, rows of 65-72 chunks): eight row waves and a ninth that
+// forms the partials of the chunks past 64 for all eight rows (below).
 // SPLIT (one or two positions, G = 32): one row per wave, its lanes taking
 // chunks lane, lane + 64, ... as 64 lanes would, with the sums formed in the
 // order of 32 lanes per row (lane g adds chunk g + 64 s, then lane g + 32's
 // chunk g + 32 + 64 s, through a 32-lane swap), so that every row carries the
 // bits of the 32-lane form with twice the waves.
-template <int FMT, bool RING, int BT = kMoeThreads, bool SPLIT = false>
+template <int FMT, bool RING, int BT = kMoeThreads, bool SPLIT = false, bool TAIL = false>
 __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, MoeBank down_sh, MoeWorkspace ws,
                                                         float* y, int G, MoeBatch batch) {
     constexpr int CW = Traits<FMT>::CW, XP = Traits<FMT>::XP;
@@ -441,7 +443,10 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
     uint4* xb = smem + XP * nch;
     static_assert(!(SPLIT && RING), "the split form is for one or two positions");
     const int lane = threadIdx.x & 63, g = SPLIT ? lane : lane & (G - 1), sub = SPLIT ? 0 : lane / G;
-    const int wpb = BT >> 6, wave = threadIdx.x >> 6;
+    // TAIL: the last wave takes chunks 64.. of the other waves' rows (its lane
+    // l: row l / 8, chunk 64 + l % 8)
+    const int wpb = (BT >> 6) - (TAIL ? 1 : 0), wave = threadIdx.x >> 6;
+    const bool tail_wave = TAIL && wave == wpb;
     const int rows_per_wave = SPLIT ? 1 : 64 / G;
     const int tiles = (d.d_model + rows_per_wave - 1) / rows_per_wave;
     // Chunk c of output row n: chunk lc of slot s's expert down row, or of the shared expert's.
@@ -470,13 +475,58 @@ __global__ void __launch_bounds__(BT) moe_down_kernel(MoeDims d, MoeBank down, M
     ChunkData<FMT> cd0, cd1;
     float w0, w1;
     int lc0, lc1;
-    fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd0, w0, lc0);
+    if (tail_wave)
+        fetch(blockIdx.x * wpb + (lane >> 3), 64 + (lane & 7), cd0, w0, lc0);
+    else
+        fetch((tile < tiles ? tile : tiles - 1) * rows_per_wave + sub, g, cd0, w0, lc0);
     __shared__ int wave_flags[BT / 64];
     publish_outliers(multi ? stage_multi_finish<FMT, true>(nch, K, 1, BT, it, xd, reinterpret_cast<float*>(xb))
                            : stage_all<FMT, true>(nch, K, ws.h, 0, 1, BT, xd, reinterpret_cast<float*>(xb)),
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, BT);
+    if constexpr (TAIL) {
+        // Rows of 65-72 chunks, one per wave, one tile per wave (the launch
+        // covers every row): the tail wave forms the partials of chunks 64..
+        // and hands them over through LDS, so that no wave takes a second
+        // step and the staging needs one item per thread. Each row's sum is
+        // the SPLIT form's, operation for operation: lane g < 32 adds chunk g,
+        // then chunk g + 32, then (g < nch - 64) chunk 64 + g.
+        __shared__ float tail_part[64];
+        __shared__ float tail_w[8];
+        const int c = tail_wave ? 64 + (lane & 7) : lane;
+        float part = 0.f;
+        if (c < nch) {
+            uint4 xv[XP];
+            uint4 bv[2];
+#pragma unroll
+            for (int j = 0; j < XP; ++j) xv[j] = xd[j * nch + c];
+            bv[0] = xb[c];
+            bv[1] = xb[nch + c];
+            dot_int<FMT>(cd0, lc0, xv, bv, part);
+            if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) dot_outliers<FMT>(cd0, lc0, xb + c, nch, part);
+        }
+        float acc = 0.f;
+        if (tail_wave) {
+            tail_part[lane] = part;
+            if (lane < 8) tail_w[lane] = w0;
+        } else {
+            float pu = part, wu = w0, pl = part, wl = w0;
+            asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(pl), "+v"(pu));
+            asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(wl), "+v"(wu));
+            if (lane < 32) {
+                acc = fmaf(w0, part, acc);
+                if (c + 32 < nch) acc = fmaf(wu, pu, acc);
+            }
+        }
+        __syncthreads();
+        if (tail_wave) return;
+        if (64 + lane < nch && lane < 8) acc = fmaf(tail_w[lane], tail_part[8 * wave + lane], acc);
+        acc = group_sum(acc, 32);
+        const int n = blockIdx.x * wpb + wave;
+        if (n < d.d_model && lane == 31) y[n] = acc;
+        return;
+    }
     if constexpr (SPLIT) {
         bool fetched = true;
         for (; tile < tiles; tile += stride) {
@@ -707,6 +757,20 @@ static hipError_t down_fmt(const MoeDims& d, const MoeBank& down, const MoeBank&
         const int scap = (batch_grid_cap(cus, b.m) * kMoeThreads + threads - 1) / threads;
         if (grid > scap) grid = scap;
         kernel = moe_down_kernel<FMT, false, 512, true>;
+        // rows of 65-72 chunks (eight routed slots of 64-weight chunks and a
+        // shared expert of the same width): a ninth wave per workgroup takes
+        // the chunks past 64 of the eight rows, when one launch covers them.
+        // On the gguf_moe workload (72 chunks) the step goes 17.18 -> 15.89 us
+        // (graph replays, five alternating runs): no lane waits for a second
+        // weight load after its first dot, and 576 threads stage the 576 items
+        // in one round. RQMV_MOE_DOWN_TAIL=0 turns it off.
+        const int tgrid = (d.d_model + 7) / 8;
+        if (nch > 64 && nch <= 72 && tgrid <= (batch_grid_cap(cus, b.m) * kMoeThreads + 575) / 576 &&
+            env_flag("RQMV_MOE_DOWN_TAIL", true)) {
+            threads = 576;
+            grid = tgrid;
+            kernel = moe_down_kernel<FMT, false, 576, true, true>;
+        }
     }
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),

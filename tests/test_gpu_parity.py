@@ -772,6 +772,39 @@ def test_weight_of_4_gib_is_rejected(gpu):
         gpu.Weight("q8_0", 4000, cols, big, experts=250)
 
 
+@pytest.mark.parametrize("fmt,d,E,top,H,HS,m,xdt", [
+    ("q4_k", 1024, 32, 8, 512, 256, 2, "f16"),   # 64 routed + 4 shared chunks per down row
+    ("q6_k", 512, 16, 9, 512, 0, 3, "f16"),      # 72 routed chunks, no shared expert
+    ("q4_0", 768, 24, 4, 1024, 512, 5, "f32"),   # 64 routed + 8 shared chunks
+])
+def test_moe_down_rows_past_64_chunks(gpu, fmt, d, E, top, H, HS, m, xdt):
+    """Down rows of 65-72 chunks. At one position a ninth wave per workgroup
+    forms the partials of every row's chunks past 64 and hands them to the row
+    waves through LDS; the row sums must be those of the batch forms (two to
+    five positions: other kernels) bit for bit, and match the oracle."""
+    gated = HS > 0
+    router, gate, up, down, shared = _moe_case(fmt, d, E, top, H, HS, gated, seed=5 * E + top)
+    xh, dt, x32 = _x(m, d, xdt, seed=d + top)
+    kw, okw = {}, {}
+    if shared is not None:
+        sg, gs, us, ds = shared
+        kw = dict(shared_gate_inp=gpu.Weight("f16", 1, d, sg), gate_sh=gpu.Weight(fmt, HS, d, gs),
+                  up_sh=gpu.Weight(fmt, HS, d, us), down_sh=gpu.Weight(fmt, d, HS, ds))
+        okw = dict(hidden_shared=HS, shared_gate_bits=sg.view(np.uint16), gate_sh=gs, up_sh=us, down_sh=ds)
+    moe = gpu.Moe(gpu.Weight("f16", E, d, router), gpu.Weight(fmt, H, d, gate, experts=E),
+                  gpu.Weight(fmt, H, d, up, experts=E), gpu.Weight(fmt, d, H, down, experts=E), top, **kw)
+    y, route = moe(xh)
+    for p in range(m):
+        y_ref, rw_ref = oracle.moe_f64(fmt, d, E, top, H, router.view(np.uint16), gate, up, down,
+                                       x32[p].astype(np.float64), **okw)
+        assert np.array_equal(route[p] != 0, rw_ref != 0), p
+        err = rel_l2(y[p], y_ref)
+        print(f"moe {fmt} d={d} top={top} H={H} HS={HS} position {p}: rel-L2 {err:.3e}", flush=True)
+        assert err <= REL_L2, p
+        y1, r1 = moe(xh[p])
+        assert np.array_equal(y1, y[p]) and np.array_equal(r1, route[p]), p
+
+
 @pytest.mark.parametrize("m,xdt", [(2, "f16"), (5, "f32"), (8, "f16"), (16, "f32"), (19, "f16"), (64, "f16")])
 def test_moe_batch_parity(gpu, m, xdt):
     """A prefill batch of positions through rqmv_moe_batch: each position routed
