@@ -129,7 +129,7 @@ def stream_copy(achieved_gbs, nbytes=1 << 30, reps=20):
     log(f"bench: device copy {gbs:.0f} GB/s (read + write)")
     return {"value": round(gbs, 1), "unit": "GB/s", "bytes_per_copy": 2 * nbytes,
             "method": "hipMemcpyAsync device to device of 1 GiB, bytes read + written",
-            "frac": round(achieved_gbs / gbs, 4)}
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "workload_frac_of_copy": round(achieved_gbs / gbs, 4)}
 
 
 def cpu_baseline(fmt, rows, cols, x32, seconds, weights_bytes, alg_bytes):
@@ -795,6 +795,8 @@ def main():
         "stream_copy": stream_copy(achieved),
         "kernel_us": round(ker_ms * 1e3, 3),
         "kernel_us_median": round(float(np.median(ker)) * 1e3, 3),
+        "kernel_us_p10": round(float(np.percentile(ker, 10)) * 1e3, 3),
+        "kernel_us_p90": round(float(np.percentile(ker, 90)) * 1e3, 3),
         "gflops": round(flops / (ker_ms * 1e-3) / 1e9, 1),
         "parity_rel_l2": rel,
     }
