@@ -88,7 +88,7 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(float* qkv, const int* pos
 // Split over positions (flash decoding), in two launches.
 //
 // attention_kernel: one workgroup of kAttnThreads per (kv head, chunk of
-// kAttnChunk positions); a chunk is read once for every query head of its
+// attn_chunk(HD) positions); a chunk is read once for every query head of its
 // group. Lanes take one 16-byte piece (eight values) of a position's key and
 // value: HD / 8 lanes per position, the whole chunk's keys and values loaded
 // into registers before any arithmetic (addresses clamped into the cache;
@@ -117,7 +117,11 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(float* qkv, const int* pos
 // (A single launch whose last workgroup merges costs more: publishing the
 // partial results across the XCDs' L2 caches takes an L2 write-back per
 // workgroup.)
-constexpr int kAttnChunk = 64;
+// Positions per chunk: 64, or 80 at head width 128 (five sweeps of 16
+// positions), so that a context of 4,097 positions over 8 kv heads takes 416
+// workgroups, at most two per CU, where 64 gave 520 and a third workgroup on
+// one CU of every XCD.
+__host__ __device__ constexpr int attn_chunk(int hd) { return hd == 128 ? 80 : 64; }
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kAttnMaxGroup = 8;      // query heads per kv head
@@ -286,7 +290,8 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
                                                                  AttnWork ws, int nchunks) {
     constexpr int LPP = HD / 8;                    // lanes per position
     constexpr int PPS = kAttnThreads / LPP;        // positions per sweep
-    constexpr int NS = kAttnChunk / PPS;           // sweeps per chunk
+    constexpr int CH = attn_chunk(HD);            // positions per chunk
+    constexpr int NS = CH / PPS;                   // sweeps per chunk
     constexpr int HALF = HD / 2;
     __shared__ float wml[kAttnWaves][MAXG][2];  // each wave's (maximum, weight sum) per head
     // the partial outputs: with at most four query heads, one padded row per
@@ -298,7 +303,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     const int kh = blockIdx.x, chunk = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int b = t % LPP, slot = t / LPP;
-    const int t0 = chunk * kAttnChunk;
+    const int t0 = chunk * CH;
     // Every load is issued before the first wait. The queries and, under ROPE,
     // the new key and value do not depend on the position, so they go out
     // while it is read; slots past the group read the group's last head (their
@@ -365,7 +370,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
         const int jn = pos - t0 - slot;
         k16 = pack8(kn);
         v16 = pack8(vn);
-        if (pos < max_ctx && jn >= 0 && jn < kAttnChunk && jn % PPS == 0) {
+        if (pos < max_ctx && jn >= 0 && jn < CH && jn % PPS == 0) {
             *reinterpret_cast<uint4*>(kc + (head_base + pos) * HD + b * 8) = k16;
             *reinterpret_cast<uint4*>(vc + (head_base + pos) * HD + b * 8) = v16;
             jsel = jn / PPS;  // (the sweep whose key and value this lane takes from k16, v16)
@@ -437,7 +442,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(const float* q,
     };
     // (wholly inside the live length and, under ROPE, wholly before the new
     // position)
-    if (t0 + kAttnChunk <= (ROPE ? min(pos, len) : len)) passes(std::true_type{});
+    if (t0 + CH <= (ROPE ? min(pos, len) : len)) passes(std::true_type{});
     else passes(std::false_type{});
     if constexpr (kSlotRows) {
         // every lane's sums go to its slot's row; each output then adds the
@@ -540,7 +545,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnWork ws, const in
         mlv[k] = *reinterpret_cast<const float2*>(hml + 2 * c);
     }
     const int len = min(*pos_dev + 1, max_ctx);
-    const int live = (len + kAttnChunk - 1) / kAttnChunk;
+    const int live = (len + attn_chunk(HD) - 1) / attn_chunk(HD);
     // this wave's maximum and weight sum over its lanes' live chunks
     float Mw = -INFINITY;
 #pragma unroll
@@ -713,7 +718,7 @@ hipError_t launch_rope_kv(float* qkv, const int* pos, int nq, int nkv, int hd, d
 }
 
 size_t attention_workspace_bytes(int nq, int hd, int max_ctx) {
-    const size_t nchunks = (size_t)(max_ctx + kAttnChunk - 1) / kAttnChunk;
+    const size_t nchunks = (size_t)(max_ctx + attn_chunk(hd) - 1) / attn_chunk(hd);
     return (nq * nchunks * 2 + nq * nchunks * (size_t)hd) * sizeof(float);
 }
 
@@ -765,7 +770,7 @@ static hipError_t launch_attention_any(int hd, const AttnLaunch& a, hipStream_t 
 
 static bool attention_shape_ok(int nq, int nkv, int hd, int max_ctx) {
     return nkv >= 1 && nq % nkv == 0 && nq / nkv <= kAttnMaxGroup && (hd == 64 || hd == 128 || hd == 256) &&
-           max_ctx <= kAttnMaxChunks * kAttnChunk;
+           max_ctx <= kAttnMaxChunks * attn_chunk(hd);
 }
 
 hipError_t launch_attention(const float* q, const __half* kc, const __half* vc, const int* pos, int nq, int nkv,
@@ -781,7 +786,7 @@ hipError_t launch_attention(const float* q, const __half* kc, const __half* vc, 
     a.nkv = nkv;
     a.group = nq / nkv;
     a.max_ctx = max_ctx;
-    a.nchunks = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    a.nchunks = (max_ctx + attn_chunk(hd) - 1) / attn_chunk(hd);
     a.ws = attn_work(workspace, nq, hd, a.nchunks);
     a.out = out;
     return launch_attention_any<false>(hd, a, stream);
@@ -801,7 +806,7 @@ hipError_t launch_attention_rope(const float* qkv, const float2* rope_table, __h
     a.nkv = nkv;
     a.group = nq / nkv;
     a.max_ctx = max_ctx;
-    a.nchunks = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    a.nchunks = (max_ctx + attn_chunk(hd) - 1) / attn_chunk(hd);
     a.ws = attn_work(workspace, nq, hd, a.nchunks);
     a.out = out;
     return launch_attention_any<true>(hd, a, stream);
