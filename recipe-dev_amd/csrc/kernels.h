@@ -29,6 +29,9 @@ struct MvParams {
     int rows_per_wave = 1;
     int tiles = 0;
     int steps = 1;
+    // 1: first tiles numbered SIMD-group-major across the workgroups (matvec.hip
+    // make_walk), for launches whose tiles do not divide evenly over the waves
+    int spread = 0;
     // F16 weights only: rows at or past `split` come from P2 (row - split), so
     // that two weights of one width run as one launch (an MoE router and its
     // shared-expert gate). split >= rows: P alone.

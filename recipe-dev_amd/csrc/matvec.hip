@@ -53,7 +53,17 @@ __device__ __forceinline__ StepWalk make_walk(const MvParams& p, int R, int g) {
     const int wpb = p.block >> 6, wave = threadIdx.x >> 6;
     w.rows_per_wave = p.rows_per_wave;
     w.tiles = p.tiles;
-    w.tile = (int)blockIdx.x * wpb + wave;
+    // The wave's first tile: workgroup-major, or with p.spread (wide
+    // workgroups whose tiles do not divide evenly over the waves) the first
+    // four waves of every workgroup before the next four of any (waves w and
+    // w + 4 share a SIMD), so that the last round's tiles spread over every CU
+    // and SIMD instead of going to the first workgroups' waves, which at one
+    // 512-thread workgroup per CU left half of the CUs with twice the last
+    // round's work.
+    if (p.spread && wpb > 4)
+        w.tile = (wave & 3) + 4 * ((int)blockIdx.x + (int)gridDim.x * (wave >> 2));
+    else
+        w.tile = (int)blockIdx.x * wpb + wave;
     w.tile_stride = (int)gridDim.x * wpb;
     w.s = 0;
     w.steps = p.steps;
@@ -646,8 +656,15 @@ LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu) {
 }
 
 template <int FMT, int R = 2>
-static hipError_t launch_fused_fmt(const MvParams& p, const LaunchShape& s, hipStream_t stream) {
-    const size_t lds = matvec_lds_bytes(FMT, X_F32, 1, p.K);
+static hipError_t launch_fused_fmt(const MvParams& p0, const LaunchShape& s, hipStream_t stream) {
+    const size_t lds = matvec_lds_bytes(FMT, X_F32, 1, p0.K);
+    MvParams p = p0;
+    const int64_t rows_per_wave = (int64_t)(64 / s.G) * R, waves = (int64_t)s.grid * (s.block / 64);
+    const int64_t tiles = (p.rows + rows_per_wave - 1) / rows_per_wave;
+    // tiles that do not divide over the waves (the decode step's QKV product:
+    // 3,072 tiles on 2,048 waves) take the spread numbering: 589.6 -> 594.6
+    // tok/s (three alternating runs). RQMV_SPREAD=0 keeps workgroup-major.
+    p.spread = env_int("RQMV_SPREAD", 1) != 0 && tiles % waves != 0;
     if (p.norm_w) return launch_kernel(matvec_int<FMT, 1, R, true, true>, p, s, lds, stream, nullptr, nullptr);
     return launch_kernel(matvec_int<FMT, 1, R, true>, p, s, lds, stream, nullptr, nullptr);
 }
