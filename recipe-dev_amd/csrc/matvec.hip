@@ -156,7 +156,7 @@ __device__ __forceinline__ void load_rows_rs(const MvParams& p, __amdgpu_buffer_
 
 // One step of matvec_int: the lane's chunk of its R rows against the staged
 // digits of every activation row; the tile's reduction after its last step.
-template <int FMT, int M, int R, bool NORM = false>
+template <int FMT, int M, int R, bool NORM = false, bool FIN = true>
 __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, int sub, int g, const ChunkData<FMT> (&d)[R],
                                          float (&acc)[R][M], const uint4* xd, const uint4* xb, bool outliers,
                                          float norm_scale = 1.f) {
@@ -184,7 +184,7 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
             }
         }
     }
-    if (w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, norm_scale);
+    if (FIN && w.s == w.steps - 1) finish_tile<M, R, NORM>(p, row0, g, acc, norm_scale);
 }
 
 // Quantized weights, integer dot of staged activation digits (chunk.h,
@@ -272,6 +272,78 @@ __global__ void __launch_bounds__(512) matvec_int(MvParams p) {
     }
 done:
     return;
+}
+
+// Long rows at one fp16 activation row, each row tile taken by two waves of
+// one 1,024-thread workgroup, one per half of the row's steps (steps
+// [0, ceil(S / 2)) and the rest). The workgroup stages x once for twice the
+// waves, so each thread encodes half the items of the 512-thread form before
+// the first dot, and each wave walks half the steps. Every row-wave holds one
+// tile (the host checks); the second half's group sums reach the first
+// through LDS after the one barrier, and the row is half 0 + half 1.
+template <int FMT, int R>
+__global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
+    constexpr int NB = 2;
+    constexpr int XP = Traits<FMT>::XP;
+    extern __shared__ uint4 smem[];
+    __shared__ int wave_flags[16];
+    __shared__ float half_sum[8][8];  // [row wave][row of its tile]: the second half's sums
+    const int nch = p.P.nch;
+    uint4* xd = smem;
+    uint4* xb = smem + XP * nch;
+    const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane >> p.g_shift;
+    const int wave = threadIdx.x >> 6, half = p.block >> 7;  // row waves per workgroup
+    const int kh = wave >= half ? 1 : 0, rw = wave - kh * half;
+    const __amdgpu_buffer_rsrc_t rs = planes_rsrc(p.P);
+    const int s_mid = (p.steps + 1) >> 1;
+    StepWalk w[NB];
+    w[0].rows_per_wave = p.rows_per_wave;
+    w[0].tiles = p.tiles;
+    w[0].tile = (int)blockIdx.x * half + rw;
+    w[0].tile_stride = (int)gridDim.x * half;
+    w[0].s = kh ? s_mid : 0;
+    w[0].steps = kh ? p.steps : s_mid;
+    w[0].g = g;
+    w[0].G = p.G;
+    w[0].nch = nch;
+    w[1] = w[0];
+    w[1].next();
+    ChunkData<FMT> buf[NB][R];
+    StageItem<false> it[kStageNJ];
+    stage_multi_issue<FMT, false>(nch, p.K, p.x, p.ldx, 1, p.block, it);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
+    publish_outliers(stage_multi_finish<FMT, false>(nch, p.K, 1, p.block, it, xd, reinterpret_cast<float*>(xb)),
+                     wave_flags);
+    __syncthreads();
+    const bool outliers = read_outliers(wave_flags, p.block);
+    float acc[R][1];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][0] = 0.f;
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (!w[i].valid()) goto done;
+            step_int<FMT, 1, R, false, false>(p, w[i], sub, g, buf[i], acc, xd, xb, outliers);
+            w[i] = w[(i + NB - 1) % NB];
+            w[i].next();
+            load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
+        }
+    }
+done:
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][0] = group_sum(acc[r][0], p.G);
+    if (kh == 1 && g == p.G - 1)
+#pragma unroll
+        for (int r = 0; r < R; ++r) half_sum[rw][sub * R + r] = acc[r][0];
+    __syncthreads();
+    const int row0 = ((int)blockIdx.x * half + rw) * p.rows_per_wave + sub * R;
+    if (kh == 0 && g == p.G - 1)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < (int)p.rows) p.y[row0 + r] = acc[r][0] + half_sum[rw][sub * R + r];
 }
 
 // Burst form of matvec_int for long rows at one or two activation rows: every
@@ -464,12 +536,16 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     const bool long_rows = nch > 128;
     s.block = long_rows ? 512 : 256;
     int per_cu = long_rows ? 1 : 2;
-    // Long Q4_K rows at one fp16 activation row: 32 lanes per row and one row
-    // per lane group (two rows per wave, seven steps each at 14336 columns)
-    // measured faster than 64 lanes and two rows per group: Q4_K 14336->4096
-    // kernel 10.37 -> 10.00 us (three alternating pairs). With fp32 rows (the
-    // decode step's down product) it was slower: 568 -> 548 tok/s.
-    if (fmt == Q4_K && M == 1 && long_rows && xtype == X_F16) {
+    // Long Q4_K and Q4_0 rows at one fp16 activation row: 32 lanes per row
+    // and one row per lane group (two rows per wave, seven steps each at 14336
+    // columns). For Q4_K it measured faster than 64 lanes and two rows per
+    // group on its own (Q4_K 14336->4096 kernel 10.37 -> 10.00 us, three
+    // alternating pairs); both formats then run two waves per tile
+    // (matvec_int_k2), which at 64 lanes and two rows measured slower for Q4_0
+    // (9.78 -> 10.44 us) and at 32 lanes and one row faster (8.82). With fp32
+    // rows (the decode step's down product) the shape was slower: 568 -> 548
+    // tok/s.
+    if ((fmt == Q4_K || fmt == Q4_0) && M == 1 && long_rows && xtype == X_F16) {
         s.G = 32;
         s.R = 1;
     }
@@ -528,6 +604,21 @@ static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s,
         if (xtype == X_F16) return launch_kernel(matvec_f16w<M, R, false>, p, s, lds, stream, ev0, ev1);
         return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
+        if constexpr (M == 1 && R == 1) {
+            // long rows at one fp16 row, 32 lanes and one row per lane group on
+            // 512-thread workgroups with one tile per wave: two waves per tile
+            // (matvec_int_k2). Q4_K 14336->4096 10.16 -> 9.07 us, Q4_0 9.78 ->
+            // 8.82 (three alternating runs each). RQMV_K2=0 keeps the one-wave
+            // form.
+            const int64_t rows_per_wave = (int64_t)(64 / s.G) * R, steps = (p.P.nch + s.G - 1) / s.G;
+            const int64_t tiles = (p.rows + rows_per_wave - 1) / rows_per_wave;
+            if (xtype == X_F16 && s.block == 512 && s.G == 32 && p.P.nch > 128 && steps >= 2 &&
+                (int64_t)s.grid * 8 >= tiles && env_int("RQMV_K2", 1)) {
+                LaunchShape s2 = s;
+                s2.block = 1024;
+                return launch_kernel(matvec_int_k2<FMT, R>, p, s2, lds, stream, ev0, ev1);
+            }
+        }
         if (xtype == X_F16) return launch_kernel(matvec_int<FMT, M, R, false>, p, s, lds, stream, ev0, ev1);
         return launch_kernel(matvec_int<FMT, M, R, true>, p, s, lds, stream, ev0, ev1);
     }
