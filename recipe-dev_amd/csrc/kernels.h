@@ -81,7 +81,7 @@ size_t matvec_lds_bytes(int fmt, int xtype, int M, int cols);
 
 // The decode-step fused product (M = 1, fp32 activations, quantized weight):
 // the launch shape it uses and the launch itself.
-LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu);
+LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu, bool norm);
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream);
 
 // Matrix-core product for 1 <= M <= 32 activation rows (quantized formats).

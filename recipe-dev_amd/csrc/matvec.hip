@@ -281,7 +281,7 @@ done:
 // the first dot, and each wave walks half the steps. Every row-wave holds one
 // tile (the host checks); the second half's group sums reach the first
 // through LDS after the one barrier, and the row is half 0 + half 1.
-template <int FMT, int R>
+template <int FMT, int R, bool XF32 = false>
 __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     constexpr int NB = 2;
     constexpr int XP = Traits<FMT>::XP;
@@ -309,13 +309,13 @@ __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     w[1] = w[0];
     w[1].next();
     ChunkData<FMT> buf[NB][R];
-    StageItem<false> it[kStageNJ];
-    stage_multi_issue<FMT, false>(nch, p.K, p.x, p.ldx, 1, p.block, it);
+    StageItem<XF32> it[kStageNJ];
+    stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, 1, p.block, it);
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
-    publish_outliers(stage_multi_finish<FMT, false>(nch, p.K, 1, p.block, it, xd, reinterpret_cast<float*>(xb)),
+    publish_outliers(stage_multi_finish<FMT, XF32>(nch, p.K, 1, p.block, it, xd, reinterpret_cast<float*>(xb)),
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, p.block);
@@ -513,9 +513,32 @@ static int env_int(const char* name, int fallback) {
     return v && *v ? atoi(v) : fallback;
 }
 
-LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus) {
+// The long-row form (matvec_int_k2): Q4_K and Q4_0 rows of more than 128
+// chunks at one activation row, 32 lanes and one row per lane group, every
+// row tile (two rows) taken by two waves of a 1,024-thread workgroup, one per
+// half of its steps, when one launch of at most one workgroup per CU gives
+// every tile its waves. Measured (kernel us, three alternating runs): with
+// fp16 x, Q4_K 14336->4096 10.37 (64 lanes, two rows per group) -> 10.00 (32
+// lanes, one row) -> 9.07-9.38 (two waves per tile); Q4_0 9.78 -> 9.94 ->
+// 8.82, where two waves per tile at 64 lanes and two rows measured slower
+// (10.44). With fp32 x (the decode step's down product, through the fused
+// entry point) 32 lanes and one row alone were slower (568 -> 548 tok/s) and
+// two waves per tile faster (597.0 -> 614.1). RQMV_K2=0 turns it off.
+static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int cus, LaunchShape& s) {
+    if ((fmt != Q4_K && fmt != Q4_0) || M != 1 || nch <= 128 || !env_int("RQMV_K2", 1)) return false;
+    const int64_t tiles = (rows + 1) / 2;
+    if (tiles > (int64_t)8 * cus) return false;
+    s.G = 32;
+    s.R = 1;
+    s.block = 1024;
+    s.grid = (int)((tiles + 7) / 8);
+    return true;
+}
+
+static LaunchShape plan_matvec_impl(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus, bool k2) {
     LaunchShape s;
     const int64_t nch = chunks_per_row(fmt, cols);
+    if (k2 && k2_shape(fmt, rows, nch, M, cus, s)) return s;
     int G = 64;
     while (G > 8 && G > nch) G >>= 1;
     // Q6_K rows of 65-95 chunks (5120 columns: 80) leave a 64-lane group's
@@ -536,16 +559,11 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     const bool long_rows = nch > 128;
     s.block = long_rows ? 512 : 256;
     int per_cu = long_rows ? 1 : 2;
-    // Long Q4_K and Q4_0 rows at one fp16 activation row: 32 lanes per row
-    // and one row per lane group (two rows per wave, seven steps each at 14336
-    // columns). For Q4_K it measured faster than 64 lanes and two rows per
-    // group on its own (Q4_K 14336->4096 kernel 10.37 -> 10.00 us, three
-    // alternating pairs); both formats then run two waves per tile
-    // (matvec_int_k2), which at 64 lanes and two rows measured slower for Q4_0
-    // (9.78 -> 10.44 us) and at 32 lanes and one row faster (8.82). With fp32
-    // rows (the decode step's down product) the shape was slower: 568 -> 548
-    // tok/s.
-    if ((fmt == Q4_K || fmt == Q4_0) && M == 1 && long_rows && xtype == X_F16) {
+    // Long Q4_K rows at one fp16 activation row (where the long-row form does
+    // not apply): 32 lanes per row and one row per lane group (Q4_K
+    // 14336->4096 kernel 10.37 -> 10.00 us with 64 lanes and two rows before
+    // it; with fp32 rows it was slower, 568 -> 548 tok/s on the decode step).
+    if (fmt == Q4_K && M == 1 && long_rows && xtype == X_F16) {
         s.G = 32;
         s.R = 1;
     }
@@ -577,6 +595,10 @@ LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, i
     return s;
 }
 
+LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus) {
+    return plan_matvec_impl(fmt, rows, cols, M, xtype, cus, true);
+}
+
 template <typename K>
 static hipError_t launch_kernel(K kernel, const MvParams& p_in, const LaunchShape& s, size_t lds, hipStream_t stream,
                                 hipEvent_t ev0, hipEvent_t ev1) {
@@ -604,20 +626,12 @@ static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s,
         if (xtype == X_F16) return launch_kernel(matvec_f16w<M, R, false>, p, s, lds, stream, ev0, ev1);
         return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
-        if constexpr (M == 1 && R == 1) {
-            // long rows at one fp16 row, 32 lanes and one row per lane group on
-            // 512-thread workgroups with one tile per wave: two waves per tile
-            // (matvec_int_k2). Q4_K 14336->4096 10.16 -> 9.07 us, Q4_0 9.78 ->
-            // 8.82 (three alternating runs each). RQMV_K2=0 keeps the one-wave
-            // form.
-            const int64_t rows_per_wave = (int64_t)(64 / s.G) * R, steps = (p.P.nch + s.G - 1) / s.G;
-            const int64_t tiles = (p.rows + rows_per_wave - 1) / rows_per_wave;
-            if (xtype == X_F16 && s.block == 512 && s.G == 32 && p.P.nch > 128 && steps >= 2 &&
-                (int64_t)s.grid * 8 >= tiles && env_int("RQMV_K2", 1)) {
-                LaunchShape s2 = s;
-                s2.block = 1024;
-                return launch_kernel(matvec_int_k2<FMT, R>, p, s2, lds, stream, ev0, ev1);
+        if (s.block == 1024) {  // the long-row form (k2_shape)
+            if constexpr (M == 1 && R == 1) {
+                if (xtype == X_F16) return launch_kernel(matvec_int_k2<FMT, 1, false>, p, s, lds, stream, ev0, ev1);
+                return launch_kernel(matvec_int_k2<FMT, 1, true>, p, s, lds, stream, ev0, ev1);
             }
+            return hipErrorInvalidValue;
         }
         if (xtype == X_F16) return launch_kernel(matvec_int<FMT, M, R, false>, p, s, lds, stream, ev0, ev1);
         return launch_kernel(matvec_int<FMT, M, R, true>, p, s, lds, stream, ev0, ev1);
@@ -720,8 +734,12 @@ hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const Lau
     }
 }
 
-LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu) {
-    LaunchShape s = plan_matvec(fmt, rows, cols, 1, X_F32, cus);
+LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu, bool norm) {
+    LaunchShape s;
+    // plain products (no prologue, no epilogue) take the plain entry point's
+    // long-row form where it applies, with the same shape
+    if (!glu && !norm && k2_shape(fmt, rows, chunks_per_row(fmt, cols), 1, cus, s)) return s;
+    s = plan_matvec_impl(fmt, rows, cols, 1, X_F32, cus, false);
     // a lane group holds a (gate, up) row pair for kEpiGlu; otherwise Q8_0
     // takes one row, as in plan_matvec
     s.R = glu || fmt != Q8_0 ? 2 : 1;
@@ -761,6 +779,15 @@ static hipError_t launch_fused_fmt(const MvParams& p0, const LaunchShape& s, hip
 }
 
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream) {
+    if (s.block == 1024) {
+        // the long-row form (plain products only; plan_fused gives it the plain
+        // entry point's shape, so the two stay bit-identical)
+        if (p.norm_w || p.epi != kEpiPlain) return hipErrorInvalidValue;
+        const size_t lds = matvec_lds_bytes(fmt, X_F32, 1, p.K);
+        if (fmt == Q4_K) return launch_kernel(matvec_int_k2<Q4_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
+        if (fmt == Q4_0) return launch_kernel(matvec_int_k2<Q4_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
+        return hipErrorInvalidValue;
+    }
     if (s.block > 512) return hipErrorInvalidValue;
     if (s.R == 1 && fmt == Q8_0 && p.epi != kEpiGlu) return launch_fused_fmt<Q8_0, 1>(p, s, stream);
     if (s.R != 2) return hipErrorInvalidValue;

@@ -439,7 +439,8 @@ int rqmv_matvec_fused(const rqmv_weight* w, const float* x_dev, float* y_dev, co
     if (rq::matvec_lds_bytes(w->fmt, RQMV_DTYPE_F32, 1, (int)w->cols) > info.lds_limit)
         return fail(RQMV_EINVAL, "fused: cols too large for one LDS stage");
     if (!y_dev) return fail(RQMV_EINVAL, "fused: y is NULL");
-    const rq::LaunchShape s = rq::plan_fused(w->fmt, w->rows, w->cols, info.cus, f->epilogue == RQMV_EPI_GLU);
+    const rq::LaunchShape s = rq::plan_fused(w->fmt, w->rows, w->cols, info.cus, f->epilogue == RQMV_EPI_GLU,
+                                             f->norm_weight != nullptr);
     p.G = s.G;
     switch (f->epilogue) {
         case RQMV_EPI_PLAIN: break;

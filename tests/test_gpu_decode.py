@@ -315,10 +315,12 @@ def test_fused_glu_epilogue(gpu, fmt, n, cols):
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q8_0", 1001, 544), ("q8_0", 4096, 4096), ("q4_0", 77, 128),
-                                           ("q4_k", 6143, 4096)])
+                                           ("q4_k", 6143, 4096), ("q4_k", 4096, 14336), ("q4_0", 1001, 14336),
+                                           ("q4_k", 4097, 8448)])
 def test_fused_plain_without_norm(gpu, fmt, rows, cols):
     """The fused entry point with neither prologue nor epilogue equals the plain
-    product bit for bit (one launch shape per format and row count)."""
+    product bit for bit (one launch shape per format and row count; long Q4_K
+    and Q4_0 rows take the two-waves-per-tile form up to 4,096 rows in both)."""
     w = synth.weights(fmt, rows, cols, seed=rows)
     W = gpu.Weight(fmt, rows, cols, w)
     x = RNG.standard_normal(cols).astype(np.float32)

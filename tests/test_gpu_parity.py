@@ -535,6 +535,27 @@ def test_matvec_ldx_ldy_strides(gpu):
     assert (y[:, rows:] == 0).all()  # nothing written past the rows
 
 
+# ------------------------------------------------------ long-row form ----
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q4_0"])
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("rows,cols", [(1, 14336), (37, 8448), (1001, 14336), (4096, 14336), (4097, 8448)])
+def test_long_row_form(gpu, fmt, xdt, rows, cols):
+    """Rows of more than 128 chunks at one activation row: each two-row tile
+    taken by two waves, one per half of its steps (up to 4,096 rows), or the
+    one-wave form beyond. Parity with recipe's fp32 order, including a tile
+    count that leaves some of the last workgroup's waves without a tile, an
+    odd step count (8,448 columns: five steps of 32 chunks) and a single row."""
+    w = synth.weights(fmt, rows, cols, seed=rows + cols)
+    W = gpu.Weight(fmt, rows, cols, w)
+    xh, dt, x32 = _x(1, cols, xdt, seed=cols)
+    y = _run_matvec(gpu, W, xh, dt, rows)
+    ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+    err = rel_l2(y, ref)
+    print(f"long rows {fmt} {xdt} {rows}x{cols}: rel-L2 {err:.3e}", flush=True)
+    assert err <= 2e-4, err
+
+
 # ------------------------------------------------- workload-size configs ----
 
 CONFIGS = [
