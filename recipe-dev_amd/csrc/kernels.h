@@ -58,6 +58,7 @@ struct LaunchShape {
     int R = 1;        // rows per lane group per tile
     int block = 256;  // threads per workgroup
     int grid = 0;     // workgroups (0 = derive)
+    bool k2 = false;  // two waves per row tile (matvec_int_k2)
 };
 
 // Chooses G, R, block and grid for a product; honours RQMV_G / RQMV_R /

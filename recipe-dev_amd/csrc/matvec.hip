@@ -274,20 +274,22 @@ done:
     return;
 }
 
-// Long rows at one fp16 activation row, each row tile taken by two waves of
-// one 1,024-thread workgroup, one per half of the row's steps (steps
-// [0, ceil(S / 2)) and the rest). The workgroup stages x once for twice the
-// waves, so each thread encodes half the items of the 512-thread form before
-// the first dot, and each wave walks half the steps. Every row-wave holds one
-// tile (the host checks); the second half's group sums reach the first
-// through LDS after the one barrier, and the row is half 0 + half 1.
+// The long-row form (k2_shape): each row tile taken by two waves of one
+// workgroup, one per half of the tile's steps (steps [0, ceil(S / 2)) and the
+// rest), the first half's waves in the workgroup's first half. The workgroup
+// stages x once for twice the waves, so each thread encodes half the items of
+// the one-wave form before the first dot, and each wave walks half the steps.
+// A wave takes up to kK2MaxTiles tiles (striding like matvec_int); at the end
+// of each tile it writes its rows' group sums to LDS, and after the one
+// barrier each row is written as half 0 + half 1.
+constexpr int kK2MaxTiles = 8;
 template <int FMT, int R, bool XF32 = false>
 __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     constexpr int NB = 2;
     constexpr int XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
     __shared__ int wave_flags[16];
-    __shared__ float half_sum[8][8];  // [row wave][row of its tile]: the second half's sums
+    __shared__ float part[2][8][kK2MaxTiles][8];  // [half][row wave][tile of the wave][row of the tile]
     const int nch = p.P.nch;
     uint4* xd = smem;
     uint4* xb = smem + XP * nch;
@@ -308,6 +310,7 @@ __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     w[0].nch = nch;
     w[1] = w[0];
     w[1].next();
+    if (kh) w[1].s = w[1].s == 0 ? s_mid : w[1].s;  // (a new tile starts the second half at its midpoint)
     ChunkData<FMT> buf[NB][R];
     StageItem<XF32> it[kStageNJ];
     stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, 1, p.block, it);
@@ -322,28 +325,36 @@ __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     float acc[R][1];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r][0] = 0.f;
+    int j = 0;  // the wave's finished tiles
     for (;;) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             if (!w[i].valid()) goto done;
             step_int<FMT, 1, R, false, false>(p, w[i], sub, g, buf[i], acc, xd, xb, outliers);
+            if (w[i].s == w[i].steps - 1) {  // the tile's last step of this half
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float t = group_sum(acc[r][0], p.G);
+                    if (g == p.G - 1) part[kh][rw][j][sub * R + r] = t;
+                    acc[r][0] = 0.f;
+                }
+                ++j;
+            }
             w[i] = w[(i + NB - 1) % NB];
             w[i].next();
+            if (kh && w[i].s == 0) w[i].s = s_mid;
             load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
         }
     }
 done:
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r][0] = group_sum(acc[r][0], p.G);
-    if (kh == 1 && g == p.G - 1)
-#pragma unroll
-        for (int r = 0; r < R; ++r) half_sum[rw][sub * R + r] = acc[r][0];
     __syncthreads();
-    const int row0 = ((int)blockIdx.x * half + rw) * p.rows_per_wave + sub * R;
-    if (kh == 0 && g == p.G - 1)
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (row0 + r < (int)p.rows) p.y[row0 + r] = acc[r][0] + half_sum[rw][sub * R + r];
+    const int rpw = p.rows_per_wave, per_wg = half * kK2MaxTiles * rpw;
+    for (int e = threadIdx.x; e < per_wg; e += p.block) {
+        const int k = e % rpw, jj = (e / rpw) % kK2MaxTiles, r_w = e / (rpw * kK2MaxTiles);
+        const int tile = (int)blockIdx.x * half + r_w + jj * (int)gridDim.x * half;
+        const int row = tile * rpw + k;
+        if (tile < p.tiles && row < (int)p.rows) p.y[row] = part[0][r_w][jj][k] + part[1][r_w][jj][k];
+    }
 }
 
 // Burst form of matvec_int for long rows at one or two activation rows: every
@@ -513,32 +524,50 @@ static int env_int(const char* name, int fallback) {
     return v && *v ? atoi(v) : fallback;
 }
 
-// The long-row form (matvec_int_k2): Q4_K and Q4_0 rows of more than 128
-// chunks at one activation row, 32 lanes and one row per lane group, every
-// row tile (two rows) taken by two waves of a 1,024-thread workgroup, one per
-// half of its steps, when one launch of at most one workgroup per CU gives
-// every tile its waves. Measured (kernel us, three alternating runs): with
-// fp16 x, Q4_K 14336->4096 10.37 (64 lanes, two rows per group) -> 10.00 (32
-// lanes, one row) -> 9.07-9.38 (two waves per tile); Q4_0 9.78 -> 9.94 ->
-// 8.82, where two waves per tile at 64 lanes and two rows measured slower
-// (10.44). With fp32 x (the decode step's down product, through the fused
-// entry point) 32 lanes and one row alone were slower (568 -> 548 tok/s) and
-// two waves per tile faster (597.0 -> 614.1). RQMV_K2=0 turns it off.
-static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int cus, LaunchShape& s) {
-    if ((fmt != Q4_K && fmt != Q4_0) || M != 1 || nch <= 128 || !env_int("RQMV_K2", 1)) return false;
+// Two waves per row tile (matvec_int_k2), at one activation row, 32 lanes
+// and one row per lane group (two rows per tile), each wave taking half of a
+// tile's steps:
+// - long rows: Q4_K and Q4_0 rows of more than 128 chunks, up to 4,096 rows,
+//   one tile per wave on at most one 1,024-thread workgroup per CU. Measured
+//   (kernel us, three alternating runs): with fp16 x, Q4_K 14336->4096 10.37
+//   (64 lanes, two rows per group) -> 10.00 (32 lanes, one row) -> 9.07-9.38
+//   (two waves per tile); Q4_0 9.78 -> 9.94 -> 8.82, where two waves per tile
+//   at 64 lanes and two rows measured slower (10.44). With fp32 x (the decode
+//   step's down product, through the fused entry point) 32 lanes and one row
+//   alone were slower (568 -> 548 tok/s) and two waves per tile faster (597.0
+//   -> 614.1).
+// - rows of 64-128 chunks with fp16 x: Q4_K, Q4_0 and Q6_K on two 512-thread
+//   workgroups per CU, each wave taking up to kK2MaxTiles tiles. Q4_K
+//   4096->14336 9.33 -> 8.63 us, Q6_K 5120->25600 22.64 -> 20.69, Q4_0
+//   4096->14336 8.55 -> 8.47 (three alternating runs; 384, 448 and 640
+//   workgroups and one 1,024-thread workgroup per CU were slower).
+// RQMV_K2=0 turns both off, RQMV_K2_SHORT=0 the second.
+static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int cus, LaunchShape& s) {
+    if (M != 1 || !env_int("RQMV_K2", 1)) return false;
     const int64_t tiles = (rows + 1) / 2;
-    if (tiles > (int64_t)8 * cus) return false;
+    if ((fmt == Q4_K || fmt == Q4_0) && nch > 128) {
+        if (tiles > (int64_t)8 * cus) return false;
+        s.block = 1024;
+        s.grid = (int)((tiles + 7) / 8);
+    } else if ((fmt == Q4_K || fmt == Q4_0 || fmt == Q6_K) && nch >= 64 && nch <= 128 && xtype == X_F16 &&
+               env_int("RQMV_K2_SHORT", 1)) {
+        s.block = 512;
+        s.grid = 2 * cus;
+        const int64_t stride = (int64_t)s.grid * (s.block / 128);
+        if (tiles < stride || (tiles + stride - 1) / stride > kK2MaxTiles) return false;
+    } else {
+        return false;
+    }
     s.G = 32;
     s.R = 1;
-    s.block = 1024;
-    s.grid = (int)((tiles + 7) / 8);
+    s.k2 = true;
     return true;
 }
 
 static LaunchShape plan_matvec_impl(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus, bool k2) {
     LaunchShape s;
     const int64_t nch = chunks_per_row(fmt, cols);
-    if (k2 && k2_shape(fmt, rows, nch, M, cus, s)) return s;
+    if (k2 && k2_shape(fmt, rows, nch, M, xtype, cus, s)) return s;
     int G = 64;
     while (G > 8 && G > nch) G >>= 1;
     // Q6_K rows of 65-95 chunks (5120 columns: 80) leave a 64-lane group's
@@ -626,7 +655,7 @@ static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s,
         if (xtype == X_F16) return launch_kernel(matvec_f16w<M, R, false>, p, s, lds, stream, ev0, ev1);
         return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
-        if (s.block == 1024) {  // the long-row form (k2_shape)
+        if (s.k2) {  // two waves per row tile (k2_shape)
             if constexpr (M == 1 && R == 1) {
                 if (xtype == X_F16) return launch_kernel(matvec_int_k2<FMT, 1, false>, p, s, lds, stream, ev0, ev1);
                 return launch_kernel(matvec_int_k2<FMT, 1, true>, p, s, lds, stream, ev0, ev1);
@@ -738,7 +767,7 @@ LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu, b
     LaunchShape s;
     // plain products (no prologue, no epilogue) take the plain entry point's
     // long-row form where it applies, with the same shape
-    if (!glu && !norm && k2_shape(fmt, rows, chunks_per_row(fmt, cols), 1, cus, s)) return s;
+    if (!glu && !norm && k2_shape(fmt, rows, chunks_per_row(fmt, cols), 1, X_F32, cus, s)) return s;
     s = plan_matvec_impl(fmt, rows, cols, 1, X_F32, cus, false);
     // a lane group holds a (gate, up) row pair for kEpiGlu; otherwise Q8_0
     // takes one row, as in plan_matvec
@@ -779,7 +808,7 @@ static hipError_t launch_fused_fmt(const MvParams& p0, const LaunchShape& s, hip
 }
 
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream) {
-    if (s.block == 1024) {
+    if (s.k2) {
         // the long-row form (plain products only; plan_fused gives it the plain
         // entry point's shape, so the two stay bit-identical)
         if (p.norm_w || p.epi != kEpiPlain) return hipErrorInvalidValue;
