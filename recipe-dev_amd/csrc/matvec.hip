@@ -536,11 +536,15 @@ static int env_int(const char* name, int fallback) {
 //   step's down product, through the fused entry point) 32 lanes and one row
 //   alone were slower (568 -> 548 tok/s) and two waves per tile faster (597.0
 //   -> 614.1).
-// - rows of 64-128 chunks with fp16 x: Q4_K, Q4_0 and Q6_K on two 512-thread
-//   workgroups per CU, each wave taking up to kK2MaxTiles tiles. Q4_K
-//   4096->14336 9.33 -> 8.63 us, Q6_K 5120->25600 22.64 -> 20.69, Q4_0
-//   4096->14336 8.55 -> 8.47 (three alternating runs; 384, 448 and 640
-//   workgroups and one 1,024-thread workgroup per CU were slower).
+// - rows of 64-128 chunks (Q8_0: 64-192 chunks of 32 weights) on two
+//   512-thread workgroups per CU, each wave taking up to kK2MaxTiles tiles,
+//   when every wave has a tile. With fp16 x: Q4_K 4096->14336 9.33 -> 8.63
+//   us, Q6_K 5120->25600 22.64 -> 20.69, Q4_0 4096->14336 8.55 -> 8.47, Q8_0
+//   5120x5120 8.39 -> 7.41 (three alternating runs; 384, 448 and 640
+//   workgroups and one 1,024-thread workgroup per CU were slower); with fp32
+//   x, Q8_0 4096x4096 6.40 -> 6.20 (6.36 in the burst form) and the decode
+//   step's output product (through the fused entry point) 607.1 -> 614.1
+//   tok/s.
 // RQMV_K2=0 turns both off, RQMV_K2_SHORT=0 the second.
 static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int cus, LaunchShape& s) {
     if (M != 1 || !env_int("RQMV_K2", 1)) return false;
@@ -549,8 +553,7 @@ static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int c
         if (tiles > (int64_t)8 * cus) return false;
         s.block = 1024;
         s.grid = (int)((tiles + 7) / 8);
-    } else if ((fmt == Q4_K || fmt == Q4_0 || fmt == Q6_K) && nch >= 64 && nch <= 128 && xtype == X_F16 &&
-               env_int("RQMV_K2_SHORT", 1)) {
+    } else if (fmt != F16 && nch >= 64 && nch <= (fmt == Q8_0 ? 192 : 128) && env_int("RQMV_K2_SHORT", 1)) {
         s.block = 512;
         s.grid = 2 * cus;
         const int64_t stride = (int64_t)s.grid * (s.block / 128);
@@ -815,6 +818,8 @@ hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s,
         const size_t lds = matvec_lds_bytes(fmt, X_F32, 1, p.K);
         if (fmt == Q4_K) return launch_kernel(matvec_int_k2<Q4_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
         if (fmt == Q4_0) return launch_kernel(matvec_int_k2<Q4_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
+        if (fmt == Q6_K) return launch_kernel(matvec_int_k2<Q6_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
+        if (fmt == Q8_0) return launch_kernel(matvec_int_k2<Q8_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
         return hipErrorInvalidValue;
     }
     if (s.block > 512) return hipErrorInvalidValue;
