@@ -274,25 +274,26 @@ done:
     return;
 }
 
-// The long-row form (k2_shape): each row tile taken by two waves of one
-// workgroup, one per half of the tile's steps (steps [0, ceil(S / 2)) and the
-// rest), the first half's waves in the workgroup's first half. The workgroup
+// Two waves per row tile (k2_shape; M = 1 or 2 activation rows): each row
+// tile taken by two waves of one workgroup, one per half of the tile's steps
+// (steps [0, ceil(S / 2)) and the rest), the first half's waves in the
+// workgroup's first half. The workgroup
 // stages x once for twice the waves, so each thread encodes half the items of
 // the one-wave form before the first dot, and each wave walks half the steps.
 // A wave takes up to kK2MaxTiles tiles (striding like matvec_int); at the end
 // of each tile it writes its rows' group sums to LDS, and after the one
 // barrier each row is written as half 0 + half 1.
 constexpr int kK2MaxTiles = 8;
-template <int FMT, int R, bool XF32 = false>
+template <int FMT, int R, bool XF32 = false, int M = 1>
 __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     constexpr int NB = 2;
     constexpr int XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
     __shared__ int wave_flags[16];
-    __shared__ float part[2][8][kK2MaxTiles][8];  // [half][row wave][tile of the wave][row of the tile]
+    __shared__ float part[2][8][kK2MaxTiles][8 * M];  // [half][row wave][tile of the wave][row of the tile, x row]
     const int nch = p.P.nch;
     uint4* xd = smem;
-    uint4* xb = smem + XP * nch;
+    uint4* xb = smem + M * XP * nch;
     const int lane = threadIdx.x & 63, g = lane & (p.G - 1), sub = lane >> p.g_shift;
     const int wave = threadIdx.x >> 6, half = p.block >> 7;  // row waves per workgroup
     const int kh = wave >= half ? 1 : 0, rw = wave - kh * half;
@@ -313,31 +314,35 @@ __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     if (kh) w[1].s = w[1].s == 0 ? s_mid : w[1].s;  // (a new tile starts the second half at its midpoint)
     ChunkData<FMT> buf[NB][R];
     StageItem<XF32> it[kStageNJ];
-    stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, 1, p.block, it);
+    stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, M, p.block, it);
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
-    publish_outliers(stage_multi_finish<FMT, XF32>(nch, p.K, 1, p.block, it, xd, reinterpret_cast<float*>(xb)),
+    publish_outliers(stage_multi_finish<FMT, XF32>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb)),
                      wave_flags);
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, p.block);
-    float acc[R][1];
+    float acc[R][M];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r][0] = 0.f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) acc[r][mm] = 0.f;
     int j = 0;  // the wave's finished tiles
     for (;;) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             if (!w[i].valid()) goto done;
-            step_int<FMT, 1, R, false, false>(p, w[i], sub, g, buf[i], acc, xd, xb, outliers);
+            step_int<FMT, M, R, false, false>(p, w[i], sub, g, buf[i], acc, xd, xb, outliers);
             if (w[i].s == w[i].steps - 1) {  // the tile's last step of this half
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float t = group_sum(acc[r][0], p.G);
-                    if (g == p.G - 1) part[kh][rw][j][sub * R + r] = t;
-                    acc[r][0] = 0.f;
-                }
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int mm = 0; mm < M; ++mm) {
+                        const float t = group_sum(acc[r][mm], p.G);
+                        if (g == p.G - 1) part[kh][rw][j][(sub * R + r) * M + mm] = t;
+                        acc[r][mm] = 0.f;
+                    }
                 ++j;
             }
             w[i] = w[(i + NB - 1) % NB];
@@ -353,7 +358,10 @@ done:
         const int k = e % rpw, jj = (e / rpw) % kK2MaxTiles, r_w = e / (rpw * kK2MaxTiles);
         const int tile = (int)blockIdx.x * half + r_w + jj * (int)gridDim.x * half;
         const int row = tile * rpw + k;
-        if (tile < p.tiles && row < (int)p.rows) p.y[row] = part[0][r_w][jj][k] + part[1][r_w][jj][k];
+        if (tile < p.tiles && row < (int)p.rows)
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm)
+                p.y[(int64_t)mm * p.ldy + row] = part[0][r_w][jj][k * M + mm] + part[1][r_w][jj][k * M + mm];
     }
 }
 
@@ -524,7 +532,7 @@ static int env_int(const char* name, int fallback) {
     return v && *v ? atoi(v) : fallback;
 }
 
-// Two waves per row tile (matvec_int_k2), at one activation row, 32 lanes
+// Two waves per row tile (matvec_int_k2), at one or two activation rows, 32 lanes
 // and one row per lane group (two rows per tile), each wave taking half of a
 // tile's steps:
 // - long rows: Q4_K and Q4_0 rows of more than 128 chunks, up to 4,096 rows,
@@ -545,9 +553,11 @@ static int env_int(const char* name, int fallback) {
 //   x, Q8_0 4096x4096 6.40 -> 6.20 (6.36 in the burst form) and the decode
 //   step's output product (through the fused entry point) 607.1 -> 614.1
 //   tok/s.
+// Both at one or two activation rows: at two, Q6_K 5120->25600 35.64 -> 32.36
+// us, Q8_0 5120x5120 10.58 -> 9.51.
 // RQMV_K2=0 turns both off, RQMV_K2_SHORT=0 the second.
 static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int cus, LaunchShape& s) {
-    if (M != 1 || !env_int("RQMV_K2", 1)) return false;
+    if (M > 2 || !env_int("RQMV_K2", 1)) return false;
     const int64_t tiles = (rows + 1) / 2;
     if ((fmt == Q4_K || fmt == Q4_0) && nch > 128) {
         if (tiles > (int64_t)8 * cus) return false;
@@ -561,6 +571,8 @@ static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int c
     } else {
         return false;
     }
+    // (the kernel stages x in one pass of at most kStageNJ items per thread)
+    if ((int64_t)stage_items_host(fmt, nch, M) > (int64_t)kStageNJ * s.block) return false;
     s.G = 32;
     s.R = 1;
     s.k2 = true;
@@ -659,9 +671,9 @@ static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s,
         return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
         if (s.k2) {  // two waves per row tile (k2_shape)
-            if constexpr (M == 1 && R == 1) {
-                if (xtype == X_F16) return launch_kernel(matvec_int_k2<FMT, 1, false>, p, s, lds, stream, ev0, ev1);
-                return launch_kernel(matvec_int_k2<FMT, 1, true>, p, s, lds, stream, ev0, ev1);
+            if constexpr (M <= 2 && R == 1) {
+                if (xtype == X_F16) return launch_kernel(matvec_int_k2<FMT, 1, false, M>, p, s, lds, stream, ev0, ev1);
+                return launch_kernel(matvec_int_k2<FMT, 1, true, M>, p, s, lds, stream, ev0, ev1);
             }
             return hipErrorInvalidValue;
         }

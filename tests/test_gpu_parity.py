@@ -539,13 +539,16 @@ def test_matvec_ldx_ldy_strides(gpu):
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q4_0"])
 @pytest.mark.parametrize("xdt", ["f16", "f32"])
-@pytest.mark.parametrize("rows,cols", [(1, 14336), (37, 8448), (1001, 14336), (4096, 14336), (4097, 8448)])
+@pytest.mark.parametrize("rows,cols", [(1, 14336), (37, 8448), (1001, 14336), (4096, 14336), (4097, 8448),
+                                       (64, 40960)])
 def test_long_row_form(gpu, fmt, xdt, rows, cols):
     """Rows of more than 128 chunks at one activation row: each two-row tile
     taken by two waves, one per half of its steps (up to 4,096 rows), or the
     one-wave form beyond. Parity with recipe's fp32 order, including a tile
     count that leaves some of the last workgroup's waves without a tile, an
-    odd step count (8,448 columns: five steps of 32 chunks) and a single row."""
+    odd step count (8,448 columns: five steps of 32 chunks), a single row, and
+    rows too long for the form's one staging pass (40,960 columns: 5,120 items
+    for 1,024 threads)."""
     w = synth.weights(fmt, rows, cols, seed=rows + cols)
     W = gpu.Weight(fmt, rows, cols, w)
     xh, dt, x32 = _x(1, cols, xdt, seed=cols)
