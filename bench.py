@@ -575,10 +575,11 @@ def grid_table(args):
     reads of 33 MB (a rotating window of a buffer >= 2x the Infinity Cache,
     256 threads per workgroup, --inflight loads in flight per thread;
     libmeasure.so) and `args.steps` Q4_K 4096->14336 products at one fp16
-    activation row with RQMV_GRID = G (rotating weight copies), each
-    dispatch timed by events it records itself. Prints one JSON line with a
-    row per (kernel, grid); profile the same command with rocprofv3 to read
-    counters per dispatch."""
+    activation row in the one-wave-per-tile form (RQMV_K2=0) with RQMV_GRID =
+    G (rotating weight copies); then the product as planned (two waves per
+    tile). Each dispatch is timed by events it records itself. Prints one
+    JSON line with a row per (kernel, grid); profile the same command with
+    rocprofv3 to read counters per dispatch."""
     import ctypes
 
     import rqmv
@@ -618,6 +619,12 @@ def grid_table(args):
         return {"mean_us": round(float(d.mean()), 3), "median_us": round(float(np.median(d)), 3),
                 "p10_us": round(float(np.percentile(d, 10)), 3), "p90_us": round(float(np.percentile(d, 90)), 3)}
 
+    def mv(i, e0, e1):
+        if e0 is None:
+            Ws[i % copies].matvec(xb, rqmv.DTYPE_F16, 1, cols, yb, rows, stream)
+        else:
+            _check_mv(rqmv, Ws[i % copies], xb, yb, rows, cols, stream, e0, e1)
+
     table = []
     for g in grids:
         def read(i, e0, e1, g=g):
@@ -632,19 +639,19 @@ def grid_table(args):
         log(f"bench: plain read grid {g}: {r}")
         table.append(r)
         os.environ["RQMV_GRID"] = str(g)
-
-        def mv(i, e0, e1):
-            if e0 is None:
-                Ws[i % copies].matvec(xb, rqmv.DTYPE_F16, 1, cols, yb, rows, stream)
-            else:
-                _check_mv(rqmv, Ws[i % copies], xb, yb, rows, cols, stream, e0, e1)
-
+        os.environ["RQMV_K2"] = "0"
         r = timed(mv)
-        r.update({"kernel": "matvec_int Q4_K 4096->14336 M=1", "grid": g, "bytes": alg,
+        r.update({"kernel": "matvec_int Q4_K 4096->14336 M=1 (one wave per tile)", "grid": g, "bytes": alg,
                   "gbs": round(alg / (r["mean_us"] * 1e-6) / 1e9, 1)})
         log(f"bench: matvec grid {g}: {r}")
         table.append(r)
         del os.environ["RQMV_GRID"]
+        del os.environ["RQMV_K2"]
+    r = timed(mv)
+    r.update({"kernel": "matvec_int_k2 Q4_K 4096->14336 M=1 (as planned: two waves per tile)", "grid": 512,
+              "threads": 512, "bytes": alg, "gbs": round(alg / (r["mean_us"] * 1e-6) / 1e9, 1)})
+    log(f"bench: matvec as planned: {r}")
+    table.append(r)
     print(json.dumps({"grid_table": table, "inflight": args.inflight, "copies": copies, "steps": args.steps}),
           flush=True)
 
