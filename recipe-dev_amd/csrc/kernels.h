@@ -64,6 +64,8 @@ struct LaunchShape {
 // Chooses G, R, block and grid for a product; honours RQMV_G / RQMV_R /
 // RQMV_BLOCK / RQMV_GRID overrides for tuning sweeps.
 LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus);
+// Whether a product of M activation rows takes two waves per row tile (matvec_int_k2).
+bool k2_takes(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus);
 
 // ev0 / ev1 (may be null): events the dispatch records at its start and end.
 hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const LaunchShape& s, hipStream_t stream,

@@ -557,15 +557,18 @@ static int env_int(const char* name, int fallback) {
 // us, Q8_0 5120x5120 10.58 -> 9.51.
 // RQMV_K2=0 turns both off, RQMV_K2_SHORT=0 the second.
 static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int cus, LaunchShape& s) {
-    if (M > 2 || !env_int("RQMV_K2", 1)) return false;
+    // (three and four activation rows: Q8_0 only, whose matrix-core form it beats)
+    if (M > (fmt == Q8_0 ? 4 : 2) || !env_int("RQMV_K2", 1)) return false;
     const int64_t tiles = (rows + 1) / 2;
     if ((fmt == Q4_K || fmt == Q4_0) && nch > 128) {
         if (tiles > (int64_t)8 * cus) return false;
         s.block = 1024;
         s.grid = (int)((tiles + 7) / 8);
     } else if (fmt != F16 && nch >= 64 && nch <= (fmt == Q8_0 ? 192 : 128) && env_int("RQMV_K2_SHORT", 1)) {
-        s.block = 512;
-        s.grid = 2 * cus;
+        // two 512-thread workgroups per CU, or one of 1,024 threads where x
+        // needs more than four items per thread of 512
+        s.block = (int64_t)stage_items_host(fmt, nch, M) > (int64_t)kStageNJ * 512 ? 1024 : 512;
+        s.grid = s.block == 1024 ? cus : 2 * cus;
         const int64_t stride = (int64_t)s.grid * (s.block / 128);
         if (tiles < stride || (tiles + stride - 1) / stride > kK2MaxTiles) return false;
     } else {
@@ -639,6 +642,11 @@ static LaunchShape plan_matvec_impl(int fmt, int64_t rows, int64_t cols, int M, 
     return s;
 }
 
+bool k2_takes(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus) {
+    LaunchShape s;
+    return k2_shape(fmt, rows, chunks_per_row(fmt, cols), M, xtype, cus, s);
+}
+
 LaunchShape plan_matvec(int fmt, int64_t rows, int64_t cols, int M, int xtype, int cus) {
     return plan_matvec_impl(fmt, rows, cols, M, xtype, cus, true);
 }
@@ -671,14 +679,18 @@ static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s,
         return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
         if (s.k2) {  // two waves per row tile (k2_shape)
-            if constexpr (M <= 2 && R == 1) {
+            if constexpr ((M <= 2 || ((M == 3 || M == 4) && FMT == Q8_0)) && R == 1) {
                 if (xtype == X_F16) return launch_kernel(matvec_int_k2<FMT, 1, false, M>, p, s, lds, stream, ev0, ev1);
                 return launch_kernel(matvec_int_k2<FMT, 1, true, M>, p, s, lds, stream, ev0, ev1);
             }
             return hipErrorInvalidValue;
         }
-        if (xtype == X_F16) return launch_kernel(matvec_int<FMT, M, R, false>, p, s, lds, stream, ev0, ev1);
-        return launch_kernel(matvec_int<FMT, M, R, true>, p, s, lds, stream, ev0, ev1);
+        if constexpr (M == 3) {
+            return hipErrorInvalidValue;  // (three rows run in the split form only)
+        } else {
+            if (xtype == X_F16) return launch_kernel(matvec_int<FMT, M, R, false>, p, s, lds, stream, ev0, ev1);
+            return launch_kernel(matvec_int<FMT, M, R, true>, p, s, lds, stream, ev0, ev1);
+        }
     }
 }
 
@@ -691,6 +703,9 @@ static hipError_t launch_fmt(int xtype, int M, const MvParams& p, const LaunchSh
         case 16 + 4: return launch_one<FMT, 1, 4>(xtype, p, s, stream, ev0, ev1);
         case 32 + 1: return launch_one<FMT, 2, 1>(xtype, p, s, stream, ev0, ev1);
         case 32 + 2: return launch_one<FMT, 2, 2>(xtype, p, s, stream, ev0, ev1);
+        case 48 + 1:  // three rows: Q8_0 in the split form only
+            if constexpr (FMT == Q8_0) return launch_one<FMT, 3, 1>(xtype, p, s, stream, ev0, ev1);
+            return hipErrorInvalidValue;
         case 64 + 1: return launch_one<FMT, 4, 1>(xtype, p, s, stream, ev0, ev1);
         case 128 + 1: return launch_one<FMT, 8, 1>(xtype, p, s, stream, ev0, ev1);
         case 256 + 1:  // sixteen activation rows: F16 weights only (a router over a batch)

@@ -173,9 +173,12 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     p.ldy = ldy;
     int done = 0;
     // Three or more activation rows of a quantized weight go to the matrix
-    // cores, up to 32 rows per launch (at two the vector kernels are as fast).
+    // cores, up to 32 rows per launch (at two the vector kernels are as fast),
+    // except three or four rows of Q8_0 in the two-waves-per-tile form, which
+    // measured faster (Q8_0 5120x5120 at four rows 16.2 -> 13.6 us).
     const int mfma_min = env_int("RQMV_MFMA_MIN", 3);
-    if (w->fmt != rq::F16 && m >= mfma_min) {
+    const bool k2_few = (m == 3 || m == 4) && w->fmt == rq::Q8_0 && rq::k2_takes(w->fmt, rows, w->cols, m, xtype, info.cus);
+    if (w->fmt != rq::F16 && m >= mfma_min && !k2_few) {
         while (done < m) {
             const int mb = m - done > 32 ? 32 : m - done;
             if (rq::mfma_lds_bytes(w->fmt, xtype, mb, rows, info.cus) > info.lds_limit)
@@ -193,6 +196,7 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     while (done < m) {
         int mb = w->fmt == rq::F16 ? 16 : 8;  // F16 (routers) takes sixteen rows per launch
         while (mb > m - done) mb >>= 1;
+        if (k2_few && done == 0) mb = m;  // (three or four rows in one launch)
         while (mb > 1 && rq::matvec_lds_bytes(w->fmt, xtype, mb, (int)w->cols) > info.lds_limit) mb >>= 1;
         if (rq::matvec_lds_bytes(w->fmt, xtype, mb, (int)w->cols) > info.lds_limit)
             return fail(RQMV_EINVAL, "cols too large for one LDS stage");

@@ -104,7 +104,7 @@ def _x(m, k, dtype, seed):
 
 @pytest.mark.parametrize("fmt", FMTS + ["f16"])
 @pytest.mark.parametrize("xdt", ["f16", "f32"])
-@pytest.mark.parametrize("m", [1, 2, 3, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
 def test_matvec_parity(gpu, fmt, xdt, m):
     shapes = _shapes(fmt) if fmt != "f16" else [(3, 64), (257, 2048)]
     for rows, cols in shapes:
