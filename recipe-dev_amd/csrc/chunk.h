@@ -10,8 +10,11 @@
 // block in fp32:
 //   Q4_0:  d * s_b * sum (q - 8) x
 //   Q4_K:  d*sc * s_b * (sum (q - 8) x) + (8 d*sc - dmin*m) * s_b * sum x
-//   Q6_K:  d*sc * s_b * (16 sum h x + sum (l - 8) x - 24 sum x),  q = l + 16 h
 //   Q8_0:  d * s_b * sum q x, with x split into two balanced bytes for v_dot4_i32_i8.
+//   Q6_K:  d*sc * s_b * (sum q x - 32 sum x), q = l + 16 h assembled into bytes
+//          (q6k_bytes), x as two balanced bytes, v_dot4_i32_i8: half the dot
+//          instructions of a nibble form (which takes two per weight, one for
+//          l and one for h, against four digits).
 // The activation quantization is the only rounding beyond fp32 accumulation
 // (relative 1/61166 of the block maximum per value).
 //
@@ -235,14 +238,53 @@ __device__ __forceinline__ uint32_t word_at(const uint4& v, int i) {
     return (uint32_t)(pair >> (32 * (i & 1)));
 }
 
+// The 6-bit codes q = l + 16 h of 16-weight scale group g of a Q6_K chunk as
+// four words of four bytes: the group's weights 0, 2, 4, 6 | 1, 3, 5, 7 |
+// 8, 10, 12, 14 | 9, 11, 13, 15 (the staged activations' byte order). The low
+// nibbles come un-XORed from the two code words of the group (weight 2j in the
+// low nibble of byte j); h of weight j sits at bits 4j and of weight 8 + j at
+// bits 4j + 2 of the group's high-field word, so shifts of it by 4, 0, 2 and
+// -2 bring the four words' fields to bits 4-5 of their bytes. Plain shifts,
+// ands and ors only (each half the issue cost of a bit-field extract or a
+// three-operand logic op).
+__device__ __forceinline__ void q6k_bytes(const ChunkData<Q6_K>& d, int g, uint32_t (&W)[4]) {
+    const uint32_t L0 = word(d.q[g >> 1], (g & 1) * 2) ^ 0x88888888u;
+    const uint32_t L1 = word(d.q[g >> 1], (g & 1) * 2 + 1) ^ 0x88888888u;
+    const uint32_t H = word(d.q[2], g);
+    W[0] = (L0 & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+    W[1] = ((L0 >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+    W[2] = (L1 & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+    W[3] = ((L1 >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+}
+
 // True in every active lane when the chunk of any active lane holds an outlier.
 __device__ __forceinline__ bool wave_has_outlier(const uint4& b0) {
     return __builtin_amdgcn_ballot_w64(((b0.x | b0.y) >> 31) != 0) != 0;
 }
 
+// Words of a chunk that every activation row's dot reads again: Q6_K's byte
+// words (q6k_bytes, formed once per chunk however many rows it meets); the
+// other formats dot their code words as loaded.
 template <int FMT>
-__device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const uint4 (&xd)[Traits<FMT>::XP],
-                                        const uint4 (&xb)[2], float& acc) {
+struct ChunkWords {
+    uint32_t w[FMT == Q6_K ? 16 : 1];
+};
+template <int FMT>
+__device__ __forceinline__ void chunk_words(const ChunkData<FMT>& d, ChunkWords<FMT>& cw) {
+    if constexpr (FMT == Q6_K) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint32_t W[4];
+            q6k_bytes(d, g, W);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cw.w[4 * g + i] = W[i];
+        }
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void dot_int_w(const ChunkData<FMT>& d, const ChunkWords<FMT>& cw, int c,
+                                          const uint4 (&xd)[Traits<FMT>::XP], const uint4 (&xb)[2], float& acc) {
     const float sb0 = fabsf(wordf(xb[0], 0)), sb1 = fabsf(wordf(xb[0], 1));
     if constexpr (FMT == Q4_K) {
         uint32_t sc0, m0, sc1, m1;
@@ -295,28 +337,35 @@ __device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const ui
         float y = acc;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const uint32_t L0 = word(d.q[g >> 1], (g & 1) * 2), L1 = word(d.q[g >> 1], (g & 1) * 2 + 1);
-            const uint32_t H = word(d.q[2], g);
-            const uint32_t He = H & 0x33333333u, Ho = (H >> 2) & 0x33333333u;
+            const uint32_t* W = cw.w + 4 * g;
             const float dsc = dd * (float)(int8_t)((d.meta.x >> (8 * g)) & 0xffu);
-            // the low fields' and the high fields' sums over the digits, each
-            // one chain from digit 3 down (as dot_nibbles4)
-            int l = 0, h = 0;
-#pragma unroll
-            for (int i = 3; i >= 0; --i) {
-                // words 2g, 2g+1 of digit i: part 2i + g/2, components (g&1)*2, (g&1)*2+1
-                const uint4 D = xd[2 * i + (g >> 1)];
-                const uint32_t D0 = word(D, (g & 1) * 2), D1 = word(D, (g & 1) * 2 + 1);
-                l = sdot8(L1, D1, sdot8(L0, D0, l * 16));
-                h = sdot8(Ho, D1, sdot8(He, D0, h * 16));
-            }
+            // the high bytes' sum times 256, then the low bytes' dots, in one
+            // chain (exact: |sum q x| <= 16 * 63 * 30583 < 2^31)
+            const uint4 Lo = xd[g], Hi = xd[4 + g];
+            int t = sdot4(W[0], Hi.x, 0);
+            t = sdot4(W[1], Hi.y, t);
+            t = sdot4(W[2], Hi.z, t);
+            t = sdot4(W[3], Hi.w, t);
+            t *= 256;
+            t = sdot4(W[0], Lo.x, t);
+            t = sdot4(W[1], Lo.y, t);
+            t = sdot4(W[2], Lo.z, t);
+            t = sdot4(W[3], Lo.w, t);
             const float s = g < 2 ? sb0 : sb1;
             const float sx = g < 2 ? wordf(xb[0], 2 + g) : wordf(xb[1], g - 2);
-            y = fmaf(dsc * s, (float)(h * 16 + l), y);
-            y = fmaf(-24.f * dsc, sx, y);
+            y = fmaf(dsc * s, (float)t, y);
+            y = fmaf(-32.f * dsc, sx, y);
         }
         acc = y;
     }
+}
+
+template <int FMT>
+__device__ __forceinline__ void dot_int(const ChunkData<FMT>& d, int c, const uint4 (&xd)[Traits<FMT>::XP],
+                                        const uint4 (&xb)[2], float& acc) {
+    ChunkWords<FMT> cw;
+    chunk_words<FMT>(d, cw);
+    dot_int_w<FMT>(d, cw, c, xd, xb, acc);
 }
 
 // The extracted activations' terms of one chunk. `xo` points at the chunk's

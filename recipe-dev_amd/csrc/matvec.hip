@@ -165,6 +165,9 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
     const int c = w.chunk();
     const int row0 = w.tile * w.rows_per_wave + sub * R, rows = (int)p.rows;
     if (c < nch) {
+        ChunkWords<FMT> cw[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) chunk_words<FMT>(d[r], cw[r]);
         // one activation row's digits live at a time; the weights stay in registers
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
@@ -176,7 +179,7 @@ __device__ __forceinline__ void step_int(const MvParams& p, const StepWalk& w, i
             bv[1] = xb[(mm * XR + 1) * nch + c];
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < rows) dot_int<FMT>(d[r], c, xv, bv, acc[r][mm]);
+                if (row0 + r < rows) dot_int_w<FMT>(d[r], cw[r], c, xv, bv, acc[r][mm]);
             if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0)) {
 #pragma unroll
                 for (int r = 0; r < R; ++r)
@@ -413,6 +416,8 @@ __global__ void __launch_bounds__(256) matvec_burst(MvParams p, int S) {
         const int r = u / S, st = u - r * S;
         const int row = wave + r * waves, c = lane + 64 * st;
         if (c < nch) {
+            ChunkWords<FMT> cw;
+            chunk_words<FMT>(d[u], cw);
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) {
                 uint4 xv[XP];
@@ -421,7 +426,7 @@ __global__ void __launch_bounds__(256) matvec_burst(MvParams p, int S) {
                 for (int j = 0; j < XP; ++j) xv[j] = xd[(mm * XP + j) * nch + c];
                 bv[0] = xb[(mm * XR + 0) * nch + c];
                 bv[1] = xb[(mm * XR + 1) * nch + c];
-                dot_int<FMT>(d[u], c, xv, bv, acc[mm]);
+                dot_int_w<FMT>(d[u], cw, c, xv, bv, acc[mm]);
                 if (__builtin_expect(outliers && wave_has_outlier(bv[0]), 0))
                     dot_outliers<FMT>(d[u], c, xb + mm * XR * nch + c, nch, acc[mm]);
             }

@@ -15,11 +15,13 @@
 // four balanced hex digits (x + 0x8888 has hex digits d_i + 8, so
 // (x + 0x8888) ^ 0x8888 holds every d_i as a signed nibble) and the digits are
 // transposed into words of eight values per digit, the weights' nibble order.
-// For Q8_0 x is split into two balanced bytes ((x + 0x8080) ^ 0x8080) and
-// transposed into words of four.
+// For Q8_0 and Q6_K x is split into two balanced bytes ((x + 0x8080) ^ 0x8080)
+// and transposed into words of four (Q6_K: the even and the odd values of
+// eight, the order of its byte words).
 //   LDS: xd [m][part][chunk] 16-byte digit words (Traits::XP parts per chunk:
-//        nibble formats: part 2i + b holds digit i of the chunk's block b;
-//        Q8_0: parts 0-1 low bytes, parts 2-3 high bytes),
+//        Q4_0 and Q4_K: part 2i + b holds digit i of the chunk's block b;
+//        Q8_0: parts 0-1 low bytes, parts 2-3 high bytes; Q6_K: part g the
+//        low bytes of 16-value group g, part 4 + g its high bytes),
 //        xb [m][XR][chunk] block data: row 0 (s_0, s_1, sx_0, sx_1), row 1
 //        (sx_2, sx_3, idx_0, idx_1), row 2 + b block b's four slot values
 //        (0 where unused); sx = s * sum x over the block (Q4_K) or the
@@ -159,7 +161,8 @@ __device__ __forceinline__ void digit_words(const uint32_t (&P)[4], uint32_t (&o
 // they are.
 template <int FMT>
 __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, uint32_t (&w4)[4], int& sum) {
-    constexpr float kOffset = FMT == Q8_0 ? 32896.f : 34952.f;  // 0x8080, 0x8888
+    constexpr bool kBytes = FMT == Q8_0 || FMT == Q6_K;
+    constexpr float kOffset = kBytes ? 32896.f : 34952.f;  // 0x8080, 0x8888
     constexpr float kMagic = 12582912.0f + kOffset;              // 1.5 * 2^23 + c
     constexpr uint32_t kMagicBits = 0x4B400000u + (uint32_t)kOffset;
     float s = amax * (1.0f / kXMax);
@@ -184,6 +187,17 @@ __device__ __forceinline__ float encode_item(const float (&v)[8], float amax, ui
         w4[1] = __builtin_amdgcn_perm(P[3], P[2], 0x06040200u) ^ 0x80808080u;
         w4[2] = __builtin_amdgcn_perm(P[1], P[0], 0x07050301u) ^ 0x80808080u;
         w4[3] = __builtin_amdgcn_perm(P[3], P[2], 0x07050301u) ^ 0x80808080u;
+    } else if constexpr (FMT == Q6_K) {
+        // low bytes of x_0, x_2, x_4, x_6 and of x_1, x_3, x_5, x_7, then their
+        // high bytes (the order of the weights' byte words, chunk.h)
+        const uint32_t e0 = __builtin_amdgcn_perm(xb[2], xb[0], 0x05010400u);  // lo 0, lo 2, hi 0, hi 2
+        const uint32_t e1 = __builtin_amdgcn_perm(xb[6], xb[4], 0x05010400u);
+        const uint32_t o0 = __builtin_amdgcn_perm(xb[3], xb[1], 0x05010400u);
+        const uint32_t o1 = __builtin_amdgcn_perm(xb[7], xb[5], 0x05010400u);
+        w4[0] = __builtin_amdgcn_perm(e1, e0, 0x05040100u) ^ 0x80808080u;
+        w4[1] = __builtin_amdgcn_perm(o1, o0, 0x05040100u) ^ 0x80808080u;
+        w4[2] = __builtin_amdgcn_perm(e1, e0, 0x07060302u) ^ 0x80808080u;
+        w4[3] = __builtin_amdgcn_perm(o1, o0, 0x07060302u) ^ 0x80808080u;
     } else {
         digit_words(P, w4);
     }
@@ -360,6 +374,16 @@ __device__ __forceinline__ bool stage_finish(int u, int nch, int M, int K, const
         const int part = q >> 1, comp = (q & 1) * 2;
         uint32_t* lo_at = xdw + ((m * XP + part) * nch + c) * 4 + comp;
         uint32_t* hi_at = xdw + ((m * XP + 2 + part) * nch + c) * 4 + comp;
+        lo_at[0] = w4[0];
+        lo_at[1] = w4[1];
+        hi_at[0] = w4[2];
+        hi_at[1] = w4[3];
+    } else if constexpr (FMT == Q6_K) {
+        // group g = 2b + q/2: low-byte words in part g, high-byte words in
+        // part 4 + g; values 0-7 of the group in components 0-1, 8-15 in 2-3
+        const int g = 2 * b + (q >> 1), comp = (q & 1) * 2;
+        uint32_t* lo_at = xdw + ((m * XP + g) * nch + c) * 4 + comp;
+        uint32_t* hi_at = xdw + ((m * XP + 4 + g) * nch + c) * 4 + comp;
         lo_at[0] = w4[0];
         lo_at[1] = w4[1];
         hi_at[0] = w4[2];
