@@ -562,8 +562,10 @@ static int env_int(const char* name, int fallback) {
 // us, Q8_0 5120x5120 10.58 -> 9.51.
 // RQMV_K2=0 turns both off, RQMV_K2_SHORT=0 the second.
 static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int cus, LaunchShape& s) {
-    // (three and four activation rows: Q8_0 only, whose matrix-core form it beats)
-    if (M > (fmt == Q8_0 ? 4 : 2) || !env_int("RQMV_K2", 1)) return false;
+    // (three and four activation rows of Q8_0 and three of Q6_K, where it beats
+    // the matrix-core forms: Q6_K 5120->25600 at three rows 38.8 -> 33.6 us, at
+    // four a tie, 39.6 against 38.9)
+    if (M > (fmt == Q8_0 ? 4 : fmt == Q6_K ? 3 : 2) || !env_int("RQMV_K2", 1)) return false;
     const int64_t tiles = (rows + 1) / 2;
     if ((fmt == Q4_K || fmt == Q4_0) && nch > 128) {
         if (tiles > (int64_t)8 * cus) return false;
@@ -684,7 +686,7 @@ static hipError_t launch_one(int xtype, const MvParams& p, const LaunchShape& s,
         return launch_kernel(matvec_f16w<M, R, true>, p, s, lds, stream, ev0, ev1);
     } else {
         if (s.k2) {  // two waves per row tile (k2_shape)
-            if constexpr ((M <= 2 || ((M == 3 || M == 4) && FMT == Q8_0)) && R == 1) {
+            if constexpr ((M <= 2 || ((M == 3 || M == 4) && FMT == Q8_0) || (M == 3 && FMT == Q6_K)) && R == 1) {
                 if (xtype == X_F16) return launch_kernel(matvec_int_k2<FMT, 1, false, M>, p, s, lds, stream, ev0, ev1);
                 return launch_kernel(matvec_int_k2<FMT, 1, true, M>, p, s, lds, stream, ev0, ev1);
             }
@@ -708,8 +710,8 @@ static hipError_t launch_fmt(int xtype, int M, const MvParams& p, const LaunchSh
         case 16 + 4: return launch_one<FMT, 1, 4>(xtype, p, s, stream, ev0, ev1);
         case 32 + 1: return launch_one<FMT, 2, 1>(xtype, p, s, stream, ev0, ev1);
         case 32 + 2: return launch_one<FMT, 2, 2>(xtype, p, s, stream, ev0, ev1);
-        case 48 + 1:  // three rows: Q8_0 in the split form only
-            if constexpr (FMT == Q8_0) return launch_one<FMT, 3, 1>(xtype, p, s, stream, ev0, ev1);
+        case 48 + 1:  // three rows: Q8_0 and Q6_K in the split form only
+            if constexpr (FMT == Q8_0 || FMT == Q6_K) return launch_one<FMT, 3, 1>(xtype, p, s, stream, ev0, ev1);
             return hipErrorInvalidValue;
         case 64 + 1: return launch_one<FMT, 4, 1>(xtype, p, s, stream, ev0, ev1);
         case 128 + 1: return launch_one<FMT, 8, 1>(xtype, p, s, stream, ev0, ev1);

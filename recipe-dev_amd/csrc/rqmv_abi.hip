@@ -174,10 +174,12 @@ int matvec_rows(const rqmv_weight* w, int64_t first_row, int64_t rows, const voi
     int done = 0;
     // Three or more activation rows of a quantized weight go to the matrix
     // cores, up to 32 rows per launch (at two the vector kernels are as fast),
-    // except three or four rows of Q8_0 in the two-waves-per-tile form, which
-    // measured faster (Q8_0 5120x5120 at four rows 16.2 -> 13.6 us).
+    // except three or four rows of Q8_0 and three of Q6_K in the
+    // two-waves-per-tile form, which measured faster (Q8_0 5120x5120 at four
+    // rows 16.2 -> 13.6 us, Q6_K 5120->25600 at three 38.8 -> 33.6).
     const int mfma_min = env_int("RQMV_MFMA_MIN", 3);
-    const bool k2_few = (m == 3 || m == 4) && w->fmt == rq::Q8_0 && rq::k2_takes(w->fmt, rows, w->cols, m, xtype, info.cus);
+    const bool k2_few = (m == 3 || m == 4) && (w->fmt == rq::Q8_0 || w->fmt == rq::Q6_K) && env_int("RQMV_K2_FEW", 1) &&
+                        rq::k2_takes(w->fmt, rows, w->cols, m, xtype, info.cus);
     if (w->fmt != rq::F16 && m >= mfma_min && !k2_few) {
         while (done < m) {
             const int mb = m - done > 32 ? 32 : m - done;

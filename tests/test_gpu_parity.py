@@ -568,8 +568,8 @@ CONFIGS = [
     ("q4_0 14336->4096", "q4_0", 4096, 14336, "f16", [1]),
     ("q4_k 4096->14336", "q4_k", 14336, 4096, "f16", [1]),
     ("q4_k 14336->4096", "q4_k", 4096, 14336, "f16", [1]),
-    ("q6_k 5120->25600", "q6_k", 25600, 5120, "f16", [1, 2, 4, 8, 16, 32]),
-    ("q8_0 5120->5120", "q8_0", 5120, 5120, "f16", [1, 2, 4, 8, 16, 32]),
+    ("q6_k 5120->25600", "q6_k", 25600, 5120, "f16", [1, 2, 3, 4, 8, 16, 32]),
+    ("q8_0 5120->5120", "q8_0", 5120, 5120, "f16", [1, 2, 3, 4, 8, 16, 32]),
 ]
 
 
