@@ -285,14 +285,18 @@ done:
 // the one-wave form before the first dot, and each wave walks half the steps.
 // A wave takes up to kK2MaxTiles tiles (striding like matvec_int); at the end
 // of each tile it writes its rows' group sums to LDS, and after the one
-// barrier each row is written as half 0 + half 1.
+// barrier each row is written as half 0 + half 1. NORM: the rmsnorm prologue
+// (M = 1, fp32 activations), its factor applied to each row's sum; with the
+// GLU epilogue (kEpiGlu, M = 1) a tile's two rows are a (gate, up) pair and
+// the pair writes silu(gate) * up.
 constexpr int kK2MaxTiles = 8;
-template <int FMT, int R, bool XF32 = false, int M = 1>
+template <int FMT, int R, bool XF32 = false, int M = 1, bool NORM = false>
 __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     constexpr int NB = 2;
     constexpr int XP = Traits<FMT>::XP;
     extern __shared__ uint4 smem[];
     __shared__ int wave_flags[16];
+    __shared__ float block_scalar[16];  // NORM: the waves' sums of squares
     __shared__ float part[2][8][kK2MaxTiles][8 * M];  // [half][row wave][tile of the wave][row of the tile, x row]
     const int nch = p.P.nch;
     uint4* xd = smem;
@@ -316,16 +320,31 @@ __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
     w[1].next();
     if (kh) w[1].s = w[1].s == 0 ? s_mid : w[1].s;  // (a new tile starts the second half at its midpoint)
     ChunkData<FMT> buf[NB][R];
-    StageItem<XF32> it[kStageNJ];
-    stage_multi_issue<FMT, XF32>(nch, p.K, p.x, p.ldx, M, p.block, it);
+    NormIn nin{};
+    float ssq = 0.f;  // NORM: this thread's share of sum (x + delta)^2
+    if constexpr (NORM) nin = NormIn{p.norm_w, p.delta, blockIdx.x == 0 ? p.x_out : nullptr};
+    constexpr int NJ = NORM ? kStageNJNorm : kStageNJ;
+    StageItem<XF32, NORM> it[NJ];
+    stage_multi_issue<FMT, XF32, NORM, NJ>(nch, p.K, p.x, p.ldx, M, p.block, it, nin);
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < NB; ++i) load_rows_rs<FMT, R>(p, rs, w[i], sub, buf[i]);
-    publish_outliers(stage_multi_finish<FMT, XF32>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb)),
+    publish_outliers(stage_multi_finish<FMT, XF32, NORM, NJ>(nch, p.K, M, p.block, it, xd, reinterpret_cast<float*>(xb),
+                                                             nin, &ssq),
                      wave_flags);
+    if constexpr (NORM) {
+        ssq = group_sum(ssq, 64);
+        if (lane == 63) block_scalar[wave] = ssq;
+    }
     __syncthreads();
     const bool outliers = read_outliers(wave_flags, p.block);
+    float norm_scale = 1.f;
+    if constexpr (NORM) {  // the waves' sums in order: every workgroup forms the same factor
+        float t = 0.f;
+        for (int i = 0; i < (p.block >> 6); ++i) t += block_scalar[i];
+        norm_scale = 1.0f / sqrtf(t / (float)p.K + p.eps);
+    }
     float acc[R][M];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -357,14 +376,30 @@ __global__ void __launch_bounds__(1024) matvec_int_k2(MvParams p) {
 done:
     __syncthreads();
     const int rpw = p.rows_per_wave, per_wg = half * kK2MaxTiles * rpw;
+    const bool glu = p.epi == kEpiGlu;
     for (int e = threadIdx.x; e < per_wg; e += p.block) {
         const int k = e % rpw, jj = (e / rpw) % kK2MaxTiles, r_w = e / (rpw * kK2MaxTiles);
         const int tile = (int)blockIdx.x * half + r_w + jj * (int)gridDim.x * half;
         const int row = tile * rpw + k;
-        if (tile < p.tiles && row < (int)p.rows)
+        if (tile >= p.tiles || row >= (int)p.rows) continue;
+        if (glu) {  // (M = 1) the pair's even row writes silu(gate) * up (recipe.rs:22662-22668, as finish_tile)
+            if ((k & 1) == 0 && row + 1 < (int)p.rows) {
+                float gt = part[0][r_w][jj][k] + part[1][r_w][jj][k];
+                float up = part[0][r_w][jj][k + 1] + part[1][r_w][jj][k + 1];
+                if constexpr (NORM) {
+                    gt *= norm_scale;
+                    up *= norm_scale;
+                }
+                p.y[row / 2] = gt * (0.5f * (tanhf(0.5f * gt) + 1.0f)) * up;
+            }
+            continue;
+        }
 #pragma unroll
-            for (int mm = 0; mm < M; ++mm)
-                p.y[(int64_t)mm * p.ldy + row] = part[0][r_w][jj][k * M + mm] + part[1][r_w][jj][k * M + mm];
+        for (int mm = 0; mm < M; ++mm) {
+            float v = part[0][r_w][jj][k * M + mm] + part[1][r_w][jj][k * M + mm];
+            if constexpr (NORM) v *= norm_scale;
+            p.y[(int64_t)mm * p.ldy + row] = v;
+        }
     }
 }
 
@@ -803,8 +838,14 @@ hipError_t launch_matvec(int fmt, int xtype, int M, const MvParams& p, const Lau
 LaunchShape plan_fused(int fmt, int64_t rows, int64_t cols, int cus, bool glu, bool norm) {
     LaunchShape s;
     // plain products (no prologue, no epilogue) take the plain entry point's
-    // long-row form where it applies, with the same shape
-    if (!glu && !norm && k2_shape(fmt, rows, chunks_per_row(fmt, cols), 1, X_F32, cus, s)) return s;
+    // two-waves-per-tile form where it applies, with the same shape (so the
+    // two entry points stay bit-identical); with the norm prologue or the GLU
+    // epilogue too (RQMV_K2_FUSED=0 keeps those in the one-wave form)
+    // (the norm prologue's staging takes at most kStageNJNorm items a thread there)
+    if ((!glu && !norm) || env_int("RQMV_K2_FUSED", 1))
+        if (k2_shape(fmt, rows, chunks_per_row(fmt, cols), 1, X_F32, cus, s) &&
+            (!norm || stage_items_host(fmt, chunks_per_row(fmt, cols), 1) <= (int64_t)kStageNJNorm * s.block))
+            return s;
     s = plan_matvec_impl(fmt, rows, cols, 1, X_F32, cus, false);
     // a lane group holds a (gate, up) row pair for kEpiGlu; otherwise Q8_0
     // takes one row, as in plan_matvec
@@ -845,16 +886,16 @@ static hipError_t launch_fused_fmt(const MvParams& p0, const LaunchShape& s, hip
 }
 
 hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s, hipStream_t stream) {
-    if (s.k2) {
-        // the long-row form (plain products only; plan_fused gives it the plain
-        // entry point's shape, so the two stay bit-identical)
-        if (p.norm_w || p.epi != kEpiPlain) return hipErrorInvalidValue;
+    if (s.k2) {  // the two-waves-per-tile form (plan_fused)
         const size_t lds = matvec_lds_bytes(fmt, X_F32, 1, p.K);
-        if (fmt == Q4_K) return launch_kernel(matvec_int_k2<Q4_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
-        if (fmt == Q4_0) return launch_kernel(matvec_int_k2<Q4_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
-        if (fmt == Q6_K) return launch_kernel(matvec_int_k2<Q6_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
-        if (fmt == Q8_0) return launch_kernel(matvec_int_k2<Q8_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
-        return hipErrorInvalidValue;
+        const bool nm = p.norm_w != nullptr;
+        switch (fmt) {
+            case Q4_K: return launch_kernel(nm ? matvec_int_k2<Q4_K, 1, true, 1, true> : matvec_int_k2<Q4_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
+            case Q4_0: return launch_kernel(nm ? matvec_int_k2<Q4_0, 1, true, 1, true> : matvec_int_k2<Q4_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
+            case Q6_K: return launch_kernel(nm ? matvec_int_k2<Q6_K, 1, true, 1, true> : matvec_int_k2<Q6_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
+            case Q8_0: return launch_kernel(nm ? matvec_int_k2<Q8_0, 1, true, 1, true> : matvec_int_k2<Q8_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
+            default: return hipErrorInvalidValue;
+        }
     }
     if (s.block > 512) return hipErrorInvalidValue;
     if (s.R == 1 && fmt == Q8_0 && p.epi != kEpiGlu) return launch_fused_fmt<Q8_0, 1>(p, s, stream);

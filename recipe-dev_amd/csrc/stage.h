@@ -435,19 +435,22 @@ __device__ __forceinline__ bool read_outliers(const int* wave_flags, int nthread
 
 // Staging with up to NJ items per thread: all activation loads are issued
 // before the caller's weight loads (stage_multi_issue), encoded afterwards
-// (stage_multi_finish).
+// (stage_multi_finish). kStageNJ by default; the norm prologue's items carry
+// three times the registers, and the two-waves-per-tile kernel (at most 128
+// registers a lane) takes kStageNJNorm of them.
 constexpr int kStageNJ = 4;
+constexpr int kStageNJNorm = 2;
 
 // `nthreads` is the workgroup's size, passed in rather than read from the
 // dispatch packet (blockDim), whose read is a memory round trip at the start
 // of every workgroup.
-template <int FMT, bool XF32, bool NORM = false>
+template <int FMT, bool XF32, bool NORM = false, int NJ = kStageNJ>
 __device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x, int64_t ldx, int M, int nthreads,
-                                                  StageItem<XF32, NORM> (&it)[kStageNJ],
+                                                  StageItem<XF32, NORM> (&it)[NJ],
                                                   const NormIn& nin = NormIn{}) {
     const int total = stage_items<FMT>(nch, M);
 #pragma unroll
-    for (int j = 0; j < kStageNJ; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         // (rounds past the last item are skipped by the whole workgroup; a
         // thread past it in the last round loads an item of its own quad)
         if (j * nthreads >= total) break;
@@ -456,14 +459,14 @@ __device__ __forceinline__ void stage_multi_issue(int nch, int K, const void* x,
     }
 }
 
-template <int FMT, bool XF32, bool NORM = false>
+template <int FMT, bool XF32, bool NORM = false, int NJ = kStageNJ>
 __device__ __forceinline__ bool stage_multi_finish(int nch, int K, int M, int nthreads,
-                                                   const StageItem<XF32, NORM> (&it)[kStageNJ], uint4* xd, float* xbf,
+                                                   const StageItem<XF32, NORM> (&it)[NJ], uint4* xd, float* xbf,
                                                    const NormIn& nin = NormIn{}, float* ss = nullptr) {
     const int total = stage_items<FMT>(nch, M);
     bool out = false;
 #pragma unroll
-    for (int j = 0; j < kStageNJ; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         if (j * nthreads >= total) break;
         const int u = (int)threadIdx.x + j * nthreads;
         if (u < total) out |= stage_finish<FMT, XF32, NORM>(u, nch, M, K, it[j], xd, xbf, nin, ss);

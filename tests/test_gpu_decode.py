@@ -270,7 +270,7 @@ def _mv_ref(fmt, w, rows, cols, x):
 @pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 6144, 4096), ("q8_0", 4096, 4096), ("q6_k", 512, 1024),
                                            ("q4_0", 300, 4096), ("q4_k", 256, 14336), ("q8_0", 1001, 544),
                                            ("q8_0", 3, 32), ("q4_k", 6143, 4096), ("q6_k", 6145, 1024),
-                                           ("q4_0", 6142, 512)])
+                                           ("q4_0", 6142, 512), ("q6_k", 4096, 5120), ("q4_0", 4100, 4096)])
 @pytest.mark.parametrize("with_delta", [False, True])
 def test_fused_norm_prologue(gpu, fmt, rows, cols, with_delta):
     w = synth.weights(fmt, rows, cols, seed=rows + cols)
@@ -294,7 +294,8 @@ def test_fused_norm_prologue(gpu, fmt, rows, cols, with_delta):
     assert np.array_equal(X.download(np.float32), x)  # x itself is not modified
 
 
-@pytest.mark.parametrize("fmt,n,cols", [("q4_k", 14336, 4096), ("q4_k", 512, 256), ("q8_0", 1000, 512)])
+@pytest.mark.parametrize("fmt,n,cols", [("q4_k", 14336, 4096), ("q4_k", 512, 256), ("q8_0", 1000, 512),
+                                        ("q6_k", 2048, 5120), ("q8_0", 2048, 4096), ("q4_0", 2050, 4096)])
 def test_fused_glu_epilogue(gpu, fmt, n, cols):
     g = synth.weights(fmt, n, cols, seed=3)
     u = synth.weights(fmt, n, cols, seed=4)
@@ -312,6 +313,28 @@ def test_fused_glu_epilogue(gpu, fmt, n, cols):
     z = Z.download(np.float32)
     assert rel_err(z[0::2], _mv_ref(fmt, g, n, cols, x)) < 1e-3
     assert rel_err(z[1::2], _mv_ref(fmt, u, n, cols, x)) < 1e-3
+
+
+@pytest.mark.parametrize("fmt,n,cols", [("q4_k", 14336, 4096), ("q6_k", 2048, 5120), ("q4_k", 300, 4096)])
+def test_fused_norm_and_glu(gpu, fmt, n, cols):
+    """The decode step's gate/up form: the norm prologue (with a delta and
+    x_out) and the GLU epilogue in one launch, at sizes that take the
+    two-waves-per-tile form (the pairs 2i, 2i + 1 of a tile) and one that
+    does not."""
+    g = synth.weights(fmt, n, cols, seed=5)
+    u = synth.weights(fmt, n, cols, seed=6)
+    W = gpu.glu_weight(fmt, n, cols, g, u)
+    x = (RNG.standard_normal(cols) * 30).astype(np.float32)
+    d = (RNG.standard_normal(cols) * 5).astype(np.float32)
+    nw = (1 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
+    X, D, NW, Y = (gpu.DeviceBuffer.from_array(a) for a in (x, d, nw, np.zeros(n, np.float32)))
+    XO = gpu.DeviceBuffer(4 * cols)
+    gpu.matvec_fused(W, X, Y, gpu.EPI_GLU, NW, 1e-5, D, XO)
+    gpu.synchronize()
+    un = ref.rmsnorm(x + d, nw, 1e-5)
+    want = ref.silu_mul(_mv_ref(fmt, g, n, cols, un), _mv_ref(fmt, u, n, cols, un))
+    assert rel_err(Y.download(np.float32), want) < 1e-3
+    assert np.array_equal(XO.download(np.float32), x + d)
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q8_0", 1001, 544), ("q8_0", 4096, 4096), ("q4_0", 77, 128),
