@@ -656,6 +656,52 @@ def grid_table(args):
           flush=True)
 
 
+def issue_rates(args):
+    """Issue cost of single VALU opcodes on this GPU (libmeasure.so's probe):
+    per opcode, `args.steps` launches of 2,048 workgroups x 256 threads, each
+    lane running eight independent chains of 4,096 instructions, timed by
+    events the dispatches record. Reports ns per wave-instruction per SIMD
+    (the launch time over the wave-instructions each SIMD issues) and that in
+    cycles at the clock the probe's plain 32-bit adds run at, taken as two
+    cycles per wave64 instruction. Prints one JSON line."""
+    import ctypes
+
+    import rqmv
+
+    rqmv.init(0)
+    blocks, iters = 2048, 4096
+    cus = 256  # MI355X (gfx950): 256 CUs of four SIMDs
+    out = rqmv.DeviceBuffer(4 * 256 * blocks)
+    stream = rqmv.Stream()
+    meas = ctypes.CDLL(os.path.join(ROOT, "recipe-dev_amd", "libmeasure.so"))
+    meas.measure_issue_name.restype = ctypes.c_char_p
+    meas.measure_issue_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p]
+    wave_ops_per_simd = blocks * 4 * iters * 8 / (cus * 4)
+    rows = []
+    for op in range(meas.measure_issue_ops()):
+        name = meas.measure_issue_name(op).decode()
+        meas.measure_issue_rate(op, blocks, iters, out.ptr, stream.handle, None, None)
+        ev = [(rqmv.Event(), rqmv.Event()) for _ in range(args.steps)]
+        for a, b in ev:
+            rc = meas.measure_issue_rate(op, blocks, iters, out.ptr, stream.handle, a.handle, b.handle)
+            if rc:
+                raise RuntimeError(f"measure_issue_rate: HIP error {rc}")
+        stream.synchronize()
+        us = float(np.median([a.elapsed_ms(b) for a, b in ev])) * 1e3
+        for a, b in ev:
+            a.close()
+            b.close()
+        rows.append({"opcode": name, "launch_us": round(us, 1),
+                     "ns_per_wave_op": round(us * 1e3 / wave_ops_per_simd, 3)})
+        log(f"bench: {rows[-1]}")
+    base = next(r["ns_per_wave_op"] for r in rows if r["opcode"] == "v_add_u32")
+    for r in rows:
+        r["cycles_if_add_is_2"] = round(2.0 * r["ns_per_wave_op"] / base, 2)
+    print(json.dumps({"issue_rates": rows, "blocks": blocks, "threads": 256, "chains": 8, "iters": iters,
+                      "cus": cus, "launches": args.steps}), flush=True)
+
+
 def _check_mv(rqmv, W, xb, yb, rows, cols, stream, e0, e1):
     rc = rqmv.lib().lib.rqmv_matvec_timed(W.handle, xb.ptr, rqmv.DTYPE_F16, 1, cols, yb.ptr, rows, stream.handle,
                                           e0, e1)
@@ -669,7 +715,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="q4_k_up",
-                    choices=sorted(WORKLOADS) + ["moe_c4", "decode_c5", "grid_table"])
+                    choices=sorted(WORKLOADS) + ["moe_c4", "decode_c5", "grid_table", "issue_rates"])
     ap.add_argument("--grids", default="512,1024,2048", help="grid_table: workgroup counts")
     ap.add_argument("--inflight", type=int, default=4, choices=[1, 2, 4, 8], help="grid_table: plain read loads in flight")
     ap.add_argument("--m", type=int, default=1, help="activation rows")
@@ -696,6 +742,9 @@ def main():
         return
     if args.workload == "decode_c5":
         decode_bench(args)
+        return
+    if args.workload == "issue_rates":
+        issue_rates(args)
         return
     if args.workload == "grid_table":
         grid_table(args)
