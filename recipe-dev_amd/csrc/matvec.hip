@@ -896,11 +896,12 @@ hipError_t launch_matvec_fused(int fmt, const MvParams& p, const LaunchShape& s,
     if (s.k2) {  // the two-waves-per-tile form (plan_fused)
         const size_t lds = matvec_lds_bytes(fmt, X_F32, 1, p.K);
         const bool nm = p.norm_w != nullptr;
+        auto go = [&](auto plain, auto norm) { return launch_kernel(nm ? norm : plain, p, s, lds, stream, nullptr, nullptr); };
         switch (fmt) {
-            case Q4_K: return launch_kernel(nm ? matvec_int_k2<Q4_K, 1, true, 1, true> : matvec_int_k2<Q4_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
-            case Q4_0: return launch_kernel(nm ? matvec_int_k2<Q4_0, 1, true, 1, true> : matvec_int_k2<Q4_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
-            case Q6_K: return launch_kernel(nm ? matvec_int_k2<Q6_K, 1, true, 1, true> : matvec_int_k2<Q6_K, 1, true>, p, s, lds, stream, nullptr, nullptr);
-            case Q8_0: return launch_kernel(nm ? matvec_int_k2<Q8_0, 1, true, 1, true> : matvec_int_k2<Q8_0, 1, true>, p, s, lds, stream, nullptr, nullptr);
+            case Q4_K: return go(matvec_int_k2<Q4_K, 1, true>, matvec_int_k2<Q4_K, 1, true, 1, true>);
+            case Q4_0: return go(matvec_int_k2<Q4_0, 1, true>, matvec_int_k2<Q4_0, 1, true, 1, true>);
+            case Q6_K: return go(matvec_int_k2<Q6_K, 1, true>, matvec_int_k2<Q6_K, 1, true, 1, true>);
+            case Q8_0: return go(matvec_int_k2<Q8_0, 1, true>, matvec_int_k2<Q8_0, 1, true, 1, true>);
             default: return hipErrorInvalidValue;
         }
     }
