@@ -608,14 +608,14 @@ static bool k2_shape(int fmt, int64_t rows, int64_t nch, int M, int xtype, int c
         s.grid = (int)((tiles + 7) / 8);
     } else if (fmt != F16 && nch >= 64 && nch <= (fmt == Q8_0 ? 192 : 128) && env_int("RQMV_K2_SHORT", 1)) {
         // two 512-thread workgroups per CU, or one of 1,024 threads where x
-        // needs more than four items per thread of 512, or where fp32
-        // activations leave one tile per wave pair (each CU then stages the
+        // needs more than four items per thread of 512, or where one row of
+        // fp32 activations leaves one tile per wave pair (each CU then stages the
         // heavier fp32 row once, not twice: Q8_0 4096x4096 6.16 -> 5.97 us,
         // the decode step, whose 4096x4096 output projection this is, 621.4
         // -> 625.8 tok/s; with fp16 x, or more tiles per pair, it measured
         // slower: Q4_K 4096->14336 8.36 -> 8.96 us median, Q8_0 5120x5120
         // 7.1 -> 7.8, the decode step with every fp32 product wide 614.0)
-        const bool fp32_one_tile = xtype == X_F32 && tiles <= (int64_t)2 * cus * 4;
+        const bool fp32_one_tile = xtype == X_F32 && M == 1 && tiles <= (int64_t)2 * cus * 4;
         s.block = (int64_t)stage_items_host(fmt, nch, M) > (int64_t)kStageNJ * 512 || fp32_one_tile ? 1024 : 512;
         s.grid = s.block == 1024 ? cus : 2 * cus;
         const int64_t stride = (int64_t)s.grid * (s.block / 128);
