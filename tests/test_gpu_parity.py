@@ -559,6 +559,28 @@ def test_long_row_form(gpu, fmt, xdt, rows, cols):
     assert err <= 2e-4, err
 
 
+@pytest.mark.parametrize("fmt,cols,ms", [("q6_k", 5120, (1, 2, 3)), ("q8_0", 4096, (1, 2, 3, 4)),
+                                         ("q4_k", 4096, (1, 2)), ("q4_0", 8192, (1, 2))])
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+@pytest.mark.parametrize("rows", [4095, 4096, 4097, 9001])
+def test_short_row_split_form(gpu, fmt, cols, ms, xdt, rows):
+    """Rows of 64-128 chunks (Q8_0: 64-192) around the two-waves-per-tile
+    form's thresholds: Q6_K on byte dots at one to three activation rows,
+    Q8_0 to four, one and two for the 4-bit formats; Q8_0 at 4,096 rows with
+    fp32 x takes one 1,024-thread workgroup per CU, 4,095 rows a partial last
+    tile, 4,097 and 9,001 tiles that do not divide over the wave pairs (the
+    other formats' products up to 20 MB at one or two rows take the burst
+    form). Parity with recipe's fp32 order."""
+    w = synth.weights(fmt, rows, cols, seed=rows + 7 * cols)
+    W = gpu.Weight(fmt, rows, cols, w)
+    for m in ms:
+        xh, dt, x32 = _x(m, cols, xdt, seed=cols + 31 * m)
+        y = _run_matvec(gpu, W, xh, dt, rows)
+        ref = oracle.matvec_recipe_f32(fmt, w, rows, cols, x32, threads=THREADS)
+        err = rel_l2(y, ref)
+        assert err <= 2e-4, (fmt, xdt, rows, m, err)
+
+
 # ------------------------------------------------- workload-size configs ----
 
 CONFIGS = [
