@@ -337,6 +337,31 @@ def test_fused_norm_and_glu(gpu, fmt, n, cols):
     assert np.array_equal(XO.download(np.float32), x + d)
 
 
+@pytest.mark.parametrize("epi", ["plain", "glu"])
+@pytest.mark.parametrize("fmt,n,cols", [("q4_k", 3072, 4096), ("q6_k", 2048, 5120), ("q4_k", 150, 4096)])
+@pytest.mark.parametrize("bad", [np.nan, np.inf])
+def test_fused_norm_non_finite(gpu, epi, fmt, n, cols, bad):
+    """A NaN or an infinity in x + delta makes the norm's sum of squares, so
+    every output of the product, non-finite (recipe's rmsnorm gives NaN there
+    too), in both forms of the fused kernel and with either epilogue; x_out
+    still receives x + delta as it is."""
+    g = synth.weights(fmt, n, cols, seed=8)
+    u = synth.weights(fmt, n, cols, seed=9)
+    W = gpu.glu_weight(fmt, n, cols, g, u) if epi == "glu" else gpu.Weight(fmt, 2 * n, cols,
+                                                                            np.concatenate([g, u]))
+    x = RNG.standard_normal(cols).astype(np.float32)
+    x[cols // 3] = bad
+    d = RNG.standard_normal(cols).astype(np.float32)
+    nw = np.ones(cols, np.float32)
+    rows_out = n if epi == "glu" else 2 * n
+    X, D, NW, Y = (gpu.DeviceBuffer.from_array(a) for a in (x, d, nw, np.zeros(rows_out, np.float32)))
+    XO = gpu.DeviceBuffer(4 * cols)
+    gpu.matvec_fused(W, X, Y, gpu.EPI_GLU if epi == "glu" else gpu.EPI_PLAIN, NW, 1e-5, D, XO)
+    gpu.synchronize()
+    assert not np.isfinite(Y.download(np.float32)).any()
+    np.testing.assert_array_equal(XO.download(np.float32), x + d)  # (NaN where x + d is NaN)
+
+
 @pytest.mark.parametrize("fmt,rows,cols", [("q8_0", 1001, 544), ("q8_0", 4096, 4096), ("q4_0", 77, 128),
                                            ("q4_k", 6143, 4096), ("q4_k", 4096, 14336), ("q4_0", 1001, 14336),
                                            ("q4_k", 4097, 8448)])
