@@ -155,6 +155,47 @@ def test_q6k_layout_decodes_each_code():
                 assert lo[e] + 16 * h == q_of(64 * c + e), (c, g, j)
 
 
+def test_q6k_byte_words_hold_each_code():
+    """The integer dot's byte words (chunk.h q6k_bytes, restated here on the
+    repacked words): for scale group g of a chunk, word 0 holds the codes of
+    the group's weights 0, 2, 4, 6, word 1 of 1, 3, 5, 7, word 2 of 8, 10, 12,
+    14 and word 3 of 9, 11, 13, 15, one 6-bit code q = l + 16 h per byte; the
+    activation staging writes its byte planes in the same order."""
+    rows, cols = 2, 512
+    w = synth.q6_k(rows, cols, seed=21)
+    code = rqmv.repack_host("q6_k", rows, cols, w)
+    row_bytes = rqmv.layout_bytes("q6_k", 1, cols)
+    nch = cols // 64
+    order = [[0, 2, 4, 6], [1, 3, 5, 7], [8, 10, 12, 14], [9, 11, 13, 15]]
+    for r in range(rows):
+        blk = w.reshape(rows, -1)[r]
+        rb = code[r * row_bytes:(r + 1) * row_bytes]
+
+        def q_of(i):  # recipe.rs:3743-3780 field positions
+            sb, k = divmod(i, 256)
+            ch, loc = divmod(k, 128)
+            g, j = divmod(loc, 32)
+            ql, qh = blk[sb * 210:sb * 210 + 128].astype(np.int64), blk[sb * 210 + 128:sb * 210 + 192].astype(np.int64)
+            lo = (ql[64 * ch + j + 32 * (g & 1)] >> (4 * (g // 2))) & 15
+            hi = (qh[32 * ch + j] >> (2 * g)) & 3
+            return int(lo | (hi << 4))
+
+        for c in range(nch):  # one group of nch chunks: part p of chunk c at (p * nch + c) * 16
+            part = [rb[(p * nch + c) * 16:(p * nch + c + 1) * 16].view(np.uint32).astype(np.uint64) for p in range(3)]
+            for g in range(4):
+                L0 = int(part[g >> 1][(g & 1) * 2]) ^ 0x88888888
+                L1 = int(part[g >> 1][(g & 1) * 2 + 1]) ^ 0x88888888
+                H = int(part[2][g])
+                W = [(L0 & 0x0F0F0F0F) | ((H << 4) & 0x30303030),
+                     ((L0 >> 4) & 0x0F0F0F0F) | (H & 0x30303030),
+                     (L1 & 0x0F0F0F0F) | ((H << 2) & 0x30303030),
+                     ((L1 >> 4) & 0x0F0F0F0F) | ((H >> 2) & 0x30303030)]
+                for t in range(4):
+                    got = [(W[t] >> (8 * k)) & 0xFF for k in range(4)]
+                    want = [q_of(64 * c + 16 * g + e) for e in order[t]]
+                    assert got == want, (r, c, g, t)
+
+
 @pytest.mark.parametrize("fmt,rows,cols", [("q4_k", 4, 100), ("q8_0", 2, 31), ("q6_k", 0, 256), (99, 2, 256)])
 def test_bad_shapes_are_rejected(fmt, rows, cols):
     with pytest.raises(rqmv.RqmvError):
