@@ -216,6 +216,9 @@ def moe_bench(args):
         stream.synchronize()
         distinct.append(int(np.count_nonzero(rb.download(np.float32).reshape(m, E).any(axis=0))))
     alg_bytes = E * d * 2 + d * 2 + expert_bytes * (float(np.mean(distinct)) + 1) + m * (d * 2 + d * 4)
+    # flops of a step: per position the router and the shared gate, and gate,
+    # up and down of the top-k routed experts and the shared one
+    flops = float(m) * (2 * E * d + 2 * d + (top + 1) * 6 * H * d)
 
     rel = None
     if not args.no_check:
@@ -261,6 +264,7 @@ def moe_bench(args):
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": "gguf_moe decode step: d_model 2048, 256 Q4_K experts of hidden 512, top-8 softmax "
                                "renormalised, fp16 router, sigmoid-gated shared expert", "bytes_per_step": alg_bytes,
+                   "flops_per_step": flops,
                    "positions": m, "distinct_experts_per_step": float(np.mean(distinct)),
                    "positions_per_s": round(m / ms_per_step * 1e3, 1),
                    "launches_per_step": 3, "weight_sets": 2, "tokens": 16, "parallelism": "single GPU"},
@@ -268,6 +272,7 @@ def moe_bench(args):
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles("moe_c4", m),
                      "note": "whole step (three launches) from the graph replay; traffic sums the three kernels"},
         "stream_copy": stream_copy(value),
+        "gflops": round(flops / (ms_per_step * 1e-3) / 1e9, 1),
         "parity_rel_l2": rel,
     }
     if not args.no_cpu:
@@ -412,6 +417,11 @@ def decode_bench(args):
     small = s.d * 4 + (2 * s.layers + 1) * s.d * 4
     bytes_per_token = model.weight_bytes() + kv_bytes + small
     achieved = bytes_per_token * tok_s / 1e9
+    # flops of a token: every projection and the head (2 per weight), and the
+    # attention's scores and weighted sum over the context
+    qkv_rows = (s.q_heads + 2 * s.kv_heads) * s.head_dim
+    per_layer = s.d * qkv_rows + s.q_heads * s.head_dim * s.d + 2 * s.ffn * s.d + s.d * s.ffn
+    flops_per_token = 2.0 * (s.layers * per_layer + s.vocab * s.d) + s.layers * 4.0 * s.q_heads * mean_len * s.head_dim
     log(f"bench: {args.steps} steps {total_ms:.2f} ms -> {ms_per_step * 1e3:.1f} us/token, {tok_s:.1f} tok/s, "
         f"{achieved:.0f} GB/s over {bytes_per_token / 1e9:.3f} GB/token")
     out = {
@@ -421,7 +431,8 @@ def decode_bench(args):
         "config": {"workload": "single-token decode, random-init 32-layer decoder: d 4096, 32/8 heads of 128, "
                                "NeoX rotary base 500000, SiLU-GLU 14336, RMSNorm 1e-5, Q4_K projections, "
                                "Q8_0 head 128256, fp16 KV cache prefilled to 4096",
-                   "bytes_per_token": int(bytes_per_token), "positions": [pos0, pos0 + args.steps - 1],
+                   "bytes_per_token": int(bytes_per_token), "flops_per_token": flops_per_token,
+                   "positions": [pos0, pos0 + args.steps - 1],
                    "launches_per_token": 1 + 6 * s.layers + 4, "activations": "f32", "kv_cache": "f16",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -429,6 +440,7 @@ def decode_bench(args):
                      "note": "whole token (every launch of the step) from graph replays; traffic sums every "
                              "kernel of one token"},
         "stream_copy": stream_copy(achieved),
+        "gflops": round(flops_per_token * tok_s / 1e9, 1),
     }
     if not args.no_cpu:
         import oracle
